@@ -1,0 +1,272 @@
+#!/usr/bin/env python3
+"""Attention-path benchmark on one MI355X: BASELINE config 4 (Llama-3.2-1B shape, 16 layers).
+
+Workload (inputs resident in HBM before any timed region; synthetic N(0,1) data generated on the device):
+  * prefill: 8192 tokens per layer - KV append with RoPE (Llama-3 frequency factors) into the layer's cache, then
+    causal GQA attention over the 8192 rows;
+  * decode: cache rows 8192..32767 seeded, then `--steps` single-token steps at positions 32768 + s, each through
+    all 16 layers (append with RoPE, then attention over 32769 + s rows). One "step" = one token through 16 layers.
+Printed: one JSON line. `value` = decode attention HBM GB/s (algorithmic bytes 8*KV*hd*L_ctx per layer-step over the
+timed wall time of the steps); `prefill` = prefill attention TFLOP/s (2*H*hd*n*(n+1) per layer). `roofline` is the
+decode kernel alone (algorithmic bytes per launch / its average event-timed duration), `prefill.roofline` the MFMA
+kernel alone. `cpu_baseline` is the reference's CpuBackend (compiled from its sources, oracle/_ref) on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import nibble_amd  # noqa: E402
+from nibble_amd import KernelTiming, configs  # noqa: E402
+
+METRIC = "decode attn HBM GB/s (%peak) @32k ctx; prefill attn TFLOP/s (%MFMA) @8k"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+FP32_PREFIX_ROWS = 256  # prefill rows below this position run on the fp32 kernel (hip_backend.cpp)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_bytes(kv, hd, ctx_len):
+    return 8 * kv * hd * ctx_len  # fp32 K and V rows read once
+
+
+def prefill_flops(h, hd, pos0, n):
+    # 4*H*hd per (query, visible key): QK^T and PV, causal-unmasked pairs only
+    t = np.arange(pos0, pos0 + n, dtype=np.float64)
+    return float(4.0 * h * hd * np.sum(t + 1))
+
+
+def cpu_baseline(be, shape, ck0, cv0, dq_dec, ctx, q_pre, budget_s):
+    """The reference's own CPU attention (ThreadPool + CpuBackend from oracle/_ref, AVX2 tier), timed on this host on
+    bounded samples of the same workload; falls back to our C restatement (kind "port") without oracle/_ref."""
+    import oracle
+
+    H, KV, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
+    threads = max(1, min(16, os.cpu_count() or 1))
+    L = ctx + 1
+    k = be.download(ck0, (L, KV, D))
+    v = be.download(cv0, (L, KV, D))
+    q = be.download(dq_dec, (1, H, D))
+    out = np.zeros((1, H, D), np.float32)
+    ref = oracle.have_ref()
+    if ref:
+        cb = oracle.RefCpuBackend(threads)
+        cb.reserve(L, H, 512, 8192)
+        run = lambda qq, kk, vv, oo, n, p0: cb.attention(qq, kk, vv, oo, n, p0, H, KV, D)  # noqa: E731
+        kind, tier = "reference", oracle.ref_kernel_set()
+    else:
+        def run(qq, kk, vv, oo, n, p0):
+            oo[...] = oracle.attention_parallel(qq, kk[:p0 + n], vv[:p0 + n], p0, KV, threads,
+                                                use_avx2=oracle.have_avx2())
+        kind, tier = "port", ("avx2" if oracle.have_avx2() else "scalar")
+
+    def timed(fn, min_reps, seconds):
+        fn()  # warm-up (cmd_bench.cpp:225-242: one untimed rep)
+        times = []
+        t_end = time.perf_counter() + seconds
+        while len(times) < min_reps or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 200:
+                break
+        return float(np.median(times)), len(times)
+
+    dec_s, dec_reps = timed(lambda: run(q, k, v, out, 1, ctx), 5, budget_s / 2)
+    dec_gbs = decode_bytes(KV, D, L) / dec_s / 1e9
+    # prefill sample: the last 256 query rows of the 8192-token prefill of layer 0 (pos0 = 7936)
+    n_s, pos0_s = 256, 8192 - 256
+    qs = np.ascontiguousarray(q_pre[pos0_s:8192])
+    outp = np.zeros_like(qs)
+    pre_s, pre_reps = timed(lambda: run(qs, k, v, outp, n_s, pos0_s), 3, budget_s / 2)
+    pre_tflops = prefill_flops(H, D, pos0_s, n_s) / pre_s / 1e12
+    try:
+        model = next((l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")), "?")
+    except OSError:
+        model = "?"
+    return {
+        "value": round(dec_gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+        "sample": f"layer-0 decode attention at {L} ctx (1 token, 32 heads), median of {dec_reps} reps; "
+                  f"reference CpuBackend::attention, tier {tier}, parallel_for over {H} heads",
+        "cpu_model": model,
+        "prefill": {"value": round(pre_tflops, 5), "unit": "TFLOP/s",
+                    "sample": f"layer-0 prefill rows {pos0_s}..8191 ({n_s} rows), median of {pre_reps} reps"},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64, help="timed decode steps (config 4 decodes 64 tokens)")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed decode steps before the timed ones")
+    ap.add_argument("--prefill-reps", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=16.0, help="budget of the CPU baseline samples")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "multi-GPU sharding is described in DESIGN.md, not run", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.steps > 64 or args.warmup < 0:
+        sys.exit("--steps must be in 1..64 (config 4 decodes 64 tokens), --warmup >= 0")
+
+    shape = configs.LLAMA32_1B
+    H, KV, D, NL = shape.n_heads, shape.n_kv_heads, shape.head_dim, shape.n_layers
+    base, neox, ff = shape.rope_base, shape.neox, shape.freq_factors()
+    n_pre, ctx, max_steps = 8192, 32768, 64
+    cap = ctx + max_steps
+    row = KV * D
+
+    be = nibble_amd.HipBackend(0)
+    be.reserve(cap, H, n_pre, 8192)
+    be.reserve_attention(KV, D)
+    be.reserve_rope(D, base, neox, ff)
+    log(f"device CUs: {be.cu_count()}; allocating caches for {NL} layers x {cap} rows")
+    ck = [be.alloc(cap * row) for _ in range(NL)]
+    cv = [be.alloc(cap * row) for _ in range(NL)]
+    for l in range(NL):  # seeded rows 8192..32767 (the prefill writes rows 0..8191)
+        be.fill_normal(ck[l].at(n_pre * row), (ctx - n_pre) * row, seed=(4 << 32) | (l << 8) | configs.T_KCACHE)
+        be.fill_normal(cv[l].at(n_pre * row), (ctx - n_pre) * row, seed=(4 << 32) | (l << 8) | configs.T_VCACHE)
+    q_pre = [be.alloc(n_pre * H * D) for _ in range(NL)]
+    k_pre = [be.alloc(n_pre * row) for _ in range(NL)]
+    v_pre = [be.alloc(n_pre * row) for _ in range(NL)]
+    for l in range(NL):
+        be.fill_normal(q_pre[l], n_pre * H * D, seed=(4 << 32) | (l << 8) | configs.T_Q)
+        be.fill_normal(k_pre[l], n_pre * row, seed=(4 << 32) | (l << 8) | configs.T_K)
+        be.fill_normal(v_pre[l], n_pre * row, seed=(4 << 32) | (l << 8) | configs.T_V)
+    out_pre = be.alloc(n_pre * H * D)
+    # decode inputs for every (step, layer)
+    qd = be.alloc(max_steps * NL * H * D)
+    kd = be.alloc(max_steps * NL * row)
+    vd = be.alloc(max_steps * NL * row)
+    be.fill_normal(qd, max_steps * NL * H * D, seed=(4 << 32) | (1 << 20) | configs.T_Q)
+    be.fill_normal(kd, max_steps * NL * row, seed=(4 << 32) | (1 << 20) | configs.T_K)
+    be.fill_normal(vd, max_steps * NL * row, seed=(4 << 32) | (1 << 20) | configs.T_V)
+    out_dec = be.alloc(H * D)
+    q_pre0_host = be.download(q_pre[0], (n_pre, H, D))  # layer-0 queries before any rotation (CPU baseline)
+    be.sync()
+
+    def prefill_pass():
+        for l in range(NL):
+            be.append_rope(q_pre[l], ck[l], cv[l], k_pre[l], v_pre[l], n_pre, 0, H, KV, D, base, neox, ff)
+            be.attention(q_pre[l], ck[l], cv[l], out_pre, n_pre, 0, H, KV, D)
+
+    def decode_step(s):
+        pos0 = ctx + s
+        for l in range(NL):
+            i = s * NL + l
+            be.append_rope(qd.at(i * H * D), ck[l], cv[l], kd.at(i * row), vd.at(i * row), 1, pos0, H, KV, D,
+                           base, neox, ff)
+            be.attention(qd.at(i * H * D), ck[l], cv[l], out_dec, 1, pos0, H, KV, D)
+
+    # ---------------- prefill (also fills cache rows 0..8191 of every layer)
+    prefill_pass()  # warm-up
+    be.sync()
+    e0, e1 = be.event(), be.event()
+    pre_ms = []
+    for _ in range(args.prefill_reps):
+        e0.record()
+        prefill_pass()
+        e1.record()
+        pre_ms.append(e0.elapsed_ms(e1))
+    pre_ms_med = float(np.median(pre_ms))
+    pre_flops = NL * prefill_flops(H, D, 0, n_pre)
+    pre_tflops = pre_flops / (pre_ms_med * 1e-3) / 1e12
+    log(f"prefill: {pre_ms_med:.3f} ms for {NL} layers -> {pre_tflops:.1f} TFLOP/s")
+
+    # ---------------- decode: warm-up steps, then exactly K timed steps (re-appending the same positions)
+    for s in range(args.warmup):
+        decode_step(s % max_steps)
+    be.sync()
+    e0.record()
+    for s in range(args.steps):
+        decode_step(s)
+    e1.record()
+    dec_ms = e0.elapsed_ms(e1)
+    be.sync()
+    dec_bytes = sum(NL * decode_bytes(KV, D, ctx + s + 1) for s in range(args.steps))
+    dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
+    log(f"decode: {dec_ms:.3f} ms for {args.steps} steps -> {dec_gbs:.1f} GB/s ({dec_gbs / HBM_PEAK_GBS:.1%})")
+
+    # ---------------- per-kernel durations (separate pass: event bracketing adds a little launch overhead)
+    KernelTiming.enable(True)
+    n_roof = min(8, args.steps)
+    for s in range(n_roof):
+        decode_step(s)
+    be.sync()
+    part_ms, part_n = KernelTiming.read(KernelTiming.DECODE_PARTIAL)
+    comb_ms, comb_n = KernelTiming.read(KernelTiming.DECODE_COMBINE)
+    app_ms, app_n = KernelTiming.read(KernelTiming.APPEND_ROPE)
+    roof_bytes = sum(NL * decode_bytes(KV, D, ctx + s + 1) for s in range(n_roof))
+    dec_kernel_gbs = roof_bytes / (part_ms * 1e-3) / 1e9
+    prefill_pass()
+    be.sync()
+    mfma_ms, mfma_n = KernelTiming.read(KernelTiming.PREFILL_MFMA)
+    stage_ms, stage_n = KernelTiming.read(KernelTiming.STAGE_KV)
+    pref32_ms, pref32_n = KernelTiming.read(KernelTiming.DECODE_PARTIAL)
+    app2_ms, app2_n = KernelTiming.read(KernelTiming.APPEND_ROPE)
+    KernelTiming.enable(False)
+    mfma_flops = prefill_flops(H, D, FP32_PREFIX_ROWS, n_pre - FP32_PREFIX_ROWS)  # rows the MFMA kernel computes
+    mfma_tflops = mfma_flops * mfma_n / (mfma_ms * 1e-3) / 1e12
+    log(f"kernels: decode partial avg {part_ms / part_n * 1e3:.2f} us ({dec_kernel_gbs:.0f} GB/s), combine avg "
+        f"{comb_ms / max(comb_n, 1) * 1e3:.2f} us, append+rope avg {app_ms / max(app_n, 1) * 1e3:.2f} us; "
+        f"prefill mfma avg {mfma_ms / mfma_n:.3f} ms ({mfma_tflops:.1f} TFLOP/s), stage avg "
+        f"{stage_ms / max(stage_n, 1) * 1e3:.1f} us, fp32 prefix avg {pref32_ms / max(pref32_n, 1) * 1e3:.1f} us")
+
+    result = {
+        "metric": METRIC,
+        "value": round(dec_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec_ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "BASELINE config 4: llama-3.2-1b shape (32 Q / 8 KV heads, hd 64, RoPE theta 5e5 with "
+                               "llama3 factors), 16 layers; decode 1 token/step at 32768+s ctx after an 8192-token "
+                               "prefill; value = decode", "layers": NL, "ctx": ctx, "prefill_tokens": n_pre,
+                   "global_batch": 1, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(dec_kernel_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dec_kernel_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "attn_decode_partial<64,4>",
+                     "avg_launch_us": round(part_ms / part_n * 1e3, 3), "launches": part_n,
+                     "algorithmic_bytes_per_launch": int(roof_bytes / part_n)},
+        "prefill": {"metric": "prefill attn TFLOP/s @8k", "value": round(pre_tflops, 2), "unit": "TFLOP/s",
+                    "ms_per_prefill_16_layers": round(pre_ms_med, 4), "reps": args.prefill_reps,
+                    "dtype": "f16 MFMA operands, f32 accumulate and softmax (rows < 256: f32)",
+                    "roofline": {"bound": "mfma", "achieved": round(mfma_tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                                 "unit": "TFLOP/s", "frac": round(mfma_tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                                 "traffic": None, "kernel": "attn_prefill_kernel<64>",
+                                 "avg_launch_us": round(mfma_ms / mfma_n * 1e3, 2), "launches": mfma_n,
+                                 "algorithmic_flops_per_launch": mfma_flops}},
+        "kernels_us": {"decode_combine": round(comb_ms / max(comb_n, 1) * 1e3, 3),
+                       "append_rope_decode": round(app_ms / max(app_n, 1) * 1e3, 3),
+                       "append_rope_prefill": round(app2_ms / max(app2_n, 1) * 1e3, 2),
+                       "stage_kv_f16": round(stage_ms / max(stage_n, 1) * 1e3, 2),
+                       "prefill_fp32_prefix": round(pref32_ms / max(pref32_n, 1) * 1e3, 2)},
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(be, shape, ck[0], cv[0], qd, ctx, q_pre0_host, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    be.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,114 @@
+/*
+ * nibble_hip.h - C ABI of the MI355X attention backend (libnibble_hip.so).
+ *
+ * This is the drop-in boundary for nibble's attention path. Each entry point wraps one member of
+ * nibble::hip::HipBackend, which implements the reference's nibble::Backend operator interface
+ * (src/backend/backend.h:36-71) on one gfx950 GPU; the citation on each declaration names the reference member it
+ * replaces. A C++ caller (nibble's Transformer) uses HipBackend directly; FFI callers (ctypes, tests, benchmarks)
+ * use these functions. Plain pointers and 64-bit sizes only.
+ *
+ * Buffers: nbh_backend_alloc() returns zeroed HBM. Every op that takes device pointers checks that each range it
+ * will touch lies inside one buffer from this backend and fails with NBH_E_INPUT otherwise, before launching work.
+ * Ops are asynchronous on the backend's HIP stream, in call order; read() and sync() wait for them.
+ *
+ * Errors: every function returns NBH_OK (0) or an NBH_E_* code; nbh_last_error() gives the message of the
+ * calling thread's last failure. The reference throws nibble::Error for the same conditions
+ * (include/nibble/error.h:11); HipBackend does too, and this layer converts it.
+ * Threading: one caller thread per backend (like CpuBackend; src/model/transformer.h:7).
+ */
+#ifndef NIBBLE_HIP_H
+#define NIBBLE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NBH_OK 0
+#define NBH_E_INPUT 1    /* nibble::Error: bad argument, range outside a buffer, allocation or device failure */
+#define NBH_E_INTERNAL 2 /* any other exception */
+
+typedef struct nbh_backend nbh_backend;
+typedef struct nbh_event nbh_event;
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* nbh_last_error(void);
+
+/* Creates a backend on HIP device `device` (must be gfx950). Replaces CpuBackend(ThreadPool&)
+ * (src/backend/cpu/cpu_backend.h:21, constructed at src/nibble.cpp:75-85). */
+int nbh_backend_create(int device, nbh_backend** out);
+
+/* Frees every buffer still allocated. Replaces CpuBackend::~CpuBackend (cpu_backend.cpp:70-72). */
+void nbh_backend_destroy(nbh_backend* be);
+
+/* Backend::supports (backend.h:41): whether weight type `dtype` (ggml id) can run matmul/embed. Always 0 for
+ * now: the HIP backend covers the attention path, not weight ops. */
+int nbh_backend_supports(const nbh_backend* be, uint32_t dtype, int* out);
+
+/* Backend::reserve (backend.h:45; ReserveParams backend.h:24-26). */
+int nbh_backend_reserve(nbh_backend* be, int64_t n_ctx, int64_t n_heads, int64_t max_rows, int64_t max_width);
+
+/* Backend::alloc (backend.h:47): zeroed HBM for n_floats floats. */
+int nbh_backend_alloc(nbh_backend* be, int64_t n_floats, float** out);
+
+/* Backend::free (backend.h:51): NULL is a no-op; pointers this backend did not allocate are ignored. */
+int nbh_backend_free(nbh_backend* be, float* p);
+
+/* Backend::read (backend.h:53): device -> host copy of n floats; waits for queued work. */
+int nbh_backend_read(nbh_backend* be, float* host_dst, const float* src, int64_t n);
+
+/* Host -> device copy of n floats. No reference counterpart: CpuBackend buffers are host memory, so its callers
+ * (e.g. tests/test_cpu_backend.cpp:69-74) write them directly. */
+int nbh_backend_write(nbh_backend* be, float* dst, const float* host_src, int64_t n);
+
+/* Backend::copy (backend.h:65; memmove semantics, cpu_backend.cpp:260-264). */
+int nbh_backend_copy(nbh_backend* be, float* dst, const float* src, int64_t count);
+
+/* Backend::rope (backend.h:64) with RopeParams (backend.h:16-20) passed field by field: freq_base, neox, and
+ * freq_factors (NULL or head_dim/2 HOST floats). Bit-exact with ref_ops.cpp:166-185. */
+int nbh_backend_rope(nbh_backend* be, float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0,
+                     float freq_base, int neox, const float* freq_factors);
+
+/* Backend::attention (backend.h:66-69): q,out [n, n_heads, head_dim]; k,v [>= pos0+n rows, n_kv_heads,
+ * head_dim] (layer cache bases); row t attends to cache rows 0..pos0+t. */
+int nbh_backend_attention(nbh_backend* be, const float* q, const float* k, const float* v, float* out, int64_t n,
+                          int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim);
+
+/* KV-cache append fused with RoPE: the per-layer sequence of src/model/transformer.cpp:171-198 (K/V rows written
+ * into cache rows pos0.., rope(q) and rope(k rows) in place) for K/V rows that arrive in their own buffers
+ * k_new/v_new [n, n_kv_heads, head_dim]. k_cache/v_cache are layer bases. Bit-identical to write + rope. */
+int nbh_backend_append_rope(nbh_backend* be, float* q, float* k_cache, float* v_cache, const float* k_new,
+                            const float* v_new, int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads,
+                            int64_t head_dim, float freq_base, int neox, const float* freq_factors);
+
+/* Extension of Backend::reserve for shapes ReserveParams does not carry: sizes the prefill operand staging
+ * (n_kv_heads x head_dim at the reserved n_ctx) so that the first prefill allocates nothing. */
+int nbh_backend_reserve_attention(nbh_backend* be, int64_t n_kv_heads, int64_t head_dim);
+
+/* Extension: builds the RoPE table for these parameters up to the reserved n_ctx ahead of the first rope(). */
+int nbh_backend_reserve_rope(nbh_backend* be, int64_t head_dim, float freq_base, int neox, const float* freq_factors);
+
+/* Waits for all queued work (no reference counterpart; CPU ops are synchronous). */
+int nbh_backend_sync(nbh_backend* be);
+
+/* Test hooks: buffers from alloc() still live (CpuBackend::live_allocations, cpu_backend.h:50); bytes of internal
+ * workspaces and tables (must not grow after reserve for in-range calls); the device's compute-unit count. */
+int nbh_backend_live_allocations(const nbh_backend* be, int64_t* out);
+int nbh_backend_internal_bytes(const nbh_backend* be, int64_t* out);
+int nbh_backend_cu_count(const nbh_backend* be, int* out);
+
+/* Synthetic N(0,1)*scale data generated on the device (benchmarks). No reference counterpart. */
+int nbh_backend_fill_normal(nbh_backend* be, float* dst, int64_t count, uint64_t seed, float scale);
+
+/* HIP events on the backend's stream, for timing a span of queued ops. No reference counterpart. */
+int nbh_event_create(nbh_backend* be, nbh_event** out);
+int nbh_event_record(nbh_backend* be, nbh_event* e);
+int nbh_event_elapsed_ms(nbh_event* start, nbh_event* end, float* ms); /* waits for `end` */
+void nbh_event_destroy(nbh_event* e);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,117 @@
+/*
+ * nibble_hip_shim.h - the thin extern "C" layer between the C++20 HipBackend and HIP.
+ *
+ * These are the only entry points that touch HIP: device/stream/memory management and one launcher per
+ * hand-written CDNA4 kernel. They take plain pointers and 64-bit sizes (byte offsets into a 131072-row,
+ * 16-layer fp32 cache exceed 2^31), return 0 or a hipError_t value (nbhs_error_string() names it), and never
+ * throw. Launchers only enqueue work on the given stream; they validate every size they are given before
+ * launching (a launch that does not fit the kernel's assumptions returns NBHS_EINVAL and enqueues nothing), but
+ * they cannot check that device pointers cover those sizes: HipBackend does that against its allocation table.
+ *
+ * The reference has no device code; each launcher names the reference operation it computes.
+ */
+#ifndef NIBBLE_HIP_SHIM_H
+#define NIBBLE_HIP_SHIM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NBHS_EINVAL 1 /* hipErrorInvalidValue: a size or shape the launcher does not accept */
+
+typedef struct nbhs_stream_* nbhs_stream; /* a hipStream_t */
+typedef struct nbhs_event_* nbhs_event;   /* a hipEvent_t */
+
+/* ---- device, streams, events, memory ---- */
+
+/* Makes `device` current on the calling thread; fails unless it is a gfx950 (MI355X) device. Reports its
+ * compute-unit count (for launch sizing). */
+int nbhs_device_init(int device, int* cu_count);
+const char* nbhs_error_string(int code);
+int nbhs_stream_create(nbhs_stream* out); /* default priority, non-blocking */
+int nbhs_stream_destroy(nbhs_stream s);
+int nbhs_stream_sync(nbhs_stream s);
+int nbhs_event_create(nbhs_event* out);
+int nbhs_event_destroy(nbhs_event e);
+int nbhs_event_record(nbhs_event e, nbhs_stream s);
+int nbhs_event_elapsed_ms(nbhs_event start, nbhs_event end, float* ms); /* waits for `end` */
+int nbhs_malloc(void** out, size_t bytes);
+int nbhs_free(void* p);
+/* Zero-fill with a kernel (never hipMemsetAsync, so the call is safe inside a captured graph). */
+int nbhs_zero(void* p, size_t bytes, nbhs_stream s);
+int nbhs_memcpy_h2d(void* dst, const void* host_src, size_t bytes, nbhs_stream s); /* returns when src is reusable */
+int nbhs_memcpy_d2h(void* host_dst, const void* src, size_t bytes, nbhs_stream s); /* returns when dst is filled */
+int nbhs_memcpy_d2d(void* dst, const void* src, size_t bytes, nbhs_stream s);      /* async; ranges must not overlap */
+
+/* ---- kernels ---- */
+
+/* RoPE in place (ref_ops.cpp:166-185 via Backend::rope, backend.h:64) on x[n, n_heads, head_dim] at positions
+ * pos0..pos0+n-1. cs_table holds (cos, sin) float pairs [table_rows, head_dim/2] built on the host exactly as the
+ * reference computes them; rows pos0..pos0+n-1 must exist (pos0 + n <= table_rows). The rotation is
+ * a*c - b*s, a*s + b*c with every product and sum rounded separately (no FMA), so results are bit-exact. */
+int nbhs_rope_f32(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0, const float* cs_table,
+                  int64_t table_rows, int neox, nbhs_stream s);
+
+/* KV-cache append fused with RoPE (transformer.cpp:171-198: K/V rows land in cache rows pos0.., then rope(q) and
+ * rope(k) in place): q[n, n_heads, head_dim] is rotated in place; cache_k rows pos0..pos0+n-1 receive
+ * rope(k_new) and cache_v rows receive v_new, for caches laid out [rows, n_kv_heads, head_dim]. Bit-identical to
+ * copying the rows and calling nbhs_rope_f32 on q and on the cache rows. */
+int nbhs_append_rope_f32(float* q, float* cache_k, float* cache_v, const float* k_new, const float* v_new, int64_t n,
+                         int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const float* cs_table,
+                         int64_t table_rows, int neox, nbhs_stream s);
+
+/* Causal GQA attention in fp32 (ref_ops.cpp:188-214 semantics via Backend::attention, backend.h:68-69) for n
+ * query rows at positions pos0..pos0+n-1 over caches k, v [>= pos0+n rows, n_kv_heads, head_dim]; out is
+ * [n, n_heads, head_dim]. Split-context ("flash-decoding"): each workgroup streams one chunk of one KV head for a
+ * group of query heads and writes an online-softmax partial (max, sum, weighted V) to `workspace`; a second kernel
+ * merges the partials with a log-sum-exp reduction. head_dim 64 or 128 take the tiled fast path, any other
+ * head_dim in [1, 256] a generic path. workspace_floats must be >= nbhs_attn_decode_workspace(...) for the same
+ * arguments, which returns the partial count the launcher will use. */
+int64_t nbhs_attn_decode_workspace(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                   int cu_count);
+int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                         int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float* workspace,
+                         int64_t workspace_floats, int cu_count, nbhs_stream s);
+
+/* Operand staging for the MFMA prefill: cache rows [0, rows) of k and v [rows, n_kv_heads, head_dim] fp32 are
+ * rounded to fp16 into k16 [n_kv_heads, rows_pad, head_dim] and vt16 [n_kv_heads, head_dim, rows_pad]
+ * (transposed), rows_pad = rows rounded up to 64, padding zero-filled. */
+int64_t nbhs_prefill_staging_halves(int64_t rows, int64_t n_kv_heads, int64_t head_dim); /* per tensor */
+int nbhs_stage_kv_f16(const float* k, const float* v, void* k16, void* vt16, int64_t rows, int64_t n_kv_heads,
+                      int64_t head_dim, nbhs_stream s);
+
+/* Causal GQA attention for n query rows at positions pos0.. on gfx950 MFMA (v_mfma_f32_32x32x16_f16): Q rounded
+ * to fp16 after scaling by log2(e)/sqrt(head_dim), K/V from the staged fp16 copies, softmax and accumulators in
+ * fp32. head_dim 64 or 128. The staged copies must cover rows [0, pos0+n). */
+int nbhs_attn_prefill_mfma(const float* q, const void* k16, const void* vt16, float* out, int64_t n, int64_t pos0,
+                           int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t staged_rows_pad,
+                           nbhs_stream s);
+
+/* Synthetic N(0,1)*scale data for benchmarks: counter-based (SplitMix64 of seed and index), Box-Muller in fp32. */
+int nbhs_fill_normal_f32(float* dst, int64_t count, uint64_t seed, float scale, nbhs_stream s);
+
+/* ---- per-kernel timing (measurement only) ----
+ * While enabled, every launcher records a HIP event pair on its own stream around each launch of its kernel, so
+ * the average device duration of one kernel can be read back live (bench.py's roofline figures). Off by default;
+ * enabling it adds two event records per launch. Not thread-safe. */
+enum nbhs_kernel_id {
+  NBHS_K_ROPE = 0,
+  NBHS_K_APPEND_ROPE = 1,
+  NBHS_K_DECODE_PARTIAL = 2,
+  NBHS_K_DECODE_COMBINE = 3,
+  NBHS_K_GENERIC = 4,
+  NBHS_K_STAGE_KV = 5,
+  NBHS_K_PREFILL_MFMA = 6,
+  NBHS_K_COUNT = 7
+};
+int nbhs_kernel_timing_enable(int on); /* on != 0: start recording (clears what was recorded) */
+/* Waits for the recorded launches of `kernel` and returns their summed duration and count, then clears them. */
+int nbhs_kernel_timing_read(int kernel, double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

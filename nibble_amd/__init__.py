@@ -1,0 +1,259 @@
+"""nibble_amd: nibble's attention path (RoPE, KV-cache append, causal GQA attention) on one MI355X.
+
+The product is libnibble_hip.so: hand-written HIP kernels for gfx950 behind a C++20 HipBackend that implements
+nibble's Backend operator interface (reference src/backend/backend.h:36-71), exported through the C ABI in
+include/nibble_hip.h. This module binds that ABI with ctypes for Python callers (tests, benchmarks). There is no
+fallback: if the library is missing or a call fails, it raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, byref, c_char_p, c_float, c_int, c_int64, c_uint32, c_uint64, c_void_p
+
+import numpy as np
+
+_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_DIR, "libnibble_hip.so")
+
+_F = POINTER(c_float)
+_I = c_int64
+
+# Every function the C ABI exports, with its ctypes signature (restype, argtypes).
+_SIGNATURES = {
+    "nbh_last_error": (c_char_p, []),
+    "nbh_backend_create": (c_int, [c_int, POINTER(c_void_p)]),
+    "nbh_backend_destroy": (None, [c_void_p]),
+    "nbh_backend_supports": (c_int, [c_void_p, c_uint32, POINTER(c_int)]),
+    "nbh_backend_reserve": (c_int, [c_void_p, _I, _I, _I, _I]),
+    "nbh_backend_alloc": (c_int, [c_void_p, _I, POINTER(c_void_p)]),
+    "nbh_backend_free": (c_int, [c_void_p, c_void_p]),
+    "nbh_backend_read": (c_int, [c_void_p, c_void_p, c_void_p, _I]),
+    "nbh_backend_write": (c_int, [c_void_p, c_void_p, c_void_p, _I]),
+    "nbh_backend_copy": (c_int, [c_void_p, c_void_p, c_void_p, _I]),
+    "nbh_backend_rope": (c_int, [c_void_p, c_void_p, _I, _I, _I, _I, c_float, c_int, c_void_p]),
+    "nbh_backend_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, _I, _I, _I, _I, _I]),
+    "nbh_backend_append_rope": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, _I, _I, _I, _I,
+                                        _I, c_float, c_int, c_void_p]),
+    "nbh_backend_reserve_attention": (c_int, [c_void_p, _I, _I]),
+    "nbh_backend_reserve_rope": (c_int, [c_void_p, _I, c_float, c_int, c_void_p]),
+    "nbh_backend_sync": (c_int, [c_void_p]),
+    "nbh_backend_live_allocations": (c_int, [c_void_p, POINTER(c_int64)]),
+    "nbh_backend_internal_bytes": (c_int, [c_void_p, POINTER(c_int64)]),
+    "nbh_backend_cu_count": (c_int, [c_void_p, POINTER(c_int)]),
+    "nbh_backend_fill_normal": (c_int, [c_void_p, c_void_p, _I, c_uint64, c_float]),
+    "nbh_event_create": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "nbh_event_record": (c_int, [c_void_p, c_void_p]),
+    "nbh_event_elapsed_ms": (c_int, [c_void_p, c_void_p, POINTER(c_float)]),
+    "nbh_event_destroy": (None, [c_void_p]),
+}
+
+_lib = None
+
+
+class BackendError(RuntimeError):
+    """A call into libnibble_hip.so failed (nibble::Error on the C++ side)."""
+
+
+def lib():
+    """The loaded libnibble_hip.so. Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                               "(there is no CPU fallback for the HIP backend)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc: int):
+    if rc != 0:
+        raise BackendError(lib().nbh_last_error().decode(errors="replace"))
+
+
+def _host_ptr(a: np.ndarray):
+    assert a.flags.c_contiguous
+    return a.ctypes.data_as(c_void_p)
+
+
+class DevicePtr(int):
+    """A device address handed out by HipBackend.alloc (float*); supports pointer arithmetic in floats via +."""
+
+    def at(self, floats: int) -> "DevicePtr":
+        return DevicePtr(int(self) + 4 * int(floats))
+
+
+class HipBackend:
+    """Python face of nibble::hip::HipBackend (the reference's Backend interface on one gfx950 GPU)."""
+
+    def __init__(self, device: int = 0):
+        h = c_void_p()
+        _check(lib().nbh_backend_create(device, byref(h)))
+        self._h = h
+
+    # -- Backend members (backend.h:36-71) --
+    def supports(self, dtype: int) -> bool:
+        out = c_int()
+        _check(lib().nbh_backend_supports(self._h, dtype, byref(out)))
+        return bool(out.value)
+
+    def reserve(self, n_ctx: int, n_heads: int, max_rows: int, max_width: int):
+        _check(lib().nbh_backend_reserve(self._h, n_ctx, n_heads, max_rows, max_width))
+
+    def alloc(self, n_floats: int) -> DevicePtr:
+        p = c_void_p()
+        _check(lib().nbh_backend_alloc(self._h, n_floats, byref(p)))
+        return DevicePtr(p.value)
+
+    def free(self, p):
+        _check(lib().nbh_backend_free(self._h, c_void_p(int(p)) if p else None))
+
+    def read(self, src, n: int, out: np.ndarray | None = None) -> np.ndarray:
+        if out is None:
+            out = np.empty(n, np.float32)
+        assert out.dtype == np.float32 and out.size >= n
+        _check(lib().nbh_backend_read(self._h, _host_ptr(out), c_void_p(int(src)), n))
+        return out
+
+    def write(self, dst, host: np.ndarray):
+        host = np.ascontiguousarray(host, dtype=np.float32)
+        _check(lib().nbh_backend_write(self._h, c_void_p(int(dst)), _host_ptr(host), host.size))
+
+    def copy(self, dst, src, count: int):
+        _check(lib().nbh_backend_copy(self._h, c_void_p(int(dst)), c_void_p(int(src)), count))
+
+    def rope(self, x, n, n_heads, head_dim, pos0, freq_base, neox, freq_factors=None):
+        ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
+        _check(lib().nbh_backend_rope(self._h, c_void_p(int(x)), n, n_heads, head_dim, pos0, freq_base, int(bool(neox)),
+                                      None if ff is None else _host_ptr(ff)))
+
+    def attention(self, q, k, v, out, n, pos0, n_heads, n_kv_heads, head_dim):
+        _check(lib().nbh_backend_attention(self._h, c_void_p(int(q)), c_void_p(int(k)), c_void_p(int(v)),
+                                           c_void_p(int(out)), n, pos0, n_heads, n_kv_heads, head_dim))
+
+    # -- HIP-only extensions --
+    def append_rope(self, q, k_cache, v_cache, k_new, v_new, n, pos0, n_heads, n_kv_heads, head_dim, freq_base,
+                    neox, freq_factors=None):
+        ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
+        _check(lib().nbh_backend_append_rope(self._h, c_void_p(int(q)), c_void_p(int(k_cache)),
+                                             c_void_p(int(v_cache)), c_void_p(int(k_new)), c_void_p(int(v_new)), n,
+                                             pos0, n_heads, n_kv_heads, head_dim, freq_base, int(bool(neox)),
+                                             None if ff is None else _host_ptr(ff)))
+
+    def reserve_attention(self, n_kv_heads: int, head_dim: int):
+        _check(lib().nbh_backend_reserve_attention(self._h, n_kv_heads, head_dim))
+
+    def reserve_rope(self, head_dim, freq_base, neox, freq_factors=None):
+        ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
+        _check(lib().nbh_backend_reserve_rope(self._h, head_dim, freq_base, int(bool(neox)),
+                                              None if ff is None else _host_ptr(ff)))
+
+    def sync(self):
+        _check(lib().nbh_backend_sync(self._h))
+
+    def live_allocations(self) -> int:
+        out = c_int64()
+        _check(lib().nbh_backend_live_allocations(self._h, byref(out)))
+        return out.value
+
+    def internal_bytes(self) -> int:
+        out = c_int64()
+        _check(lib().nbh_backend_internal_bytes(self._h, byref(out)))
+        return out.value
+
+    def cu_count(self) -> int:
+        out = c_int()
+        _check(lib().nbh_backend_cu_count(self._h, byref(out)))
+        return out.value
+
+    def fill_normal(self, dst, count: int, seed: int, scale: float = 1.0):
+        _check(lib().nbh_backend_fill_normal(self._h, c_void_p(int(dst)), count, seed & (2**64 - 1), scale))
+
+    # -- convenience --
+    def upload(self, host: np.ndarray) -> DevicePtr:
+        host = np.ascontiguousarray(host, dtype=np.float32)
+        p = self.alloc(host.size)
+        self.write(p, host)
+        return p
+
+    def download(self, src, shape) -> np.ndarray:
+        n = int(np.prod(shape))
+        return self.read(src, n).reshape(shape)
+
+    def event(self) -> "Event":
+        return Event(self)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().nbh_backend_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class KernelTiming:
+    """Live per-kernel device durations from the shim's launch bracketing (nbhs_kernel_timing_*,
+    include/nibble_hip_shim.h). Used by the benchmark for roofline figures."""
+
+    ROPE, APPEND_ROPE, DECODE_PARTIAL, DECODE_COMBINE, GENERIC, STAGE_KV, PREFILL_MFMA = range(7)
+
+    @staticmethod
+    def enable(on: bool = True):
+        L = lib()
+        L.nbhs_kernel_timing_enable.argtypes = [c_int]
+        L.nbhs_kernel_timing_enable.restype = c_int
+        if L.nbhs_kernel_timing_enable(int(on)) != 0:
+            raise BackendError("nbhs_kernel_timing_enable failed")
+
+    @staticmethod
+    def read(kernel: int) -> tuple[float, int]:
+        """(total milliseconds, launches) recorded for `kernel` since the last read; clears them."""
+        L = lib()
+        L.nbhs_kernel_timing_read.argtypes = [c_int, POINTER(ctypes.c_double), POINTER(c_int64)]
+        L.nbhs_kernel_timing_read.restype = c_int
+        total, count = ctypes.c_double(), c_int64()
+        rc = L.nbhs_kernel_timing_read(kernel, byref(total), byref(count))
+        if rc != 0:
+            raise BackendError(f"nbhs_kernel_timing_read failed ({rc})")
+        return total.value, count.value
+
+
+class Event:
+    """A HIP event on the backend's stream."""
+
+    def __init__(self, be: HipBackend):
+        h = c_void_p()
+        _check(lib().nbh_event_create(be._h, byref(h)))
+        self._be = be
+        self._h = h
+
+    def record(self):
+        _check(lib().nbh_event_record(self._be._h, self._h))
+        return self
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = c_float()
+        _check(lib().nbh_event_elapsed_ms(self._h, end._h, byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib().nbh_event_destroy(self._h)
+        except Exception:
+            pass

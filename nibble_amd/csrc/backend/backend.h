@@ -1,0 +1,54 @@
+#pragma once
+// The compute-backend operator interface that nibble's transformer forward is written against
+// (src/backend/backend.h:16-71 in the reference). The declarations keep the reference's names, argument order
+// and meaning exactly, so a Backend implemented here drops in where nibble constructs its CpuBackend.
+//
+// Activation pointers are opaque to the caller: for the HIP backend they are device addresses, and only the
+// backend dereferences them. RopeParams::freq_factors is host memory.
+#include <cstdint>
+#include <span>
+
+#include "backend/tensor.h"
+
+namespace nibble {
+
+struct RopeParams {
+  float freq_base;            // theta (1e4, 5e5, 1e6, ...)
+  bool neox;                  // rotate (i, i + head_dim/2) if true, else (2i, 2i + 1)
+  const float* freq_factors;  // nullptr or head_dim/2 host floats; the angle is divided by factor i
+};
+
+struct ReserveParams {
+  int64_t n_ctx, n_heads, max_rows, max_width;
+};
+
+class Backend {
+ public:
+  virtual ~Backend() = default;
+  virtual bool supports(DType weight_type) const = 0;
+  // After reserve(), ops with pos0 + n <= n_ctx, n_heads <= the reserved count and n <= max_rows allocate nothing.
+  virtual void reserve(const ReserveParams&) = 0;
+  // Zeroed memory for n_floats floats; throws Error if n_floats < 0 or allocation fails.
+  virtual float* alloc(int64_t n_floats) = 0;
+  // free(nullptr) is a no-op; pointers this backend did not hand out are ignored.
+  virtual void free(float* p) = 0;
+  virtual void read(float* host_dst, const float* src, int64_t n) = 0;
+  virtual void embed(const Tensor& table, std::span<const int32_t> ids, float* out) = 0;
+  virtual void matmul(const Tensor& w, const float* x, float* y, int64_t n) = 0;
+  virtual void matmul_multi(std::span<const Tensor* const> ws, const float* x, std::span<float* const> ys, int64_t n) {
+    for (size_t i = 0; i < ws.size(); ++i) matmul(*ws[i], x, ys[i], n);
+  }
+  virtual void rmsnorm(const float* x, const Tensor& weight, float* y, int64_t n, float eps) = 0;
+  virtual void add(float* x, const float* y, int64_t count) = 0;
+  virtual void add_bias(float* x, const Tensor& bias, int64_t n) = 0;
+  // x[n, n_heads, head_dim] in place at positions pos0..pos0+n-1.
+  virtual void rope(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0, const RopeParams&) = 0;
+  virtual void copy(float* dst, const float* src, int64_t count) = 0;
+  // q,out: [n, n_heads, head_dim]; k,v: [n_ctx, n_kv_heads, head_dim]; row t has position pos0+t and attends to
+  // cache rows 0..pos0+t.
+  virtual void attention(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                         int64_t n_heads, int64_t n_kv_heads, int64_t head_dim) = 0;
+  virtual void silu_mul(float* gate, const float* up, int64_t count) = 0;
+};
+
+}  // namespace nibble

@@ -1,0 +1,11 @@
+#pragma once
+// Run-time errors caused by input (bad sizes, ranges outside a backend buffer, allocation or device failure) are
+// thrown as nibble::Error, the reference's single exception type (include/nibble/error.h:11).
+#include <stdexcept>
+
+namespace nibble {
+class Error : public std::runtime_error {
+ public:
+  using std::runtime_error::runtime_error;
+};
+}  // namespace nibble

@@ -1,0 +1,317 @@
+// HipBackend implementation: argument validation against the allocation table, the RoPE (cos, sin) tables, and
+// the routing of attention calls to the decode (fp32, split-context) and prefill (fp16 MFMA) kernels.
+// Host-side C++20 only; every device action goes through nibble_hip_shim.h.
+#include "backend/hip/hip_backend.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <thread>
+
+namespace nibble::hip {
+namespace {
+
+// Calls with at most this many query rows take the fp32 split-context kernel (decode, short appends).
+constexpr int64_t kDecodeMaxRows = 16;
+// Prefill rows at positions below this see fewer keys than it takes for fp16 rounding of single V rows to
+// average out; they take the fp32 kernel (a few hundred rows, negligible work next to the MFMA pass).
+constexpr int64_t kFp32PrefixRows = 256;
+
+std::string str(int64_t v) { return std::to_string(v); }
+
+bool overflow_mul(int64_t a, int64_t b, int64_t* out) { return __builtin_mul_overflow(a, b, out); }
+
+}  // namespace
+
+HipBackend::HipBackend(int device) : device_(device) {
+  check(nbhs_device_init(device, &cu_count_), "device init");
+  check(nbhs_stream_create(&stream_), "stream create");
+}
+
+HipBackend::~HipBackend() {
+  if (stream_) nbhs_stream_sync(stream_);
+  for (auto& [p, bytes] : allocs_) nbhs_free(reinterpret_cast<void*>(p));
+  for (auto& t : rope_tables_) nbhs_free(t.dev);
+  nbhs_free(decode_ws_);
+  nbhs_free(k16_);
+  nbhs_free(vt16_);
+  nbhs_free(copy_tmp_);
+  if (stream_) nbhs_stream_destroy(stream_);
+}
+
+void HipBackend::not_on_gpu(const char* op) {
+  throw Error(std::string("HipBackend: ") + op + " is not implemented on the GPU backend (attention path only)");
+}
+
+void HipBackend::check(int code, const char* what) const {
+  if (code != 0) throw Error(std::string("HipBackend: ") + what + " failed: " + nbhs_error_string(code));
+}
+
+void HipBackend::check_range(const void* p, int64_t n_floats, const char* op, const char* arg) const {
+  if (!p) throw Error(std::string(op) + ": " + arg + " is null");
+  int64_t bytes;
+  if (n_floats < 0 || overflow_mul(n_floats, int64_t(sizeof(float)), &bytes))
+    throw Error(std::string(op) + ": " + arg + " size " + str(n_floats) + " floats is invalid");
+  const auto a = reinterpret_cast<uintptr_t>(p);
+  auto it = allocs_.upper_bound(a);
+  if (it != allocs_.begin()) {
+    --it;
+    if (a >= it->first && a - it->first + uint64_t(bytes) <= it->second) return;
+  }
+  throw Error(std::string(op) + ": " + arg + " range of " + str(n_floats) +
+              " floats is not inside one buffer allocated by this backend");
+}
+
+void HipBackend::ensure(float*& buf, size_t& cap_bytes, size_t need_bytes) {
+  if (need_bytes <= cap_bytes) return;
+  check(nbhs_stream_sync(stream_), "sync before workspace growth");
+  check(nbhs_free(buf), "free workspace");
+  buf = nullptr;
+  cap_bytes = 0;
+  void* p = nullptr;
+  check(nbhs_malloc(&p, need_bytes), "workspace allocation");
+  buf = static_cast<float*>(p);
+  cap_bytes = need_bytes;
+}
+
+size_t HipBackend::internal_bytes() const {
+  size_t s = decode_ws_bytes_ + k16_bytes_ + vt16_bytes_ + copy_tmp_bytes_;
+  for (auto& t : rope_tables_) s += size_t(t.rows) * size_t(t.head_dim) * sizeof(float);
+  return s;
+}
+
+void HipBackend::reserve(const ReserveParams& rp) {
+  if (rp.n_ctx < 0 || rp.n_heads < 0 || rp.max_rows < 0 || rp.max_width < 0)
+    throw Error("reserve: negative size (n_ctx=" + str(rp.n_ctx) + " n_heads=" + str(rp.n_heads) + ")");
+  reserved_ = rp;
+  // Decode partials: the split plan never exceeds ~4 workgroups per CU in total, each holding up to
+  // (head_dim + 2) floats per query head (head_dim <= 128 on the tiled path); multi-row calls split fewer ways.
+  const int64_t chunks = std::max<int64_t>(1, std::min<int64_t>((rp.n_ctx + 63) / 64, int64_t(cu_count_) * 4 + 16));
+  int64_t floats;
+  if (overflow_mul(rp.n_heads, chunks * 130, &floats)) throw Error("reserve: decode workspace size overflows");
+  ensure(decode_ws_, decode_ws_bytes_, size_t(floats) * sizeof(float));
+}
+
+void HipBackend::reserve_attention(int64_t n_kv_heads, int64_t head_dim) {
+  if (head_dim != 64 && head_dim != 128) return;  // no staging on the generic path
+  const int64_t halves = nbhs_prefill_staging_halves(std::max<int64_t>(reserved_.n_ctx, 1), n_kv_heads, head_dim);
+  if (halves < 0) throw Error("reserve_attention: invalid n_kv_heads " + str(n_kv_heads));
+  ensure(k16_, k16_bytes_, size_t(halves) * 2);
+  ensure(vt16_, vt16_bytes_, size_t(halves) * 2);
+}
+
+void HipBackend::reserve_rope(int64_t head_dim, const RopeParams& p) {
+  if (head_dim <= 0 || head_dim % 2 != 0) throw Error("reserve_rope: head_dim must be positive and even");
+  int64_t rows;
+  rope_table(head_dim, std::max<int64_t>(reserved_.n_ctx, 1), p, &rows);
+}
+
+float* HipBackend::alloc(int64_t n_floats) {
+  if (n_floats < 0) throw Error("alloc: negative size " + str(n_floats) + " floats");
+  int64_t bytes;
+  if (overflow_mul(n_floats, int64_t(sizeof(float)), &bytes) || bytes > INT64_MAX - 63)
+    throw Error("alloc: size of " + str(n_floats) + " floats overflows");
+  bytes = std::max<int64_t>(64, (bytes + 63) & ~int64_t(63));
+  void* p = nullptr;
+  if (nbhs_malloc(&p, size_t(bytes)) != 0 || !p) throw Error("alloc: cannot allocate " + str(bytes) + " bytes of HBM");
+  const int zr = nbhs_zero(p, size_t(bytes), stream_);
+  if (zr != 0) {
+    nbhs_free(p);
+    check(zr, "alloc zero-fill");
+  }
+  allocs_.emplace(reinterpret_cast<uintptr_t>(p), size_t(bytes));
+  return static_cast<float*>(p);
+}
+
+void HipBackend::free(float* p) {
+  if (!p) return;
+  auto it = allocs_.find(reinterpret_cast<uintptr_t>(p));
+  if (it == allocs_.end()) return;  // not ours: ignore rather than risk a double free
+  nbhs_stream_sync(stream_);        // queued work may still use it
+  nbhs_free(p);
+  allocs_.erase(it);
+}
+
+void HipBackend::read(float* host_dst, const float* src, int64_t n) {
+  if (n < 0 || (n > 0 && !host_dst)) throw Error("read: invalid destination or size " + str(n));
+  if (n == 0) return;
+  check_range(src, n, "read", "src");
+  check(nbhs_memcpy_d2h(host_dst, src, size_t(n) * sizeof(float), stream_), "read");
+}
+
+void HipBackend::write(float* dst, const float* host_src, int64_t n) {
+  if (n < 0 || (n > 0 && !host_src)) throw Error("write: invalid source or size " + str(n));
+  if (n == 0) return;
+  check_range(dst, n, "write", "dst");
+  check(nbhs_memcpy_h2d(dst, host_src, size_t(n) * sizeof(float), stream_), "write");
+}
+
+void HipBackend::copy(float* dst, const float* src, int64_t count) {
+  if (count < 0) throw Error("copy: negative count " + str(count));
+  if (count == 0 || dst == src) return;
+  check_range(dst, count, "copy", "dst");
+  check_range(src, count, "copy", "src");
+  const size_t bytes = size_t(count) * sizeof(float);
+  const auto d = reinterpret_cast<uintptr_t>(dst), s = reinterpret_cast<uintptr_t>(src);
+  if (d < s + bytes && s < d + bytes) {  // overlapping: bounce through a scratch buffer (memmove semantics)
+    ensure(copy_tmp_, copy_tmp_bytes_, bytes);
+    check(nbhs_memcpy_d2d(copy_tmp_, src, bytes, stream_), "copy");
+    check(nbhs_memcpy_d2d(dst, copy_tmp_, bytes, stream_), "copy");
+    return;
+  }
+  check(nbhs_memcpy_d2d(dst, src, bytes, stream_), "copy");
+}
+
+void HipBackend::sync() { check(nbhs_stream_sync(stream_), "sync"); }
+
+void HipBackend::fill_normal(float* dst, int64_t count, uint64_t seed, float scale) {
+  if (count == 0) return;
+  check_range(dst, count, "fill_normal", "dst");
+  check(nbhs_fill_normal_f32(dst, count, seed, scale, stream_), "fill_normal");
+}
+
+// The table holds, for every position `pos` and pair i, float(cos(theta)) and float(sin(theta)) with
+// theta = double(pos) * pow(double(base), -2i/head_dim) [/ double(freq_factors[i])] - the reference's angle
+// (ref_ops.cpp:169-176) computed by the same libm calls on the same doubles, so the device rotation that reads it is
+// bit-exact. pow depends only on i, so it is evaluated once per pair; the product is the reference's own.
+const float* HipBackend::rope_table(int64_t head_dim, int64_t rows_needed, const RopeParams& p, int64_t* rows_out) {
+  const int64_t half = head_dim / 2;
+  auto same = [&](const RopeTable& t) {
+    if (std::memcmp(&t.base, &p.freq_base, sizeof(float)) != 0 || t.head_dim != head_dim) return false;
+    if (!p.freq_factors) return t.factors.empty();
+    return !t.factors.empty() && std::memcmp(t.factors.data(), p.freq_factors, size_t(half) * sizeof(float)) == 0;
+  };
+  auto it = std::find_if(rope_tables_.begin(), rope_tables_.end(), same);
+  if (it != rope_tables_.end() && it->rows >= rows_needed) {
+    *rows_out = it->rows;
+    return it->dev;
+  }
+  const int64_t rows = std::max(rows_needed, reserved_.n_ctx);
+  int64_t entries;
+  if (overflow_mul(rows, head_dim, &entries)) throw Error("rope: table size overflows");
+  std::vector<float> host(static_cast<size_t>(entries));
+  std::vector<double> inv(static_cast<size_t>(half));
+  for (int64_t i = 0; i < half; ++i)
+    inv[size_t(i)] = std::pow(static_cast<double>(p.freq_base), -2.0 * static_cast<double>(i) / static_cast<double>(head_dim));
+  const float* ff = p.freq_factors;
+  auto fill = [&](int64_t r0, int64_t r1) {
+    for (int64_t pos = r0; pos < r1; ++pos) {
+      const double dpos = static_cast<double>(pos);
+      float* row = host.data() + pos * head_dim;
+      for (int64_t i = 0; i < half; ++i) {
+        double theta = dpos * inv[size_t(i)];
+        if (ff) theta /= ff[i];
+        row[2 * i] = static_cast<float>(std::cos(theta));
+        row[2 * i + 1] = static_cast<float>(std::sin(theta));
+      }
+    }
+  };
+  const unsigned hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  const int64_t nt = entries > (int64_t(1) << 16) ? int64_t(hw) : 1;
+  if (nt == 1) {
+    fill(0, rows);
+  } else {
+    std::vector<std::thread> th;
+    const int64_t step = (rows + nt - 1) / nt;
+    for (int64_t r = 0; r < rows; r += step) th.emplace_back(fill, r, std::min(rows, r + step));
+    for (auto& x : th) x.join();
+  }
+  if (it == rope_tables_.end()) {
+    rope_tables_.push_back(RopeTable{});
+    it = rope_tables_.end() - 1;
+    it->base = p.freq_base;
+    it->head_dim = head_dim;
+    if (ff) it->factors.assign(ff, ff + half);
+  } else {
+    check(nbhs_stream_sync(stream_), "sync before rope table growth");
+    check(nbhs_free(it->dev), "free rope table");
+    it->dev = nullptr;
+    it->rows = 0;
+  }
+  void* d = nullptr;
+  check(nbhs_malloc(&d, size_t(entries) * sizeof(float)), "rope table allocation");
+  it->dev = static_cast<float*>(d);
+  it->rows = rows;
+  check(nbhs_memcpy_h2d(d, host.data(), size_t(entries) * sizeof(float), stream_), "rope table upload");
+  *rows_out = rows;
+  return it->dev;
+}
+
+void HipBackend::rope(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0, const RopeParams& p) {
+  if (n <= 0 || n_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || pos0 < 0)
+    throw Error("rope: invalid shape n=" + str(n) + " n_heads=" + str(n_heads) + " head_dim=" + str(head_dim) +
+                " (must be even) pos0=" + str(pos0));
+  int64_t count;
+  if (overflow_mul(n, n_heads, &count) || overflow_mul(count, head_dim, &count)) throw Error("rope: size overflows");
+  check_range(x, count, "rope", "x");
+  int64_t rows;
+  const float* table = rope_table(head_dim, pos0 + n, p, &rows);
+  check(nbhs_rope_f32(x, n, n_heads, head_dim, pos0, table, rows, p.neox ? 1 : 0, stream_), "rope");
+}
+
+void HipBackend::append_rope(float* q, float* k_cache, float* v_cache, const float* k_new, const float* v_new,
+                             int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                             const RopeParams& p) {
+  if (n <= 0 || n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || pos0 < 0)
+    throw Error("append_rope: invalid shape n=" + str(n) + " n_heads=" + str(n_heads) + " n_kv_heads=" +
+                str(n_kv_heads) + " head_dim=" + str(head_dim) + " pos0=" + str(pos0));
+  int64_t qf, kvf, cachef;
+  if (overflow_mul(n * n_heads, head_dim, &qf) || overflow_mul(n * n_kv_heads, head_dim, &kvf) ||
+      overflow_mul((pos0 + n) * n_kv_heads, head_dim, &cachef))
+    throw Error("append_rope: size overflows");
+  check_range(q, qf, "append_rope", "q");
+  check_range(k_new, kvf, "append_rope", "k_new");
+  check_range(v_new, kvf, "append_rope", "v_new");
+  check_range(k_cache, cachef, "append_rope", "k_cache");
+  check_range(v_cache, cachef, "append_rope", "v_cache");
+  int64_t rows;
+  const float* table = rope_table(head_dim, pos0 + n, p, &rows);
+  check(nbhs_append_rope_f32(q, k_cache, v_cache, k_new, v_new, n, pos0, n_heads, n_kv_heads, head_dim, table, rows,
+                             p.neox ? 1 : 0, stream_),
+        "append_rope");
+}
+
+void HipBackend::attention(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                           int64_t n_heads, int64_t n_kv_heads, int64_t head_dim) {
+  if (n <= 0 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || head_dim <= 0 ||
+      head_dim > 256)
+    throw Error("attention: invalid shape n=" + str(n) + " pos0=" + str(pos0) + " n_heads=" + str(n_heads) +
+                " n_kv_heads=" + str(n_kv_heads) + " head_dim=" + str(head_dim) +
+                " (n_heads must be a multiple of n_kv_heads, head_dim at most 256)");
+  int64_t qf, cachef;
+  if (overflow_mul(n * n_heads, head_dim, &qf) || overflow_mul((pos0 + n) * n_kv_heads, head_dim, &cachef))
+    throw Error("attention: size overflows");
+  check_range(q, qf, "attention", "q");
+  check_range(out, qf, "attention", "out");
+  check_range(k, cachef, "attention", "k");
+  check_range(v, cachef, "attention", "v");
+
+  auto decode_rows = [&](const float* qq, float* oo, int64_t rows, int64_t p0) {
+    const int64_t ws = nbhs_attn_decode_workspace(rows, p0, n_heads, n_kv_heads, head_dim, cu_count_);
+    if (ws < 0) throw Error("attention: invalid decode shape");
+    ensure(decode_ws_, decode_ws_bytes_, size_t(ws) * sizeof(float));
+    check(nbhs_attn_decode_f32(qq, k, v, oo, rows, p0, n_heads, n_kv_heads, head_dim, decode_ws_,
+                               int64_t(decode_ws_bytes_ / sizeof(float)), cu_count_, stream_),
+          "attention (decode kernel)");
+  };
+
+  const bool mfma_shape = head_dim == 64 || head_dim == 128;
+  if (!mfma_shape || n <= kDecodeMaxRows) {
+    decode_rows(q, out, n, pos0);
+    return;
+  }
+  const int64_t split = std::clamp<int64_t>(kFp32PrefixRows - pos0, 0, n);
+  if (split > 0) decode_rows(q, out, split, pos0);
+  if (split == n) return;
+  const int64_t rows = pos0 + n;
+  const int64_t halves = nbhs_prefill_staging_halves(rows, n_kv_heads, head_dim);
+  ensure(k16_, k16_bytes_, size_t(halves) * 2);
+  ensure(vt16_, vt16_bytes_, size_t(halves) * 2);
+  check(nbhs_stage_kv_f16(k, v, k16_, vt16_, rows, n_kv_heads, head_dim, stream_), "attention (staging)");
+  const int64_t rows_pad = halves / (n_kv_heads * head_dim);
+  check(nbhs_attn_prefill_mfma(q + split * n_heads * head_dim, k16_, vt16_, out + split * n_heads * head_dim,
+                               n - split, pos0 + split, n_heads, n_kv_heads, head_dim, rows_pad, stream_),
+        "attention (prefill kernel)");
+}
+
+}  // namespace nibble::hip

@@ -1,0 +1,100 @@
+#pragma once
+// HipBackend: nibble's Backend (backend.h) on one MI355X (gfx950), the attention path in hand-written HIP.
+// It replaces CpuBackend (reference src/backend/cpu/cpu_backend.h:18-91) for the ops the attention path uses:
+// reserve/alloc/free/read/copy, rope and attention, plus HIP-only extensions (host upload, the fused KV append
+// with RoPE, synthetic fill, events). The weight ops (embed, matmul, rmsnorm, add, add_bias, silu_mul) are not on
+// the GPU yet and throw nibble::Error; supports() is false for every weight type, so a model load fails early.
+//
+// Memory: every buffer handed out is HBM, zeroed, tracked; every op checks that the device ranges it is given lie
+// inside one tracked buffer before it launches anything, and throws Error otherwise (a bad range never reaches a
+// kernel). Ops run asynchronously on the backend's own HIP stream in call order; read() and sync() wait.
+// Not thread-safe (one caller thread, as for CpuBackend).
+#include <cstdint>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "backend/backend.h"
+#include "backend/error.h"
+#include "nibble_hip_shim.h"
+
+namespace nibble::hip {
+
+class HipBackend final : public Backend {
+ public:
+  // Selects `device` (must be gfx950) and creates the backend's stream. Throws Error on failure.
+  explicit HipBackend(int device = 0);
+  ~HipBackend() override;
+  HipBackend(const HipBackend&) = delete;
+  HipBackend& operator=(const HipBackend&) = delete;
+
+  bool supports(DType) const override { return false; }
+  // Sizes the decode workspace for n_heads query heads at up to n_ctx positions. Shapes it cannot know from
+  // ReserveParams (KV heads, head_dim) are sized by reserve_attention() or on first use.
+  void reserve(const ReserveParams&) override;
+  float* alloc(int64_t n_floats) override;  // HBM, 64-byte granular, zeroed
+  void free(float* p) override;
+  void read(float* host_dst, const float* src, int64_t n) override;  // waits for queued work
+  void embed(const Tensor&, std::span<const int32_t>, float*) override { not_on_gpu("embed"); }
+  void matmul(const Tensor&, const float*, float*, int64_t) override { not_on_gpu("matmul"); }
+  void rmsnorm(const float*, const Tensor&, float*, int64_t, float) override { not_on_gpu("rmsnorm"); }
+  void add(float*, const float*, int64_t) override { not_on_gpu("add"); }
+  void add_bias(float*, const Tensor&, int64_t) override { not_on_gpu("add_bias"); }
+  void rope(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0, const RopeParams& p) override;
+  void copy(float* dst, const float* src, int64_t count) override;  // memmove semantics
+  void attention(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                 int64_t n_heads, int64_t n_kv_heads, int64_t head_dim) override;
+  void silu_mul(float*, const float*, int64_t) override { not_on_gpu("silu_mul"); }
+
+  // ---- HIP-only extensions ----
+  // Host -> device upload of n floats (the reference needs none: its buffers are host memory).
+  void write(float* dst, const float* host_src, int64_t n);
+  // Pre-sizes the prefill operand staging for caches of n_kv_heads x head_dim at up to the reserved n_ctx rows,
+  // so the first prefill allocates nothing.
+  void reserve_attention(int64_t n_kv_heads, int64_t head_dim);
+  // Prebuilds the RoPE (cos, sin) table for these parameters up to the reserved n_ctx positions.
+  void reserve_rope(int64_t head_dim, const RopeParams& p);
+  // KV-cache append fused with RoPE: the sequence matmul-into-cache, rope(q), rope(k rows) of
+  // transformer.cpp:171-198 for K/V rows arriving in a separate buffer. k_cache/v_cache are layer bases.
+  void append_rope(float* q, float* k_cache, float* v_cache, const float* k_new, const float* v_new, int64_t n,
+                   int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const RopeParams& p);
+  void fill_normal(float* dst, int64_t count, uint64_t seed, float scale);
+  void sync();
+  nbhs_stream stream() const { return stream_; }
+  int cu_count() const { return cu_count_; }
+  size_t live_allocations() const { return allocs_.size(); }  // test hook (cpu_backend.h:50)
+  // Internal device memory held for workspaces and tables, in bytes (test hook: must not grow after reserve).
+  size_t internal_bytes() const;
+
+ private:
+  struct RopeTable {
+    float base = 0;
+    int64_t head_dim = 0;
+    std::vector<float> factors;  // empty when no freq_factors
+    int64_t rows = 0;
+    float* dev = nullptr;  // [rows, head_dim/2] (cos, sin) float pairs
+  };
+
+  [[noreturn]] static void not_on_gpu(const char* op);
+  void check(int code, const char* what) const;
+  // Throws unless [p, p + n_floats) lies inside one buffer from alloc().
+  void check_range(const void* p, int64_t n_floats, const char* op, const char* arg) const;
+  const float* rope_table(int64_t head_dim, int64_t rows_needed, const RopeParams& p, int64_t* rows_out);
+  void ensure(float*& buf, size_t& cap_bytes, size_t need_bytes);
+
+  int device_ = 0;
+  int cu_count_ = 0;
+  nbhs_stream stream_ = nullptr;
+  std::map<uintptr_t, size_t> allocs_;  // user buffers: start -> bytes
+  ReserveParams reserved_{0, 0, 0, 0};
+  std::vector<RopeTable> rope_tables_;
+  float* decode_ws_ = nullptr;  // split-context partials
+  size_t decode_ws_bytes_ = 0;
+  float* k16_ = nullptr;  // prefill staging: fp16 K and transposed V
+  float* vt16_ = nullptr;
+  size_t k16_bytes_ = 0, vt16_bytes_ = 0;
+  float* copy_tmp_ = nullptr;  // bounce buffer for overlapping copies
+  size_t copy_tmp_bytes_ = 0;
+};
+
+}  // namespace nibble::hip

@@ -1,0 +1,296 @@
+// The thin extern "C" shim over HIP: device selection, streams, events, memory, and the small element-wise
+// kernels of the attention path (RoPE, the fused KV append, zero-fill, synthetic data). The attention kernels
+// live in kernels/attn_decode.hip and kernels/attn_prefill.hip. This is one of the few translation units that
+// include HIP; HipBackend (hip_backend.cpp) sees only nibble_hip_shim.h.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <vector>
+
+#include "backend/hip/kernel_timing.h"
+#include "nibble_hip_shim.h"
+
+namespace nbhs_timing {
+namespace {
+struct Record {
+  int kernel;
+  hipEvent_t start, end;
+};
+bool g_enabled = false;
+std::vector<Record> g_records;
+hipEvent_t g_pending[NBHS_K_COUNT] = {};  // start event of the launch being bracketed, per kernel id
+
+void drop_all() {
+  for (auto& r : g_records) {
+    (void)hipEventDestroy(r.start);
+    (void)hipEventDestroy(r.end);
+  }
+  g_records.clear();
+}
+}  // namespace
+
+bool enabled() { return g_enabled; }
+
+void record_begin(int kernel, hipStream_t s) {
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return;
+  (void)hipEventRecord(e, s);
+  g_pending[kernel] = e;
+}
+
+void record_end(int kernel, hipStream_t s) {
+  hipEvent_t start = g_pending[kernel];
+  g_pending[kernel] = nullptr;
+  if (!start) return;
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) {
+    (void)hipEventDestroy(start);
+    return;
+  }
+  (void)hipEventRecord(e, s);
+  g_records.push_back({kernel, start, e});
+}
+
+}  // namespace nbhs_timing
+
+// RoPE must round every product and sum separately, as the reference does (it is compiled with
+// -ffp-contract=off, CMakeLists.txt:72-73); this file is also built with -ffp-contract=off.
+#pragma clang fp contract(off)
+
+namespace {
+
+inline hipStream_t S(nbhs_stream s) { return reinterpret_cast<hipStream_t>(s); }
+inline hipEvent_t E(nbhs_event e) { return reinterpret_cast<hipEvent_t>(e); }
+
+constexpr int kThreads = 256;
+
+// Grid size for a grid-stride loop over `items` work items: enough blocks to fill the chip several times over,
+// never more than the items need.
+inline unsigned grid_for(int64_t items) {
+  const int64_t blocks = (items + kThreads - 1) / kThreads;
+  return static_cast<unsigned>(blocks < 1 ? 1 : (blocks > 65536 ? 65536 : blocks));
+}
+
+// One (a, b) pair rotated by the tabulated angle: a*c - b*s, a*s + b*c, each op rounded on its own.
+__device__ __forceinline__ void rotate(float& a, float& b, float c, float s) {
+  const float a0 = a, b0 = b;
+  a = __fsub_rn(__fmul_rn(a0, c), __fmul_rn(b0, s));
+  b = __fadd_rn(__fmul_rn(a0, s), __fmul_rn(b0, c));
+}
+
+// x[n, heads, hd] in place, one thread per (row, head, pair). Pair i of a row is (i, i + hd/2) for NeoX, else
+// (2i, 2i + 1) (ref_ops.cpp:177-178).
+__global__ void rope_kernel(float* __restrict__ x, int64_t n, int64_t heads, int64_t hd, int64_t pos0,
+                            const float2* __restrict__ cs, int neox) {
+  const int64_t half = hd / 2, total = n * heads * half;
+  for (int64_t idx = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; idx < total;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t i = idx % half, rest = idx / half, t = rest / heads;
+    float* row = x + rest * hd;
+    const float2 c = cs[(pos0 + t) * half + i];
+    const int64_t ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
+    float a = row[ia], b = row[ib];
+    rotate(a, b, c.x, c.y);
+    row[ia] = a;
+    row[ib] = b;
+  }
+}
+
+// Fused append: per row t, slots [0, H) rotate q heads in place, [H, H+KV) rotate k_new heads into the cache,
+// [H+KV, H+2KV) copy v_new heads into the cache; one thread per (row, slot, pair).
+__global__ void append_rope_kernel(float* __restrict__ q, float* __restrict__ ck, float* __restrict__ cv,
+                                   const float* __restrict__ kn, const float* __restrict__ vn, int64_t n, int64_t pos0,
+                                   int64_t H, int64_t KV, int64_t hd, const float2* __restrict__ cs, int neox) {
+  const int64_t half = hd / 2, slots = H + 2 * KV, total = n * slots * half;
+  for (int64_t idx = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; idx < total;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t i = idx % half, rest = idx / half, slot = rest % slots, t = rest / slots;
+    const int64_t ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
+    if (slot < H) {
+      float* row = q + (t * H + slot) * hd;
+      const float2 c = cs[(pos0 + t) * half + i];
+      float a = row[ia], b = row[ib];
+      rotate(a, b, c.x, c.y);
+      row[ia] = a;
+      row[ib] = b;
+    } else if (slot < H + KV) {
+      const int64_t g = slot - H;
+      const float* src = kn + (t * KV + g) * hd;
+      float* dst = ck + ((pos0 + t) * KV + g) * hd;
+      const float2 c = cs[(pos0 + t) * half + i];
+      float a = src[ia], b = src[ib];
+      rotate(a, b, c.x, c.y);
+      dst[ia] = a;
+      dst[ib] = b;
+    } else {
+      const int64_t g = slot - H - KV;
+      const float* src = vn + (t * KV + g) * hd;
+      float* dst = cv + ((pos0 + t) * KV + g) * hd;
+      dst[ia] = src[ia];
+      dst[ib] = src[ib];
+    }
+  }
+}
+
+__global__ void zero_kernel(uint8_t* __restrict__ p, int64_t bytes) {
+  const int64_t vecs = bytes / 16;
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < vecs; i += stride)
+    reinterpret_cast<uint4*>(p)[i] = make_uint4(0, 0, 0, 0);
+  for (int64_t i = vecs * 16 + blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < bytes; i += stride) p[i] = 0;
+}
+
+// SplitMix64 finaliser.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// Element 2p and 2p+1 come from one Box-Muller pair of the two uniforms hashed from (seed, p).
+__global__ void fill_normal_kernel(float* __restrict__ dst, int64_t count, uint64_t seed, float scale) {
+  const int64_t pairs = (count + 1) / 2;
+  for (int64_t p = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; p < pairs; p += int64_t(gridDim.x) * blockDim.x) {
+    const uint64_t h1 = mix64(seed + (2 * uint64_t(p) + 1) * 0x9E3779B97F4A7C15ull);
+    const uint64_t h2 = mix64(seed + (2 * uint64_t(p) + 2) * 0x9E3779B97F4A7C15ull);
+    const float u1 = (float((h1 >> 40) + 1)) * 0x1p-24f;  // (0, 1]
+    const float u2 = float(h2 >> 40) * 0x1p-24f;          // [0, 1)
+    const float r = sqrtf(-2.0f * logf(u1));
+    float sn, cs;
+    sincosf(6.283185307179586f * u2, &sn, &cs);
+    dst[2 * p] = r * cs * scale;
+    if (2 * p + 1 < count) dst[2 * p + 1] = r * sn * scale;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int nbhs_device_init(int device, int* cu_count) {
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) return e;
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return e;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return hipErrorInvalidDevice;
+  if (cu_count) *cu_count = prop.multiProcessorCount;
+  return hipSuccess;
+}
+
+const char* nbhs_error_string(int code) { return hipGetErrorString(static_cast<hipError_t>(code)); }
+
+int nbhs_stream_create(nbhs_stream* out) {
+  hipStream_t s = nullptr;
+  const hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  *out = reinterpret_cast<nbhs_stream>(s);
+  return e;
+}
+int nbhs_stream_destroy(nbhs_stream s) { return hipStreamDestroy(S(s)); }
+int nbhs_stream_sync(nbhs_stream s) { return hipStreamSynchronize(S(s)); }
+
+int nbhs_event_create(nbhs_event* out) {
+  hipEvent_t e = nullptr;
+  const hipError_t r = hipEventCreate(&e);
+  *out = reinterpret_cast<nbhs_event>(e);
+  return r;
+}
+int nbhs_event_destroy(nbhs_event e) { return hipEventDestroy(E(e)); }
+int nbhs_event_record(nbhs_event e, nbhs_stream s) { return hipEventRecord(E(e), S(s)); }
+int nbhs_event_elapsed_ms(nbhs_event start, nbhs_event end, float* ms) {
+  const hipError_t e = hipEventSynchronize(E(end));
+  if (e != hipSuccess) return e;
+  return hipEventElapsedTime(ms, E(start), E(end));
+}
+
+int nbhs_malloc(void** out, size_t bytes) { return hipMalloc(out, bytes == 0 ? 1 : bytes); }
+int nbhs_free(void* p) { return hipFree(p); }
+
+int nbhs_zero(void* p, size_t bytes, nbhs_stream s) {
+  if (bytes == 0) return hipSuccess;
+  if (!p) return NBHS_EINVAL;
+  zero_kernel<<<grid_for(int64_t(bytes / 16 + 1)), kThreads, 0, S(s)>>>(static_cast<uint8_t*>(p), int64_t(bytes));
+  return hipGetLastError();
+}
+
+int nbhs_memcpy_h2d(void* dst, const void* src, size_t bytes, nbhs_stream s) {
+  if (bytes == 0) return hipSuccess;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, S(s));
+  if (e != hipSuccess) return e;
+  return hipStreamSynchronize(S(s));
+}
+int nbhs_memcpy_d2h(void* dst, const void* src, size_t bytes, nbhs_stream s) {
+  if (bytes == 0) return hipSuccess;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, S(s));
+  if (e != hipSuccess) return e;
+  return hipStreamSynchronize(S(s));
+}
+int nbhs_memcpy_d2d(void* dst, const void* src, size_t bytes, nbhs_stream s) {
+  if (bytes == 0) return hipSuccess;
+  return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, S(s));
+}
+
+int nbhs_rope_f32(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0, const float* cs_table,
+                  int64_t table_rows, int neox, nbhs_stream s) {
+  if (!x || !cs_table || n <= 0 || n_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || pos0 < 0 ||
+      pos0 + n > table_rows)
+    return NBHS_EINVAL;
+  nbhs_timing::KernelTimer timer(NBHS_K_ROPE, S(s));
+  rope_kernel<<<grid_for(n * n_heads * (head_dim / 2)), kThreads, 0, S(s)>>>(
+      x, n, n_heads, head_dim, pos0, reinterpret_cast<const float2*>(cs_table), neox);
+  return hipGetLastError();
+}
+
+int nbhs_append_rope_f32(float* q, float* cache_k, float* cache_v, const float* k_new, const float* v_new, int64_t n,
+                         int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const float* cs_table,
+                         int64_t table_rows, int neox, nbhs_stream s) {
+  if (!q || !cache_k || !cache_v || !k_new || !v_new || !cs_table || n <= 0 || n_heads <= 0 || n_kv_heads <= 0 ||
+      head_dim <= 0 || head_dim % 2 != 0 || pos0 < 0 || pos0 + n > table_rows)
+    return NBHS_EINVAL;
+  nbhs_timing::KernelTimer timer(NBHS_K_APPEND_ROPE, S(s));
+  append_rope_kernel<<<grid_for(n * (n_heads + 2 * n_kv_heads) * (head_dim / 2)), kThreads, 0, S(s)>>>(
+      q, cache_k, cache_v, k_new, v_new, n, pos0, n_heads, n_kv_heads, head_dim,
+      reinterpret_cast<const float2*>(cs_table), neox);
+  return hipGetLastError();
+}
+
+int nbhs_fill_normal_f32(float* dst, int64_t count, uint64_t seed, float scale, nbhs_stream s) {
+  if (count < 0 || (count > 0 && !dst)) return NBHS_EINVAL;
+  if (count == 0) return hipSuccess;
+  fill_normal_kernel<<<grid_for((count + 1) / 2), kThreads, 0, S(s)>>>(dst, count, seed, scale);
+  return hipGetLastError();
+}
+
+int nbhs_kernel_timing_enable(int on) {
+  nbhs_timing::drop_all();
+  nbhs_timing::g_enabled = on != 0;
+  return hipSuccess;
+}
+
+int nbhs_kernel_timing_read(int kernel, double* total_ms, int64_t* launches) {
+  if (kernel < 0 || kernel >= NBHS_K_COUNT || !total_ms || !launches) return NBHS_EINVAL;
+  double total = 0;
+  int64_t count = 0;
+  hipError_t first_error = hipSuccess;
+  std::vector<nbhs_timing::Record> keep;
+  for (auto& r : nbhs_timing::g_records) {
+    if (r.kernel != kernel) {
+      keep.push_back(r);
+      continue;
+    }
+    float ms = 0;
+    hipError_t e = hipEventSynchronize(r.end);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.start, r.end);
+    (void)hipEventDestroy(r.start);
+    (void)hipEventDestroy(r.end);
+    if (e != hipSuccess && first_error == hipSuccess) first_error = e;
+    total += ms;
+    ++count;
+  }
+  nbhs_timing::g_records.swap(keep);
+  *total_ms = total;
+  *launches = count;
+  return first_error;
+}
+
+}  // extern "C"

@@ -1,0 +1,186 @@
+// The C ABI of include/nibble_hip.h over nibble::hip::HipBackend: exceptions become NBH_E_* codes plus a
+// thread-local message.
+#include <exception>
+#include <new>
+#include <string>
+
+#include "backend/hip/hip_backend.h"
+#include "nibble_hip.h"
+
+using nibble::RopeParams;
+using nibble::hip::HipBackend;
+
+struct nbh_backend {
+  HipBackend impl;
+  explicit nbh_backend(int device) : impl(device) {}
+};
+
+struct nbh_event {
+  nbhs_event ev = nullptr;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <class F>
+int guarded(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return NBH_OK;
+  } catch (const nibble::Error& e) {
+    g_last_error = e.what();
+    return NBH_E_INPUT;
+  } catch (const std::bad_alloc&) {
+    g_last_error = "out of host memory";
+    return NBH_E_INPUT;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return NBH_E_INTERNAL;
+  } catch (...) {
+    g_last_error = "unknown exception";
+    return NBH_E_INTERNAL;
+  }
+}
+
+HipBackend& B(nbh_backend* be) {
+  if (!be) throw nibble::Error("null backend handle");
+  return be->impl;
+}
+const HipBackend& B(const nbh_backend* be) {
+  if (!be) throw nibble::Error("null backend handle");
+  return be->impl;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* nbh_last_error(void) { return g_last_error.c_str(); }
+
+int nbh_backend_create(int device, nbh_backend** out) {
+  return guarded([&] {
+    if (!out) throw nibble::Error("null output handle");
+    *out = nullptr;
+    *out = new nbh_backend(device);
+  });
+}
+
+void nbh_backend_destroy(nbh_backend* be) { delete be; }
+
+int nbh_backend_supports(const nbh_backend* be, uint32_t dtype, int* out) {
+  return guarded([&] { *out = B(be).supports(static_cast<nibble::DType>(dtype)) ? 1 : 0; });
+}
+
+int nbh_backend_reserve(nbh_backend* be, int64_t n_ctx, int64_t n_heads, int64_t max_rows, int64_t max_width) {
+  return guarded([&] { B(be).reserve({n_ctx, n_heads, max_rows, max_width}); });
+}
+
+int nbh_backend_alloc(nbh_backend* be, int64_t n_floats, float** out) {
+  return guarded([&] {
+    if (!out) throw nibble::Error("alloc: null output pointer");
+    *out = B(be).alloc(n_floats);
+  });
+}
+
+int nbh_backend_free(nbh_backend* be, float* p) {
+  return guarded([&] { B(be).free(p); });
+}
+
+int nbh_backend_read(nbh_backend* be, float* host_dst, const float* src, int64_t n) {
+  return guarded([&] { B(be).read(host_dst, src, n); });
+}
+
+int nbh_backend_write(nbh_backend* be, float* dst, const float* host_src, int64_t n) {
+  return guarded([&] { B(be).write(dst, host_src, n); });
+}
+
+int nbh_backend_copy(nbh_backend* be, float* dst, const float* src, int64_t count) {
+  return guarded([&] { B(be).copy(dst, src, count); });
+}
+
+int nbh_backend_rope(nbh_backend* be, float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0,
+                     float freq_base, int neox, const float* freq_factors) {
+  return guarded([&] { B(be).rope(x, n, n_heads, head_dim, pos0, RopeParams{freq_base, neox != 0, freq_factors}); });
+}
+
+int nbh_backend_attention(nbh_backend* be, const float* q, const float* k, const float* v, float* out, int64_t n,
+                          int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim) {
+  return guarded([&] { B(be).attention(q, k, v, out, n, pos0, n_heads, n_kv_heads, head_dim); });
+}
+
+int nbh_backend_append_rope(nbh_backend* be, float* q, float* k_cache, float* v_cache, const float* k_new,
+                            const float* v_new, int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads,
+                            int64_t head_dim, float freq_base, int neox, const float* freq_factors) {
+  return guarded([&] {
+    B(be).append_rope(q, k_cache, v_cache, k_new, v_new, n, pos0, n_heads, n_kv_heads, head_dim,
+                      RopeParams{freq_base, neox != 0, freq_factors});
+  });
+}
+
+int nbh_backend_reserve_attention(nbh_backend* be, int64_t n_kv_heads, int64_t head_dim) {
+  return guarded([&] { B(be).reserve_attention(n_kv_heads, head_dim); });
+}
+
+int nbh_backend_reserve_rope(nbh_backend* be, int64_t head_dim, float freq_base, int neox, const float* freq_factors) {
+  return guarded([&] { B(be).reserve_rope(head_dim, RopeParams{freq_base, neox != 0, freq_factors}); });
+}
+
+int nbh_backend_sync(nbh_backend* be) {
+  return guarded([&] { B(be).sync(); });
+}
+
+int nbh_backend_live_allocations(const nbh_backend* be, int64_t* out) {
+  return guarded([&] { *out = int64_t(B(be).live_allocations()); });
+}
+
+int nbh_backend_internal_bytes(const nbh_backend* be, int64_t* out) {
+  return guarded([&] { *out = int64_t(B(be).internal_bytes()); });
+}
+
+int nbh_backend_cu_count(const nbh_backend* be, int* out) {
+  return guarded([&] { *out = B(be).cu_count(); });
+}
+
+int nbh_backend_fill_normal(nbh_backend* be, float* dst, int64_t count, uint64_t seed, float scale) {
+  return guarded([&] { B(be).fill_normal(dst, count, seed, scale); });
+}
+
+int nbh_event_create(nbh_backend* be, nbh_event** out) {
+  return guarded([&] {
+    if (!out) throw nibble::Error("null output handle");
+    B(be);
+    auto* e = new nbh_event;
+    const int rc = nbhs_event_create(&e->ev);
+    if (rc != 0) {
+      delete e;
+      throw nibble::Error(std::string("event create failed: ") + nbhs_error_string(rc));
+    }
+    *out = e;
+  });
+}
+
+int nbh_event_record(nbh_backend* be, nbh_event* e) {
+  return guarded([&] {
+    if (!e) throw nibble::Error("null event");
+    const int rc = nbhs_event_record(e->ev, B(be).stream());
+    if (rc != 0) throw nibble::Error(std::string("event record failed: ") + nbhs_error_string(rc));
+  });
+}
+
+int nbh_event_elapsed_ms(nbh_event* start, nbh_event* end, float* ms) {
+  return guarded([&] {
+    if (!start || !end || !ms) throw nibble::Error("null event or output");
+    const int rc = nbhs_event_elapsed_ms(start->ev, end->ev, ms);
+    if (rc != 0) throw nibble::Error(std::string("event elapsed failed: ") + nbhs_error_string(rc));
+  });
+}
+
+void nbh_event_destroy(nbh_event* e) {
+  if (!e) return;
+  nbhs_event_destroy(e->ev);
+  delete e;
+}
+
+}  // extern "C"

@@ -1,0 +1,246 @@
+"""ctypes bindings for the CPU oracle. TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and only as the
+checker or the reported CPU baseline. The product path (nibble_amd/) never imports it.
+
+Two libraries:
+  liboracle.so            our C restatement of nibble's attention path (oracle.c, oracle_avx2.c)
+  _ref/libnibble_ref.so   the reference's own CPU backend compiled from its sources (absent when the reference
+                          tree was not available at build time; `have_ref()` says which)
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int64, c_void_p
+
+import numpy as np
+
+_DIR = os.path.dirname(os.path.abspath(__file__))
+_F = POINTER(c_float)
+_D = POINTER(c_double)
+_I = c_int64
+
+_lib = None
+_ref = None
+_ref_tried = False
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        path = os.path.join(_DIR, "liboracle.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"oracle library missing: {path} (run __graft_entry__.build())")
+        lib = ctypes.CDLL(path)
+        lib.orc_rope.argtypes = [_F, _I, _I, _I, _I, c_float, c_int, _F]
+        lib.orc_rope.restype = None
+        lib.orc_softmax_inplace.argtypes = [_F, _I]
+        lib.orc_softmax_inplace.restype = None
+        attn = [_F, _F, _F, _F, _I, _I, _I, _I, _I, _I, _I, _F]
+        lib.orc_attention_scalar.argtypes = attn
+        lib.orc_attention_scalar.restype = None
+        lib.orc_attention_avx2.argtypes = attn
+        lib.orc_attention_avx2.restype = c_int
+        lib.orc_exp_ps.argtypes = [_F, _F, _I]
+        lib.orc_exp_ps.restype = c_int
+        lib.orc_have_avx2.argtypes = []
+        lib.orc_have_avx2.restype = c_int
+        lib.orc_attention_heads_parallel.argtypes = [_F, _F, _F, _F, _I, _I, _I, _I, _I, c_int, c_int, _F]
+        lib.orc_attention_heads_parallel.restype = c_int
+        lib.orc_attention_f64.argtypes = [_F, _F, _F, _D, _I, _I, _I, _I, _I]
+        lib.orc_attention_f64.restype = None
+        lib.orc_llama3_freq_factors.argtypes = [_F, _I, c_double, c_double, c_double, c_double, c_double]
+        lib.orc_llama3_freq_factors.restype = None
+        _lib = lib
+    return _lib
+
+
+def _load_ref():
+    global _ref, _ref_tried
+    if not _ref_tried:
+        _ref_tried = True
+        path = os.path.join(_DIR, "_ref", "libnibble_ref.so")
+        if os.path.exists(path):
+            lib = ctypes.CDLL(path)
+            lib.ref_rope.argtypes = [_F, _I, _I, _I, _I, c_float, c_int, _F]
+            attn = [_F, _F, _F, _F, _I, _I, _I, _I, _I, _I, _I, _F]
+            lib.ref_attention_scalar.argtypes = attn
+            lib.ref_attention_simd.argtypes = attn
+            lib.ref_kernel_set.restype = c_char_p
+            lib.ref_backend_create.argtypes = [c_int]
+            lib.ref_backend_create.restype = c_void_p
+            lib.ref_backend_destroy.argtypes = [c_void_p]
+            lib.ref_backend_destroy.restype = None
+            lib.ref_backend_reserve.argtypes = [c_void_p, _I, _I, _I, _I]
+            lib.ref_backend_attention.argtypes = [c_void_p, _F, _F, _F, _F, _I, _I, _I, _I, _I]
+            lib.ref_backend_rope.argtypes = [c_void_p, _F, _I, _I, _I, _I, c_float, c_int, _F]
+            _ref = lib
+    return _ref
+
+
+def have_ref() -> bool:
+    return _load_ref() is not None
+
+
+def have_avx2() -> bool:
+    return bool(_load().orc_have_avx2())
+
+
+def _fp(a):
+    return a.ctypes.data_as(_F) if a is not None else None
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a
+
+
+# ---- our restatement ----
+
+def rope(x, pos0, freq_base, neox, freq_factors=None):
+    """In-place restatement of cpu::rope on x[n, heads, hd] (returns x)."""
+    assert x.dtype == np.float32 and x.flags.c_contiguous and x.ndim == 3
+    n, h, hd = x.shape
+    ff = _f32(freq_factors) if freq_factors is not None else None
+    _load().orc_rope(_fp(x), n, h, hd, pos0, freq_base, int(bool(neox)), _fp(ff))
+    return x
+
+
+def softmax_inplace(x):
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    _load().orc_softmax_inplace(_fp(x), x.size)
+    return x
+
+
+def _attn_args(q, k, v, pos0, n_kv_heads):
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    n, h, hd = q.shape
+    ctx = pos0 + n
+    assert k.size >= ctx * n_kv_heads * hd and v.size >= ctx * n_kv_heads * hd
+    return q, k, v, n, h, hd, ctx
+
+
+def attention_scalar(q, k, v, pos0, n_kv_heads):
+    """cpu::attention_heads restated (all heads). q[n,H,hd]; k,v[>=pos0+n, KV, hd]."""
+    q, k, v, n, h, hd, ctx = _attn_args(q, k, v, pos0, n_kv_heads)
+    out = np.zeros_like(q)
+    sc = np.zeros(ctx, np.float32)
+    _load().orc_attention_scalar(_fp(q), _fp(k), _fp(v), _fp(out), n, pos0, h, n_kv_heads, hd, 0, h, _fp(sc))
+    return out
+
+
+def attention_avx2(q, k, v, pos0, n_kv_heads):
+    """simd::avx2::attention_heads restated (all heads); None when AVX2 is unavailable."""
+    q, k, v, n, h, hd, ctx = _attn_args(q, k, v, pos0, n_kv_heads)
+    out = np.zeros_like(q)
+    sc = np.zeros(ctx, np.float32)
+    rc = _load().orc_attention_avx2(_fp(q), _fp(k), _fp(v), _fp(out), n, pos0, h, n_kv_heads, hd, 0, h, _fp(sc))
+    return out if rc == 0 else None
+
+
+def attention_parallel(q, k, v, pos0, n_kv_heads, threads, use_avx2=True):
+    """CpuBackend::attention restated: one task per head over `threads` threads."""
+    q, k, v, n, h, hd, ctx = _attn_args(q, k, v, pos0, n_kv_heads)
+    out = np.zeros_like(q)
+    sc = np.zeros(ctx * h, np.float32)
+    rc = _load().orc_attention_heads_parallel(_fp(q), _fp(k), _fp(v), _fp(out), n, pos0, h, n_kv_heads, hd,
+                                              threads, int(use_avx2), _fp(sc))
+    if rc != 0:
+        raise RuntimeError("AVX2 requested but unavailable")
+    return out
+
+
+def attention_f64(q, k, v, pos0, n_kv_heads):
+    q, k, v, n, h, hd, ctx = _attn_args(q, k, v, pos0, n_kv_heads)
+    out = np.zeros(q.shape, np.float64)
+    _load().orc_attention_f64(_fp(q), _fp(k), _fp(v), out.ctypes.data_as(_D), n, pos0, h, n_kv_heads, hd)
+    return out
+
+
+def exp_ps(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    if _load().orc_exp_ps(_fp(x), _fp(y), x.size) != 0:
+        return None
+    return y
+
+
+def llama3_freq_factors(head_dim, base, factor=32.0, low=1.0, high=4.0, orig_ctx=8192.0):
+    out = np.zeros(head_dim // 2, np.float32)
+    _load().orc_llama3_freq_factors(_fp(out), head_dim, base, factor, low, high, orig_ctx)
+    return out
+
+
+# ---- the compiled reference (oracle/_ref) ----
+
+def ref_rope(x, pos0, freq_base, neox, freq_factors=None):
+    lib = _load_ref()
+    assert lib is not None and x.dtype == np.float32 and x.flags.c_contiguous
+    n, h, hd = x.shape
+    ff = _f32(freq_factors) if freq_factors is not None else None
+    lib.ref_rope(_fp(x), n, h, hd, pos0, freq_base, int(bool(neox)), _fp(ff))
+    return x
+
+
+def ref_attention_scalar(q, k, v, pos0, n_kv_heads):
+    lib = _load_ref()
+    q, k, v, n, h, hd, ctx = _attn_args(q, k, v, pos0, n_kv_heads)
+    out = np.zeros_like(q)
+    sc = np.zeros(ctx, np.float32)
+    lib.ref_attention_scalar(_fp(q), _fp(k), _fp(v), _fp(out), n, pos0, h, n_kv_heads, hd, 0, h, _fp(sc))
+    return out
+
+
+def ref_attention_simd(q, k, v, pos0, n_kv_heads):
+    lib = _load_ref()
+    q, k, v, n, h, hd, ctx = _attn_args(q, k, v, pos0, n_kv_heads)
+    out = np.zeros_like(q)
+    sc = np.zeros(ctx, np.float32)
+    rc = lib.ref_attention_simd(_fp(q), _fp(k), _fp(v), _fp(out), n, pos0, h, n_kv_heads, hd, 0, h, _fp(sc))
+    return out if rc == 0 else None
+
+
+def ref_kernel_set() -> str:
+    return _load_ref().ref_kernel_set().decode()
+
+
+class RefCpuBackend:
+    """The reference's ThreadPool + CpuBackend (compiled from its sources), for the CPU baseline."""
+
+    def __init__(self, threads: int):
+        lib = _load_ref()
+        if lib is None:
+            raise RuntimeError("oracle/_ref is not built")
+        self._lib = lib
+        self._h = lib.ref_backend_create(threads)
+        if not self._h:
+            raise RuntimeError("ref_backend_create failed")
+        self.threads = threads
+
+    def reserve(self, n_ctx, n_heads, max_rows, max_width):
+        if self._lib.ref_backend_reserve(self._h, n_ctx, n_heads, max_rows, max_width) != 0:
+            raise RuntimeError("reserve failed")
+
+    def attention(self, q, k, v, out, n, pos0, n_heads, n_kv_heads, head_dim):
+        rc = self._lib.ref_backend_attention(self._h, _fp(q), _fp(k), _fp(v), _fp(out), n, pos0, n_heads,
+                                             n_kv_heads, head_dim)
+        if rc != 0:
+            raise RuntimeError("attention failed")
+
+    def rope(self, x, n, n_heads, head_dim, pos0, base, neox, freq_factors=None):
+        rc = self._lib.ref_backend_rope(self._h, _fp(x), n, n_heads, head_dim, pos0, base, int(bool(neox)),
+                                        _fp(freq_factors))
+        if rc != 0:
+            raise RuntimeError("rope failed")
+
+    def close(self):
+        if self._h:
+            self._lib.ref_backend_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,80 @@
+/*
+ * CPU oracle for nibble's attention path. TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference's scalar and AVX2 attention-path kernels, used solely as the checker
+ * for the HIP backend: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and
+ * never as the thing measured or shipped. The product path (nibble_amd/) does not link or call anything here.
+ *
+ * Each function names the reference file:line it restates (paths relative to the nibble source tree).
+ * Pins (how each function is checked, see tests/test_oracle.py):
+ *   orc_rope               bit-exact vs the compiled reference (oracle/_ref) and the committed fixtures;
+ *                          known answers of tests/test_ref_ops.cpp:41-70; fp64 closed form.
+ *   orc_softmax_inplace    known answer of test_ref_ops.cpp:130-135; bit-exact vs oracle/_ref through attention.
+ *   orc_attention_scalar   bit-exact vs oracle/_ref and fixtures; known answers of test_ref_ops.cpp:73-95;
+ *                          fp64 brute force within 2e-6.
+ *   orc_attention_avx2     bit-exact vs oracle/_ref and fixtures; the 2e-6*qscale contract of
+ *                          tests/test_ops.cpp:196-216 against orc_attention_scalar.
+ *   orc_exp_ps             <= 2e-7 relative vs exp() over [-88, 88] (simd_helpers_test.cpp:92-137 contract).
+ *   orc_attention_f64      independent fp64 brute force (tests/naive_llama.h:118-134 pattern); known answers.
+ *   orc_llama3_freq_factors  closed form of llama.cpp's Llama-3 rope scaling (third-party, not vendored):
+ *                          checked against its defining properties (band limits, continuity at both edges,
+ *                          monotonicity). Bit-level parity with the converter's float32 output is UNPINNED.
+ */
+#ifndef NIBBLE_ORACLE_H
+#define NIBBLE_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ref_ops.cpp:166-185 (cpu::rope). In place on x[n, n_heads, head_dim]; freq_factors is NULL or head_dim/2
+ * floats. neox != 0 pairs (i, i + head_dim/2), else (2i, 2i+1) (config.cpp:24). */
+void orc_rope(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0, float freq_base, int neox,
+              const float* freq_factors);
+
+/* ref_ops.cpp:66-77 (cpu::softmax_inplace): float max, expf, double sum, float(1/sum) scaling. */
+void orc_softmax_inplace(float* x, int64_t n);
+
+/* ref_ops.cpp:188-214 (cpu::attention_heads): heads [head_begin, head_end); scratch holds pos0 + n floats. */
+void orc_attention_scalar(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                          int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t head_begin,
+                          int64_t head_end, float* scratch);
+
+/* simd/ops.cpp:104-139 (simd::avx2::attention_heads) with exp_sub_sum (:31-51), exp_ps (simd.h:103-126) and
+ * hsum_ps (simd.h:37-42). Returns -1 (and does nothing) when this build or CPU lacks AVX2/FMA. */
+int orc_attention_avx2(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                       int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t head_begin, int64_t head_end,
+                       float* scratch);
+
+/* simd.h:103-126 (exp_ps), 8 lanes at a time over x[0..n) into y; -1 without AVX2. */
+int orc_exp_ps(const float* x, float* y, int64_t n);
+
+/* 1 when the AVX2 restatement is compiled in and the CPU supports AVX2+FMA+F16C. */
+int orc_have_avx2(void);
+
+/* cpu_backend.cpp:271-290 (CpuBackend::attention): one task per head on a pool of `threads` threads
+ * (thread_pool.cpp:114-137 parallel_for with chunk 1, caller participates), scratch slot h*(pos0+n).
+ * use_avx2 selects orc_attention_avx2 (the production tier, dispatch.cpp:123-136), else the scalar path.
+ * scratch: n_heads*(pos0+n) floats. Returns 0, or -1 if use_avx2 is requested without AVX2. */
+int orc_attention_heads_parallel(const float* q, const float* k, const float* v, float* out, int64_t n,
+                                 int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int threads,
+                                 int use_avx2, float* scratch);
+
+/* Independent fp64 brute force (tests/naive_llama.h:118-134 pattern) on the same fp32 inputs; out is double. */
+void orc_attention_f64(const float* q, const float* k, const float* v, double* out, int64_t n, int64_t pos0,
+                       int64_t n_heads, int64_t n_kv_heads, int64_t head_dim);
+
+/* Llama-3 rope frequency factors (llama.cpp convert_hf_to_gguf.py, rope_type "llama3"; not in the reference
+ * tree, the reference only reads rope_freqs.weight, weights.cpp:56, and divides by it, ref_ops.cpp:175):
+ * for freq_i = base^(-2i/head_dim) and wavelen = 2*pi/freq_i, factor_i = 1 if wavelen < orig/high,
+ * `factor` if wavelen > orig/low, else 1/((1-s)/factor + s) with s = (orig/wavelen - low)/(high - low).
+ * Computed in double, stored as float. */
+void orc_llama3_freq_factors(float* out, int64_t head_dim, double base, double factor, double low_freq_factor,
+                             double high_freq_factor, double orig_ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,106 @@
+// C entry points over the compiled reference CPU backend. TEST INFRASTRUCTURE ONLY: the real nibble sources are
+// compiled where they lie under the reference tree (oracle/Makefile, target `ref`) into oracle/_ref/, and this
+// file (our own code) exposes them to ctypes so tests can pin the C restatement against the reference itself and
+// bench.py can time the reference's CPU attention as its baseline. Nothing of the reference is copied here.
+#include <cstdint>
+#include <exception>
+#include <new>
+
+#include "backend/cpu/cpu_backend.h"
+#include "backend/cpu/ref_ops.h"
+#include "backend/cpu/simd/dispatch.h"
+#include "thread_pool.h"
+
+namespace {
+struct RefBackend {
+  nibble::ThreadPool pool;
+  nibble::cpu::CpuBackend be;
+  explicit RefBackend(int threads) : pool(threads), be(pool) {}
+};
+}  // namespace
+
+extern "C" {
+
+// nibble::cpu::rope (ref_ops.cpp:166-185).
+int ref_rope(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0, float base, int neox,
+             const float* freq_factors) {
+  nibble::RopeParams p{base, neox != 0, freq_factors};
+  nibble::cpu::rope(x, n, n_heads, head_dim, pos0, p);
+  return 0;
+}
+
+// nibble::cpu::attention_heads (ref_ops.cpp:188-214).
+int ref_attention_scalar(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                         int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t head_begin, int64_t head_end,
+                         float* scratch) {
+  nibble::cpu::attention_heads(q, k, v, out, n, pos0, n_heads, n_kv_heads, head_dim, head_begin, head_end, scratch);
+  return 0;
+}
+
+// The selected SIMD tier's attention_heads (simd/ops.cpp:104-139 on AVX2 hosts); -1 when no tier is available.
+int ref_attention_simd(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                       int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t head_begin, int64_t head_end,
+                       float* scratch) {
+  try {
+    const nibble::simd::Kernels* ks = nibble::simd::select();
+    if (!ks) return -1;
+    ks->attention_heads(q, k, v, out, n, pos0, n_heads, n_kv_heads, head_dim, head_begin, head_end, scratch);
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// "scalar", "avx2+fma+f16c", ...: the tier CpuBackend runs on this host (dispatch.cpp:150-153).
+const char* ref_kernel_set() {
+  try {
+    return nibble::simd::kernel_set();
+  } catch (const std::exception&) {
+    return "error";
+  }
+}
+
+// A ThreadPool of `threads` threads and a CpuBackend on it (nibble.cpp:75-85 builds the same pair).
+void* ref_backend_create(int threads) {
+  try {
+    return new RefBackend(threads);
+  } catch (const std::exception&) {
+    return nullptr;
+  }
+}
+
+void ref_backend_destroy(void* h) { delete static_cast<RefBackend*>(h); }
+
+// CpuBackend::reserve (cpu_backend.cpp:24-67).
+int ref_backend_reserve(void* h, int64_t n_ctx, int64_t n_heads, int64_t max_rows, int64_t max_width) {
+  try {
+    static_cast<RefBackend*>(h)->be.reserve({n_ctx, n_heads, max_rows, max_width});
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// CpuBackend::attention (cpu_backend.cpp:271-290): parallel_for over heads, chunk 1.
+int ref_backend_attention(void* h, const float* q, const float* k, const float* v, float* out, int64_t n,
+                          int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim) {
+  try {
+    static_cast<RefBackend*>(h)->be.attention(q, k, v, out, n, pos0, n_heads, n_kv_heads, head_dim);
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// CpuBackend::rope (cpu_backend.cpp:253-259): scalar, on the calling thread.
+int ref_backend_rope(void* h, float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0, float base,
+                     int neox, const float* freq_factors) {
+  try {
+    static_cast<RefBackend*>(h)->be.rope(x, n, n_heads, head_dim, pos0, {base, neox != 0, freq_factors});
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,126 @@
+"""Writes the golden vectors in tests/golden/*.npz from the reference's own CPU kernels.
+
+Run in a container where oracle/_ref/libnibble_ref.so was built from the reference sources (oracle/Makefile,
+target `ref`). The reference holds no RoPE or attention golden vectors of its own (its tests compute expected
+values inline), so these are produced by its compiled code: cpu::rope (ref_ops.cpp:166-185),
+cpu::attention_heads (ref_ops.cpp:188-214) and the AVX2 attention_heads (simd/ops.cpp:104-139).
+
+Inputs come from nibble_amd.synth (counter-based, deterministic); each case stores its stream keys, its shape and
+a SHA-256 of the input bytes (so a generator change is detected), plus the expected outputs. Large inputs are not
+stored: the keys regenerate them.
+
+    python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import hashlib
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+import oracle  # noqa: E402
+from nibble_amd import synth  # noqa: E402
+
+# (name, n, pos0, H, KV, D, qscale): the six shapes of the reference's SIMD-vs-scalar attention test
+# (tests/test_ops.cpp:196-216) plus the BASELINE shapes at sizes a CPU finishes quickly.
+ATTN_CASES = [
+    ("ops_d8", 1, 0, 2, 1, 8, 1.0),
+    ("ops_d16", 7, 3, 6, 2, 16, 1.0),
+    ("ops_d64_pos300", 4, 300, 4, 2, 64, 1.0),
+    ("ops_d13", 3, 40, 2, 2, 13, 1.0),
+    ("ops_d128", 2, 20, 4, 1, 128, 1.0),
+    ("ops_qscale30", 5, 60, 4, 2, 64, 30.0),
+    ("backend_d16", 7, 3, 6, 2, 16, 1.0),           # test_cpu_backend.cpp:64-77 shape
+    ("cfg1_qwen_decode", 1, 512, 14, 2, 64, 1.0),    # config 1 exactly
+    ("qwen_prefill_96", 96, 0, 14, 2, 64, 1.0),      # config 2 shape, reduced length
+    ("qwen_chunk", 40, 300, 14, 2, 64, 1.0),         # chunked prefill (pos0 > 0)
+    ("tinyllama_decode", 1, 1792, 32, 4, 64, 1.0),   # config 3 first step
+    ("llama_decode_2k", 1, 2047, 32, 8, 64, 1.0),    # config 4/5 shape, reduced context
+    ("llama_prefill_300", 300, 0, 32, 8, 64, 1.0),   # crosses the fp32/MFMA prefill split at 256
+    ("d128_prefill", 64, 200, 8, 2, 128, 1.0),
+]
+
+# (name, n, heads, hd, pos0, base, neox, llama3)
+ROPE_CASES = [
+    ("qwen_q_pos512", 1, 14, 64, 512, 1e6, True, False),
+    ("qwen_k_prefill", 2048, 2, 64, 0, 1e6, True, False),
+    ("tinyllama_q_pos2047", 1, 32, 64, 2047, 1e4, False, False),
+    ("llama_k_pos8191", 3, 8, 64, 8191, 5e5, False, True),
+    ("llama_q_pos32768", 2, 32, 64, 32768, 5e5, False, True),
+    ("llama_k_pos131071", 1, 8, 64, 131071, 5e5, False, True),
+    ("neox_hd128_pos65536", 2, 4, 128, 65536, 1e4, True, False),
+    ("hd4_pos1", 1, 1, 4, 1, 1e4, False, False),
+]
+
+
+def sha(*arrays) -> np.ndarray:
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return np.frombuffer(h.digest(), dtype=np.uint8).copy()
+
+
+FULL_LIMIT = 16384  # outputs larger than this many floats are stored as a SHA-256 plus sample rows
+
+
+def put_output(out, key, y):
+    """Stores y whole, or (when large) its SHA-256 with its first two and last rows, under key."""
+    if y.size <= FULL_LIMIT:
+        out[key] = y
+    else:
+        out[key + "_sha256"] = sha(y)
+        out[key + "_head"] = y[:2].copy()
+        out[key + "_tail"] = y[-1:].copy()
+
+
+def attn_inputs(i, n, pos0, H, KV, D, qscale):
+    ctx = pos0 + n
+    q = synth.normal_array((n, H, D), 900, i, 1) * np.float32(qscale)
+    k = synth.normal_array((ctx, KV, D), 900, i, 2)
+    v = synth.normal_array((ctx, KV, D), 900, i, 3)
+    return q.astype(np.float32), k, v
+
+
+def rope_input(i, n, heads, hd):
+    return synth.normal_array((n, heads, hd), 901, i, 1)
+
+
+def main():
+    if not oracle.have_ref():
+        sys.exit("oracle/_ref/libnibble_ref.so is not built; run `make -C oracle ref` first")
+    out = {}
+    for i, (name, n, pos0, H, KV, D, qs) in enumerate(ATTN_CASES):
+        q, k, v = attn_inputs(i, n, pos0, H, KV, D, qs)
+        out[f"attn/{name}/shape"] = np.array([i, n, pos0, H, KV, D], np.int64)
+        out[f"attn/{name}/qscale"] = np.array([qs], np.float32)
+        out[f"attn/{name}/input_sha256"] = sha(q, k, v)
+        put_output(out, f"attn/{name}/scalar", oracle.ref_attention_scalar(q, k, v, pos0, KV))
+        simd = oracle.ref_attention_simd(q, k, v, pos0, KV)
+        if simd is None:
+            sys.exit("the reference's SIMD tier is unavailable on this host; golden vectors need AVX2")
+        put_output(out, f"attn/{name}/simd", simd)
+    for i, (name, n, heads, hd, pos0, base, neox, l3) in enumerate(ROPE_CASES):
+        x = rope_input(i, n, heads, hd)
+        ff = synth.llama3_freq_factors(hd, base) if l3 else None
+        y = oracle.ref_rope(x.copy(), pos0, base, neox, ff)
+        out[f"rope/{name}/params"] = np.array([i, n, heads, hd, pos0, int(neox), int(l3)], np.int64)
+        out[f"rope/{name}/base"] = np.array([base], np.float32)
+        out[f"rope/{name}/input_sha256"] = sha(x)
+        if ff is not None:
+            out[f"rope/{name}/freq_factors"] = ff
+        put_output(out, f"rope/{name}/out", y)
+    # Known answers of test_ref_ops.cpp:73-95 / 130-135 evaluated by the reference itself.
+    qkv = np.array([[[1, 0]], [[0, 1]]], np.float32)  # n=2, H=1, D=2
+    out["kat/attention_2tok/out"] = oracle.ref_attention_scalar(qkv, qkv, qkv, 0, 1)
+    path = os.path.join(HERE, "reference_vectors.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path}: {len(out)} arrays, {os.path.getsize(path)} bytes, kernel tier {oracle.ref_kernel_set()}")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,68 @@
+"""Shared helpers for the GPU parity tests: device buffers that are freed at the end of a test, and the parity
+metric used everywhere.
+
+Parity (fp32 attention outputs vs the oracle): all three must hold, with ATOL = RTOL = 1e-3
+  * max |g - r|                      <= ATOL        (max-abs error)
+  * max |g - r| / max |r|            <= RTOL        (relative error, normalised by the output's magnitude)
+  * |g - r| <= ATOL + RTOL * |r|     elementwise    (numpy.allclose form)
+RoPE outputs, appended cache rows and masked/unmasked comparisons are bit-exact (compared as uint32).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+ATOL = 1e-3
+RTOL = 1e-3
+
+
+def parity(got: np.ndarray, ref: np.ndarray) -> dict:
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    scale = float(np.max(np.abs(ref))) if ref.size else 0.0
+    return {
+        "max_abs": float(err.max()) if err.size else 0.0,
+        "max_rel": float(err.max() / scale) if err.size and scale > 0 else 0.0,
+        "allclose": bool(np.all(err <= ATOL + RTOL * np.abs(ref))),
+        "finite": bool(np.all(np.isfinite(got))),
+    }
+
+
+def assert_parity(got, ref, what=""):
+    p = parity(got, ref)
+    print(f"parity {what}: max_abs={p['max_abs']:.3e} max_rel={p['max_rel']:.3e} allclose={p['allclose']}", flush=True)
+    assert p["finite"], f"{what}: non-finite output"
+    assert p["max_abs"] <= ATOL, f"{what}: max-abs {p['max_abs']:.3e} > {ATOL}"
+    assert p["max_rel"] <= RTOL, f"{what}: max-rel {p['max_rel']:.3e} > {RTOL}"
+    assert p["allclose"], f"{what}: elementwise |g-r| <= atol + rtol|r| violated"
+    return p
+
+
+def bits(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+class Buffers:
+    """Device buffers from a HipBackend, freed together (use as a context manager)."""
+
+    def __init__(self, be):
+        self.be = be
+        self.ptrs = []
+
+    def alloc(self, n_floats):
+        p = self.be.alloc(n_floats)
+        self.ptrs.append(p)
+        return p
+
+    def upload(self, host):
+        p = self.be.upload(host)
+        self.ptrs.append(p)
+        return p
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        for p in self.ptrs:
+            self.be.free(p)
+        self.ptrs.clear()

@@ -1,0 +1,340 @@
+"""GPU parity of the HIP attention path against the CPU oracle, through the C ABI (libnibble_hip.so).
+
+RoPE and the KV append are bit-exact; attention meets the tolerance in gpu_util (1e-3 max-abs, 1e-3 relative,
+elementwise allclose) against the restated reference (scalar cpu::attention_heads, and the AVX2 tier where the
+host has it); the causal mask is checked bitwise with NaN poison beyond each row's window.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from nibble_amd import configs, synth
+from tests.gpu_util import Buffers, assert_parity, bits
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLD = np.load(os.path.join(HERE, "golden", "reference_vectors.npz"))
+
+import importlib.util as _ilu  # noqa: E402
+
+_spec = _ilu.spec_from_file_location("make_golden", os.path.join(HERE, "golden", "make_golden.py"))
+make_golden = _ilu.module_from_spec(_spec)
+_spec.loader.exec_module(make_golden)
+
+
+def cpu_attention(q, k, v, pos0, kv):
+    """The reference's production CPU path (AVX2 tier, head-parallel) where available, else its scalar path."""
+    if oracle.have_avx2():
+        return oracle.attention_parallel(q, k, v, pos0, kv, threads=min(16, os.cpu_count() or 1))
+    return oracle.attention_scalar(q, k, v, pos0, kv)
+
+
+def gpu_attention(be, q, k, v, pos0, kv):
+    """Uploads q and the caches k, v and runs Backend::attention."""
+    n, H, D = q.shape
+    with Buffers(be) as B:
+        dq, dk, dv, do = B.upload(q), B.upload(k), B.upload(v), B.alloc(q.size)
+        be.attention(dq, dk, dv, do, n, pos0, H, kv, D)
+        return be.download(do, q.shape)
+
+
+# ------------------------------------------------------------------------------------------------ RoPE
+
+@pytest.mark.parametrize("case", make_golden.ROPE_CASES, ids=[c[0] for c in make_golden.ROPE_CASES])
+def test_rope_bit_exact_vs_reference_vectors(backend, case):
+    name, n, heads, hd, pos0, base, neox, l3 = case
+    i = int(GOLD[f"rope/{name}/params"][0])
+    x = make_golden.rope_input(i, n, heads, hd)
+    ff = synth.llama3_freq_factors(hd, base) if l3 else None
+    with Buffers(backend) as B:
+        dx = B.upload(x)
+        backend.rope(dx, n, heads, hd, pos0, base, neox, ff)
+        y = backend.download(dx, x.shape)
+    ref = oracle.rope(x.copy(), pos0, base, neox, ff)
+    assert np.array_equal(bits(y), bits(ref)), f"{name}: {np.sum(bits(y) != bits(ref))} elements differ"
+
+
+@pytest.mark.parametrize("shape", [configs.QWEN25_05B, configs.TINYLLAMA_11B, configs.LLAMA32_1B],
+                         ids=lambda s: s.name)
+def test_append_rope_bit_exact_and_rows_outside_untouched(backend, shape):
+    H, KV, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
+    ff = shape.freq_factors()
+    n_ctx, pos0, n = 600, 517, 20
+    q = synth.normal_array((n, H, D), 3, 1)
+    kn = synth.normal_array((n, KV, D), 3, 2)
+    vn = synth.normal_array((n, KV, D), 3, 3)
+    with Buffers(backend) as B:
+        dq, dkn, dvn = B.upload(q), B.upload(kn), B.upload(vn)
+        ck, cv = B.alloc(n_ctx * KV * D), B.alloc(n_ctx * KV * D)
+        backend.append_rope(dq, ck, cv, dkn, dvn, n, pos0, H, KV, D, shape.rope_base, shape.neox, ff)
+        gq = backend.download(dq, q.shape)
+        gk = backend.download(ck, (n_ctx, KV, D))
+        gv = backend.download(cv, (n_ctx, KV, D))
+        # the same through the drop-in ops: write rows, then rope in place on the cache rows (transformer.cpp:198)
+        ck2 = B.alloc(n_ctx * KV * D)
+        backend.write(ck2.at(pos0 * KV * D), kn)
+        backend.rope(ck2.at(pos0 * KV * D), n, KV, D, pos0, shape.rope_base, shape.neox, ff)
+        gk2 = backend.download(ck2, (n_ctx, KV, D))
+    assert np.array_equal(bits(gq), bits(oracle.rope(q.copy(), pos0, shape.rope_base, shape.neox, ff)))
+    rk = oracle.rope(kn.copy(), pos0, shape.rope_base, shape.neox, ff)
+    assert np.array_equal(bits(gk[pos0:pos0 + n]), bits(rk))
+    assert np.array_equal(bits(gv[pos0:pos0 + n]), bits(vn))
+    assert not np.any(bits(gk[:pos0])) and not np.any(bits(gk[pos0 + n:]))
+    assert not np.any(bits(gv[:pos0])) and not np.any(bits(gv[pos0 + n:]))
+    assert np.array_equal(bits(gk2), bits(gk))
+
+
+# ------------------------------------------------------------------------------------------------ attention
+
+@pytest.mark.parametrize("case", make_golden.ATTN_CASES, ids=[c[0] for c in make_golden.ATTN_CASES])
+def test_attention_golden_cases(backend, case):
+    name, n, pos0, H, KV, D, qs = case
+    i = int(GOLD[f"attn/{name}/shape"][0])
+    q, k, v = make_golden.attn_inputs(i, n, pos0, H, KV, D, qs)
+    ref = oracle.attention_scalar(q, k, v, pos0, KV)
+    key = f"attn/{name}/scalar"
+    if key in GOLD.files:
+        assert np.array_equal(bits(ref), bits(GOLD[key]))  # the oracle reproduces the reference's vector
+    got = gpu_attention(backend, q, k, v, pos0, KV)
+    assert_parity(got, ref, name)
+
+
+@pytest.mark.parametrize("D", [2, 8, 13, 16, 24, 64, 128])
+@pytest.mark.parametrize("H,KV", [(4, 4), (6, 3), (8, 2), (14, 2), (32, 4), (16, 1)])
+def test_attention_head_shapes(backend, D, H, KV):
+    rng = np.random.default_rng(D * 131 + H * 7 + KV)
+    for n, pos0 in [(1, 0), (1, 77), (3, 50), (40, 0), (37, 300)]:
+        q = rng.standard_normal((n, H, D)).astype(np.float32)
+        k = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+        v = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+        assert_parity(gpu_attention(backend, q, k, v, pos0, KV), oracle.attention_scalar(q, k, v, pos0, KV),
+                      f"D={D} H={H} KV={KV} n={n} pos0={pos0}")
+
+
+def test_config1_qwen_decode(backend):
+    """Qwen shape, one layer, one token at position 512 over 512 cached rows."""
+    s = configs.QWEN25_05B
+    H, KV, D, pos0 = s.n_heads, s.n_kv_heads, s.head_dim, 512
+    cache_k = synth.normal_array((pos0, KV, D), 1, 0, configs.T_KCACHE)
+    cache_v = synth.normal_array((pos0, KV, D), 1, 0, configs.T_VCACHE)
+    q = synth.normal_array((1, H, D), 1, 0, configs.T_Q)
+    kn = synth.normal_array((1, KV, D), 1, 0, configs.T_K)
+    vn = synth.normal_array((1, KV, D), 1, 0, configs.T_V)
+    with Buffers(backend) as B:
+        ck, cv = B.alloc((pos0 + 1) * KV * D), B.alloc((pos0 + 1) * KV * D)
+        backend.write(ck, cache_k)
+        backend.write(cv, cache_v)
+        dq, dkn, dvn, do = B.upload(q), B.upload(kn), B.upload(vn), B.alloc(H * D)
+        backend.append_rope(dq, ck, cv, dkn, dvn, 1, pos0, H, KV, D, s.rope_base, s.neox, None)
+        backend.attention(dq, ck, cv, do, 1, pos0, H, KV, D)
+        got = backend.download(do, (1, H, D))
+        gk = backend.download(ck, (pos0 + 1, KV, D))
+    qr = oracle.rope(q.copy(), pos0, s.rope_base, s.neox)
+    kr = oracle.rope(kn.copy(), pos0, s.rope_base, s.neox)
+    assert np.array_equal(bits(gk[pos0]), bits(kr[0]))
+    k_all = np.concatenate([cache_k, kr])
+    v_all = np.concatenate([cache_v, vn])
+    ref = oracle.attention_scalar(qr, k_all, v_all, pos0, KV)
+    assert_parity(got, ref, "config1 vs scalar")
+    if oracle.have_avx2():
+        assert_parity(got, oracle.attention_avx2(qr, k_all, v_all, pos0, KV), "config1 vs avx2")
+    assert_parity(got, oracle.attention_f64(qr, k_all, v_all, pos0, KV), "config1 vs fp64")
+
+
+@pytest.mark.parametrize("n,pos0", [(1, 0), (1, 63), (1, 4095), (2, 1000), (7, 333), (16, 2500), (17, 10),
+                                    (300, 0), (600, 100), (1024, 0)])
+def test_causal_mask_poison(backend, n, pos0):
+    """Rows past the causal window (and past the context) are NaN: the result must be finite and bitwise equal
+    to the run without poison (decode, fp32-prefix and MFMA paths)."""
+    H, KV, D = 32, 8, 64
+    q = synth.normal_array((n, H, D), 7, n, pos0, 1)
+    k = synth.normal_array((pos0 + n, KV, D), 7, n, pos0, 2)
+    v = synth.normal_array((pos0 + n, KV, D), 7, n, pos0, 3)
+    clean = gpu_attention(backend, q, k, v, pos0, KV)
+    # Poison inside the window of later rows cannot be used (they legitimately see it); poison only rows > ctx.
+    with Buffers(backend) as B:
+        pad = 200
+        kp = np.concatenate([k, np.full((pad, KV, D), np.nan, np.float32)])
+        vp = np.concatenate([v, np.full((pad, KV, D), np.nan, np.float32)])
+        dq, dk, dv, do = B.upload(q), B.upload(kp), B.upload(vp), B.alloc(q.size)
+        backend.attention(dq, dk, dv, do, n, pos0, H, KV, D)
+        poisoned = backend.download(do, q.shape)
+    assert np.all(np.isfinite(poisoned))
+    assert np.array_equal(bits(clean), bits(poisoned))
+    # Per-row poison: row t of a separate single-row call at position pos0+t sees NaN right after its window.
+    rng = np.random.default_rng(n + pos0)
+    for t in sorted(set(rng.integers(0, n, 3).tolist())):
+        with Buffers(backend) as B:
+            L = pos0 + t + 1
+            kp = np.concatenate([k[:L], np.full((5, KV, D), np.nan, np.float32)])
+            vp = np.concatenate([v[:L], np.full((5, KV, D), np.nan, np.float32)])
+            dq, dk, dv, do = B.upload(q[t:t + 1]), B.upload(kp), B.upload(vp), B.alloc(H * D)
+            backend.attention(dq, dk, dv, do, 1, pos0 + t, H, KV, D)
+            row = backend.download(do, (1, H, D))
+        assert np.all(np.isfinite(row))
+    assert_parity(clean, cpu_attention(q, k, v, pos0, KV), f"poison case n={n} pos0={pos0}")
+
+
+def test_mfma_rows_chunking_invariant_bitwise(backend):
+    """A prefill split into max_batch chunks (transformer.cpp:135-136) gives bitwise the same rows as one call."""
+    H, KV, D, n = 32, 8, 64, 1536
+    q = synth.normal_array((n, H, D), 8, 1)
+    k = synth.normal_array((n, KV, D), 8, 2)
+    v = synth.normal_array((n, KV, D), 8, 3)
+    with Buffers(backend) as B:
+        dq, dk, dv = B.upload(q), B.upload(k), B.upload(v)
+        whole, parts = B.alloc(q.size), B.alloc(q.size)
+        backend.attention(dq, dk, dv, whole, n, 0, H, KV, D)
+        for off in range(0, n, 512):
+            backend.attention(dq.at(off * H * D), dk, dv, parts.at(off * H * D), 512, off, H, KV, D)
+        a = backend.download(whole, q.shape)
+        b = backend.download(parts, q.shape)
+    assert np.array_equal(bits(a), bits(b))
+    assert_parity(a, cpu_attention(q, k, v, 0, KV), "prefill 1536")
+
+
+def test_small_chunks_match_batch_within_tolerance(backend):
+    """Incremental (n=1), 2-token chunks and one batch agree within tolerance (the reference requires bitwise
+    equality of its CPU paths, test_model.cpp:141-151; here n <= 16 calls take the fp32 kernel and larger batches
+    the fp16-operand MFMA kernel)."""
+    H, KV, D, n = 14, 2, 64, 300
+    q = synth.normal_array((n, H, D), 9, 1)
+    k = synth.normal_array((n, KV, D), 9, 2)
+    v = synth.normal_array((n, KV, D), 9, 3)
+    with Buffers(backend) as B:
+        dq, dk, dv = B.upload(q), B.upload(k), B.upload(v)
+        whole, ones, twos = B.alloc(q.size), B.alloc(q.size), B.alloc(q.size)
+        backend.attention(dq, dk, dv, whole, n, 0, H, KV, D)
+        for t in range(n):
+            backend.attention(dq.at(t * H * D), dk, dv, ones.at(t * H * D), 1, t, H, KV, D)
+        for t in range(0, n, 2):
+            backend.attention(dq.at(t * H * D), dk, dv, twos.at(t * H * D), 2, t, H, KV, D)
+        a, b, c = (backend.download(x, q.shape) for x in (whole, ones, twos))
+    ref = oracle.attention_scalar(q, k, v, 0, KV)
+    for got, what in ((a, "batch"), (b, "one-by-one"), (c, "2-token chunks")):
+        assert_parity(got, ref, what)
+
+
+# ------------------------------------------------------------------------------------------------ full-size configs
+
+def test_config4_prefill_8k_one_layer_sampled_rows(backend):
+    """Config 4 prefill at its full size (8192 tokens, Llama-3.2 shape) for layer 0: RoPE'd K rows land in the cache
+    bit-exactly; attention output checked against the oracle on a sample of rows spread over the sequence."""
+    s = configs.LLAMA32_1B
+    H, KV, D, n = s.n_heads, s.n_kv_heads, s.head_dim, 8192
+    ff = s.freq_factors()
+    q = synth.normal_array((n, H, D), 4, 0, configs.T_Q)
+    kn = synth.normal_array((n, KV, D), 4, 0, configs.T_K)
+    vn = synth.normal_array((n, KV, D), 4, 0, configs.T_V)
+    with Buffers(backend) as B:
+        dq, dkn, dvn = B.upload(q), B.upload(kn), B.upload(vn)
+        ck, cv, do = B.alloc(n * KV * D), B.alloc(n * KV * D), B.alloc(q.size)
+        backend.append_rope(dq, ck, cv, dkn, dvn, n, 0, H, KV, D, s.rope_base, s.neox, ff)
+        backend.attention(dq, ck, cv, do, n, 0, H, KV, D)
+        got = backend.download(do, q.shape)
+        gk = backend.download(ck, kn.shape)
+        gq = backend.download(dq, q.shape)
+    kr = oracle.rope(kn.copy(), 0, s.rope_base, s.neox, ff)
+    qr = oracle.rope(q.copy(), 0, s.rope_base, s.neox, ff)
+    assert np.array_equal(bits(gk), bits(kr)) and np.array_equal(bits(gq), bits(qr))
+    rows = sorted(set([0, 1, 2, 63, 64, 127, 255, 256, 257, 511, 4095, 4096, 8190, 8191] +
+                      np.random.default_rng(4).integers(0, n, 40).tolist()))
+    for t in rows:
+        ref = cpu_attention(qr[t:t + 1], kr[:t + 1], vn[:t + 1], t, KV)
+        assert_parity(got[t:t + 1], ref, f"prefill row {t}")
+
+
+def test_config4_decode_32k(backend):
+    """Config 4 decode: one layer, 32768-row cache (rows 0..8191 from the prefill stream, rest seeded), one new token
+    appended at 32768 and attended; two more steps."""
+    s = configs.LLAMA32_1B
+    H, KV, D, ctx = s.n_heads, s.n_kv_heads, s.head_dim, 32768
+    ff = s.freq_factors()
+    cache_k = synth.normal_array((ctx, KV, D), 4, 0, configs.T_KCACHE)
+    cache_v = synth.normal_array((ctx, KV, D), 4, 0, configs.T_VCACHE)
+    with Buffers(backend) as B:
+        cap = ctx + 64
+        ck, cv = B.alloc(cap * KV * D), B.alloc(cap * KV * D)
+        backend.write(ck, cache_k)
+        backend.write(cv, cache_v)
+        k_all, v_all = cache_k, cache_v
+        for step in range(3):
+            pos0 = ctx + step
+            q = synth.normal_array((1, H, D), 4, 0, 100 + step, configs.T_Q)
+            kn = synth.normal_array((1, KV, D), 4, 0, 100 + step, configs.T_K)
+            vn = synth.normal_array((1, KV, D), 4, 0, 100 + step, configs.T_V)
+            dq, dkn, dvn, do = B.upload(q), B.upload(kn), B.upload(vn), B.alloc(H * D)
+            backend.append_rope(dq, ck, cv, dkn, dvn, 1, pos0, H, KV, D, s.rope_base, s.neox, ff)
+            backend.attention(dq, ck, cv, do, 1, pos0, H, KV, D)
+            got = backend.download(do, (1, H, D))
+            kr = oracle.rope(kn.copy(), pos0, s.rope_base, s.neox, ff)
+            qr = oracle.rope(q.copy(), pos0, s.rope_base, s.neox, ff)
+            row = backend.download(ck.at(pos0 * KV * D), (1, KV, D))
+            assert np.array_equal(bits(row), bits(kr))
+            k_all = np.concatenate([k_all, kr])
+            v_all = np.concatenate([v_all, vn])
+            assert_parity(got, cpu_attention(qr, k_all, v_all, pos0, KV), f"decode step {step} @ {pos0}")
+
+
+# ------------------------------------------------------------------------------------------------ boundary behaviour
+
+def test_out_of_range_arguments_raise_before_launch(backend):
+    import nibble_amd
+
+    H, KV, D = 8, 2, 64
+    with Buffers(backend) as B:
+        q, out = B.alloc(H * D), B.alloc(H * D)
+        k, v = B.alloc(100 * KV * D), B.alloc(100 * KV * D)
+        backend.attention(q, k, v, out, 1, 99, H, KV, D)  # exactly fits
+        with pytest.raises(nibble_amd.BackendError, match="not inside"):
+            backend.attention(q, k, v, out, 1, 100, H, KV, D)  # needs 101 rows
+        with pytest.raises(nibble_amd.BackendError, match="not inside"):
+            backend.attention(q, k, v, out, 2, 0, H, KV, D)  # q too short for 2 rows
+        with pytest.raises(nibble_amd.BackendError, match="multiple"):
+            backend.attention(q, k, v, out, 1, 0, 6, 4, D)
+        with pytest.raises(nibble_amd.BackendError, match="even"):
+            backend.rope(q, 1, H, 63, 0, 1e4, False)
+        with pytest.raises(nibble_amd.BackendError, match="not inside"):
+            backend.rope(q.at(1), 1, H, D, 0, 1e4, False)
+        host = np.zeros(10, np.float32)
+        with pytest.raises(nibble_amd.BackendError):
+            backend.read(0x1000, 10, host)
+        backend.sync()
+
+
+def test_alloc_free_bookkeeping(backend):
+    base = backend.live_allocations()
+    a = backend.alloc(100)
+    assert backend.live_allocations() == base + 1
+    assert not np.any(backend.read(a, 100))  # zeroed
+    backend.free(a)
+    backend.free(None)
+    backend.free(a)  # unknown now: ignored
+    assert backend.live_allocations() == base
+
+
+def test_reserve_prevents_workspace_growth(backend):
+    """After reserve() and reserve_attention(), decode at every position up to n_ctx and prefill chunks allocate
+    nothing (the HIP counterpart of test_cpu_backend.cpp:89-103)."""
+    import nibble_amd
+
+    be = nibble_amd.HipBackend(0)
+    try:
+        H, KV, D, n_ctx = 32, 8, 64, 4096
+        be.reserve(n_ctx, H, 512, 2048)
+        be.reserve_attention(KV, D)
+        be.reserve_rope(D, 5e5, False, synth.llama3_freq_factors(D, 5e5))
+        cap = be.internal_bytes()
+        q, out = be.alloc(512 * H * D), be.alloc(512 * H * D)
+        k, v = be.alloc(n_ctx * KV * D), be.alloc(n_ctx * KV * D)
+        for pos in list(range(0, 64)) + list(range(64, n_ctx, 97)) + [n_ctx - 1]:
+            be.attention(q, k, v, out, 1, pos, H, KV, D)
+            be.rope(q, 1, H, D, pos, 5e5, False, synth.llama3_freq_factors(D, 5e5))
+        for off in range(0, n_ctx, 512):
+            be.attention(q, k, v, out, 512, off, H, KV, D)
+        be.sync()
+        assert be.internal_bytes() == cap
+    finally:
+        be.close()

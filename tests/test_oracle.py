@@ -1,0 +1,284 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it. CPU only.
+
+Sources of truth, in order:
+  * tests/golden/reference_vectors.npz, written by the reference's own compiled kernels (make_golden.py):
+    the restatement must reproduce them bit for bit;
+  * oracle/_ref (the reference compiled from its sources) on fresh random shapes, when present;
+  * the reference's known-answer tests (tests/test_ref_ops.cpp:41-135) and tolerance contracts
+    (tests/test_ops.cpp:196-216, simd_helpers_test.cpp:92-137);
+  * mathematics: an fp64 brute force, closed-form rotations, Llama-3 factor properties.
+The last tests plant plausible mistakes in copies of the oracle's math and check that the pins reject them.
+"""
+import hashlib
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from nibble_amd import synth
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLD = np.load(os.path.join(HERE, "golden", "reference_vectors.npz"))  # allow_pickle defaults to False
+
+import importlib.util as _ilu  # noqa: E402
+
+_spec = _ilu.spec_from_file_location("make_golden", os.path.join(HERE, "golden", "make_golden.py"))
+make_golden = _ilu.module_from_spec(_spec)
+_spec.loader.exec_module(make_golden)
+
+
+def sha(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return np.frombuffer(h.digest(), dtype=np.uint8)
+
+
+def matches_gold(key, y):
+    """y equals the stored output bit for bit (whole array, or its SHA-256 for large outputs)."""
+    if key in GOLD.files:
+        return np.array_equal(GOLD[key].view(np.uint32), np.ascontiguousarray(y).view(np.uint32))
+    return np.array_equal(GOLD[key + "_sha256"], sha(y))
+
+
+def bits_equal(a, b):
+    return np.array_equal(np.ascontiguousarray(a).view(np.uint32), np.ascontiguousarray(b).view(np.uint32))
+
+
+# ---------------------------------------------------------------- golden vectors (written by the reference)
+
+@pytest.mark.parametrize("case", make_golden.ATTN_CASES, ids=[c[0] for c in make_golden.ATTN_CASES])
+def test_attention_restatement_reproduces_reference_vectors(case):
+    name, n, pos0, H, KV, D, qs = case
+    i = int(GOLD[f"attn/{name}/shape"][0])
+    q, k, v = make_golden.attn_inputs(i, n, pos0, H, KV, D, qs)
+    assert np.array_equal(GOLD[f"attn/{name}/input_sha256"], sha(q, k, v)), "input generator drifted"
+    assert matches_gold(f"attn/{name}/scalar", oracle.attention_scalar(q, k, v, pos0, KV))
+    if oracle.have_avx2():
+        assert matches_gold(f"attn/{name}/simd", oracle.attention_avx2(q, k, v, pos0, KV))
+        assert matches_gold(f"attn/{name}/simd", oracle.attention_parallel(q, k, v, pos0, KV, threads=3))
+
+
+@pytest.mark.parametrize("case", make_golden.ROPE_CASES, ids=[c[0] for c in make_golden.ROPE_CASES])
+def test_rope_restatement_reproduces_reference_vectors(case):
+    name, n, heads, hd, pos0, base, neox, l3 = case
+    i = int(GOLD[f"rope/{name}/params"][0])
+    x = make_golden.rope_input(i, n, heads, hd)
+    assert np.array_equal(GOLD[f"rope/{name}/input_sha256"], sha(x)), "input generator drifted"
+    ff = synth.llama3_freq_factors(hd, base) if l3 else None
+    if ff is not None:
+        assert bits_equal(ff, GOLD[f"rope/{name}/freq_factors"])
+    assert matches_gold(f"rope/{name}/out", oracle.rope(x.copy(), pos0, base, neox, ff))
+
+
+def test_reference_known_answer_in_vectors():
+    # test_ref_ops.cpp:73-81, as evaluated by the reference: out row 1 = softmax([0, 1/sqrt 2]) . v
+    y = GOLD["kat/attention_2tok/out"].reshape(2, 2)
+    e = math.exp(1 / math.sqrt(2))
+    np.testing.assert_allclose(y, [[1, 0], [1 / (1 + e), e / (1 + e)]], rtol=1e-6, atol=1e-7)
+
+
+# ---------------------------------------------------------------- the compiled reference on fresh shapes
+
+@pytest.mark.skipif(not oracle.have_ref(), reason="oracle/_ref not built (needs the reference tree at build time)")
+@pytest.mark.parametrize("seed", range(6))
+def test_restatement_bit_exact_vs_compiled_reference(seed):
+    rng = np.random.default_rng(seed)
+    for _ in range(4):
+        KV = int(rng.integers(1, 5))
+        H = KV * int(rng.integers(1, 8))
+        D = int(rng.choice([2, 8, 13, 16, 24, 64, 128]))
+        n = int(rng.integers(1, 9))
+        pos0 = int(rng.integers(0, 200))
+        q = rng.standard_normal((n, H, D)).astype(np.float32) * np.float32(rng.choice([1, 5, 30]))
+        k = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+        v = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+        assert bits_equal(oracle.attention_scalar(q, k, v, pos0, KV), oracle.ref_attention_scalar(q, k, v, pos0, KV))
+        if oracle.have_avx2():
+            assert bits_equal(oracle.attention_avx2(q, k, v, pos0, KV), oracle.ref_attention_simd(q, k, v, pos0, KV))
+        base = float(rng.choice([1e4, 5e5, 1e6]))
+        neox = bool(rng.integers(0, 2))
+        ff = (rng.uniform(1, 8, D // 2).astype(np.float32) if D % 2 == 0 and rng.integers(0, 2) else None)
+        if D % 2 == 0:
+            p0 = int(rng.integers(0, 140000))
+            x = rng.standard_normal((n, H, D)).astype(np.float32)
+            assert bits_equal(oracle.rope(x.copy(), p0, base, neox, ff), oracle.ref_rope(x.copy(), p0, base, neox, ff))
+
+
+# ---------------------------------------------------------------- the reference's known-answer tests
+
+def rel(a, b):
+    return abs(a - b) <= 1e-6 * abs(b) + 1e-7
+
+
+def test_kat_rope():  # test_ref_ops.cpp:41-70
+    c1, s1, c2, s2 = math.cos(1.0), math.sin(1.0), math.cos(0.01), math.sin(0.01)
+    x = np.array([[[1, 0, 1, 0]]], np.float32)
+    y = oracle.rope(x.copy(), 1, 10000.0, False)[0, 0]
+    assert rel(y[0], c1) and rel(y[1], s1) and rel(y[2], c2) and rel(y[3], s2)
+    y = oracle.rope(x.copy(), 1, 10000.0, True)[0, 0]
+    assert rel(y[0], c1 - s1) and rel(y[1], 0) and rel(y[2], s1 + c1) and rel(y[3], 0)
+    y = oracle.rope(x.copy(), 0, 10000.0, False)[0, 0]
+    assert list(y) == [1, 0, 1, 0]
+    y = oracle.rope(x.copy(), 1, 10000.0, False, np.array([1, 2], np.float32))[0, 0]
+    assert rel(y[2], math.cos(0.005)) and rel(y[3], math.sin(0.005))
+
+
+def test_kat_attention_two_tokens():  # test_ref_ops.cpp:73-81
+    qkv = np.array([[[1, 0]], [[0, 1]]], np.float32)
+    out = oracle.attention_scalar(qkv, qkv, qkv, 0, 1).reshape(2, 2)
+    e = math.exp(1 / math.sqrt(2))
+    assert rel(out[0, 0], 1) and rel(out[0, 1], 0)
+    assert rel(out[1, 0], 1 / (1 + e)) and rel(out[1, 1], e / (1 + e))
+
+
+def test_kat_attention_gqa():  # test_ref_ops.cpp:84-95
+    H, KV, D, N = 4, 2, 2, 3
+    q = np.ones((1, H, D), np.float32)
+    k = np.zeros((N, KV, D), np.float32)
+    v = np.zeros((N, KV, D), np.float32)
+    for j in range(N):
+        for g in range(KV):
+            for d in range(D):
+                v[j, g, d] = 10 * g + j + d
+    for fn in (oracle.attention_scalar, oracle.attention_avx2, oracle.attention_f64):
+        out = fn(q, k, v, N - 1, KV)
+        if out is None:
+            continue
+        for h in range(H):
+            for d in range(D):
+                assert rel(float(out[0, h, d]), 10 * (h // 2) + 1 + d)
+
+
+def test_kat_softmax_overflow_safe():  # test_ref_ops.cpp:130-135
+    x = np.array([1000, 1000], np.float32)
+    oracle.softmax_inplace(x)
+    assert rel(x[0], 0.5) and rel(x[1], 0.5)
+
+
+@pytest.mark.skipif(not oracle.have_avx2(), reason="no AVX2 on this host")
+def test_exp_ps_error_bound():  # simd_helpers_test.cpp:92-137: <= 2e-7 relative over [-88, 88]
+    x = np.linspace(-88, 88, 1 << 20, dtype=np.float32)
+    y = oracle.exp_ps(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    assert np.max(np.abs(y - ref) / ref) <= 2e-7
+    edge = oracle.exp_ps(np.array([0, -np.inf, np.inf, 89.0, -104.5, np.nan, -90, 1e-30], np.float32))
+    assert edge[0] == 1 and edge[1] == 0 and np.isinf(edge[2]) and np.isinf(edge[3]) and edge[4] == 0
+    assert np.isnan(edge[5]) and 0 < edge[6] < 1e-38 and edge[7] == 1
+
+
+@pytest.mark.skipif(not oracle.have_avx2(), reason="no AVX2 on this host")
+def test_simd_matches_scalar_within_contract():  # test_ops.cpp:196-216
+    rng = np.random.default_rng(5)
+    for n, pos0, H, KV, D, qs in [(1, 0, 2, 1, 8, 1), (7, 3, 6, 2, 16, 1), (4, 300, 4, 2, 64, 1),
+                                  (3, 40, 2, 2, 13, 1), (2, 20, 4, 1, 128, 1), (5, 60, 4, 2, 64, 30)]:
+        q = (rng.uniform(-1, 1, (n, H, D)) * qs).astype(np.float32)
+        k = rng.uniform(-1, 1, (pos0 + n, KV, D)).astype(np.float32)
+        v = rng.uniform(-1, 1, (pos0 + n, KV, D)).astype(np.float32)
+        ref = oracle.attention_scalar(q, k, v, pos0, KV)
+        got = oracle.attention_avx2(q, k, v, pos0, KV)
+        assert np.max(np.abs(ref - got)) <= 2e-6 * qs
+
+
+# ---------------------------------------------------------------- mathematics
+
+def test_attention_matches_fp64_brute_force():
+    rng = np.random.default_rng(11)
+    for n, pos0, H, KV, D in [(1, 512, 14, 2, 64), (33, 0, 8, 2, 64), (5, 100, 4, 4, 128), (3, 7, 6, 3, 13)]:
+        q = rng.standard_normal((n, H, D)).astype(np.float32)
+        k = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+        v = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+        f = oracle.attention_f64(q, k, v, pos0, KV)
+        assert np.max(np.abs(oracle.attention_scalar(q, k, v, pos0, KV) - f)) < 2e-6
+        if oracle.have_avx2():
+            assert np.max(np.abs(oracle.attention_avx2(q, k, v, pos0, KV) - f)) < 2e-6
+
+
+def test_fp64_brute_force_known_answers():
+    # One key: output equals that key's value row. Identical keys: output is the mean of the value rows.
+    q = np.ones((1, 2, 4), np.float32)
+    v = np.arange(8, dtype=np.float32).reshape(1, 2, 4)
+    assert np.array_equal(oracle.attention_f64(q, v, v, 0, 2), v.astype(np.float64))
+    k = np.ones((5, 1, 4), np.float32)
+    v = np.arange(20, dtype=np.float32).reshape(5, 1, 4)
+    out = oracle.attention_f64(np.ones((1, 3, 4), np.float32), k, v, 4, 1)
+    np.testing.assert_allclose(out[0], np.tile(v[:, 0].mean(0), (3, 1)), rtol=1e-15)
+
+
+def test_rope_matches_closed_form_rotation():
+    rng = np.random.default_rng(3)
+    for neox in (False, True):
+        for pos0 in (0, 5, 8191, 40000):
+            x = rng.standard_normal((2, 3, 16)).astype(np.float32)
+            y = oracle.rope(x.copy(), pos0, 5e5, neox)
+            i = np.arange(8)
+            for t in range(2):
+                th = (pos0 + t) * 5e5 ** (-2.0 * i / 16)
+                a_idx, b_idx = (i, i + 8) if neox else (2 * i, 2 * i + 1)
+                a, b = x[t][:, a_idx].astype(np.float64), x[t][:, b_idx].astype(np.float64)
+                np.testing.assert_allclose(y[t][:, a_idx], a * np.cos(th) - b * np.sin(th), atol=2e-6)
+                np.testing.assert_allclose(y[t][:, b_idx], a * np.sin(th) + b * np.cos(th), atol=2e-6)
+
+
+def test_llama3_factor_properties():
+    for base, hd in [(5e5, 64), (5e5, 128), (1e4, 64)]:
+        f = oracle.llama3_freq_factors(hd, base)
+        assert bits_equal(f, synth.llama3_freq_factors(hd, base))
+        i = np.arange(hd // 2)
+        wl = 2 * np.pi / base ** (-2.0 * i / hd)
+        assert np.all(f[wl < 8192 / 4] == 1) and np.all(f[wl > 8192] == 32)
+        assert np.all(np.diff(f) >= 0) and f.min() >= 1 and f.max() <= 32
+    # continuity at both band edges: s = 1 gives 1, s = 0 gives `factor`
+    s1 = 1.0 / ((1 - 1.0) / 32 + 1.0)
+    s0 = 1.0 / ((1 - 0.0) / 32 + 0.0)
+    assert s1 == 1 and s0 == 32
+
+
+# ---------------------------------------------------------------- planted mistakes must be caught
+
+def _np_rope(x, pos0, base, neox, sign=1.0, swap=False):
+    """numpy copy of the oracle's rope with optional planted mistakes (sign of sin, pairing)."""
+    y = x.copy()
+    n, h, hd = x.shape
+    half = hd // 2
+    i = np.arange(half)
+    for t in range(n):
+        th = (pos0 + t) * np.power(float(base), -2.0 * i / hd)
+        c, s = np.cos(th).astype(np.float32), (sign * np.sin(th)).astype(np.float32)
+        use_neox = (not neox) if swap else neox
+        a_idx, b_idx = (i, i + half) if use_neox else (2 * i, 2 * i + 1)
+        a, b = x[t][:, a_idx], x[t][:, b_idx]
+        y[t][:, a_idx] = a * c - b * s
+        y[t][:, b_idx] = a * s + b * c
+    return y
+
+
+def test_pins_reject_planted_rope_mistakes():
+    name, n, heads, hd, pos0, base, neox, l3 = make_golden.ROPE_CASES[0]
+    x = make_golden.rope_input(0, n, heads, hd)
+    good = _np_rope(x, pos0, base, neox)
+    assert bits_equal(good, oracle.rope(x.copy(), pos0, base, neox))  # the numpy copy is faithful
+    assert matches_gold(f"rope/{name}/out", good)
+    assert not matches_gold(f"rope/{name}/out", _np_rope(x, pos0, base, neox, sign=-1.0))
+    assert not matches_gold(f"rope/{name}/out", _np_rope(x, pos0, base, neox, swap=True))
+    assert not matches_gold(f"rope/{name}/out", _np_rope(x, pos0 + 1, base, neox))
+
+
+def test_pins_reject_planted_attention_mistakes():
+    name, n, pos0, H, KV, D, qs = make_golden.ATTN_CASES[7]  # config 1 shape
+    q, k, v = make_golden.attn_inputs(7, n, pos0, H, KV, D, qs)
+    key = f"attn/{name}/scalar"
+    assert matches_gold(key, oracle.attention_scalar(q, k, v, pos0, KV))
+    # wrong GQA mapping (h % KV instead of h // group)
+    q_wrong = q.reshape(n, KV, H // KV, D).transpose(0, 2, 1, 3).reshape(n, H, D).copy()
+    assert not matches_gold(key, oracle.attention_scalar(q_wrong, k, v, pos0, KV))
+    # off-by-one causal window (attends one row short)
+    assert not matches_gold(key, oracle.attention_scalar(q, k[:-1], v[:-1], pos0 - 1, KV))
+    # missing 1/sqrt(d) scale
+    assert not matches_gold(key, oracle.attention_scalar(q * np.float32(8.0), k, v, pos0, KV))
+    # K and V swapped
+    assert not matches_gold(key, oracle.attention_scalar(q, v, k, pos0, KV))
+    # and the tolerance checks would catch them too (differences far above 1e-3)
+    assert np.max(np.abs(oracle.attention_scalar(q, v, k, pos0, KV) - oracle.attention_scalar(q, k, v, pos0, KV))) > 1e-2
