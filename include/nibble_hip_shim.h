@@ -72,6 +72,9 @@ int nbhs_append_rope_f32(float* q, float* cache_k, float* cache_v, const float* 
  * arguments, which returns the partial count the launcher will use. */
 int64_t nbhs_attn_decode_workspace(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
                                    int cu_count);
+/* Upper bound of nbhs_attn_decode_workspace over every call shape with n_heads query heads (any context length,
+ * row count, KV-head count and head_dim), for sizing the workspace once. */
+int64_t nbhs_attn_decode_workspace_bound(int64_t n_heads, int cu_count);
 int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
                          int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float* workspace,
                          int64_t workspace_floats, int cu_count, nbhs_stream s);

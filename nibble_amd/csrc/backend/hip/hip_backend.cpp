@@ -84,11 +84,9 @@ void HipBackend::reserve(const ReserveParams& rp) {
   if (rp.n_ctx < 0 || rp.n_heads < 0 || rp.max_rows < 0 || rp.max_width < 0)
     throw Error("reserve: negative size (n_ctx=" + str(rp.n_ctx) + " n_heads=" + str(rp.n_heads) + ")");
   reserved_ = rp;
-  // Decode partials: the split plan never exceeds ~4 workgroups per CU in total, each holding up to
-  // (head_dim + 2) floats per query head (head_dim <= 128 on the tiled path); multi-row calls split fewer ways.
-  const int64_t chunks = std::max<int64_t>(1, std::min<int64_t>((rp.n_ctx + 63) / 64, int64_t(cu_count_) * 4 + 16));
-  int64_t floats;
-  if (overflow_mul(rp.n_heads, chunks * 130, &floats)) throw Error("reserve: decode workspace size overflows");
+  // Decode partials, sized for the worst split the decode kernel plans for this many query heads.
+  const int64_t floats = nbhs_attn_decode_workspace_bound(std::max<int64_t>(rp.n_heads, 1), cu_count_);
+  if (floats < 0) throw Error("reserve: invalid n_heads " + str(rp.n_heads));
   ensure(decode_ws_, decode_ws_bytes_, size_t(floats) * sizeof(float));
 }
 

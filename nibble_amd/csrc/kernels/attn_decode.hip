@@ -1,14 +1,21 @@
 // fp32 causal GQA attention for few query rows (decode): Backend::attention (backend.h:68-69) with the semantics
 // of ref_ops.cpp:188-214 - row t attends to cache rows 0..pos0+t, query head h reads KV head h / (H/KV).
 //
-// Design (CDNA4, wave64, HBM-bound: arithmetic intensity H/(2*KV) FLOP/B, far below the fp32 ridge):
-//  * Grid = (context chunk, KV head x head subgroup, query row). A workgroup streams one chunk of one KV head
-//    and serves every query head of its GQA group from registers, so each K/V byte is read from HBM once per
+// Design (CDNA4, wave64; HBM-bound: arithmetic intensity H/(2*KV) FLOP/B, far below the fp32 ridge). Measured on
+// MI355X: a pure read of this access pattern streams at ~6 TB/s; what separates the kernel from that is VALU work
+// per byte, so the loop is built to spend as few instructions per K/V byte as possible.
+//  * Grid = (context chunk, KV head x head subgroup, query row). A workgroup streams one contiguous chunk of one
+//    KV head and serves every query head of its GQA group from registers: each K/V byte is read from HBM once per
 //    step, not once per query head.
-//  * A 64-float K/V row is 16 lanes x float4 (256 B, one coalesced segment); a wave covers 4 rows per load and
-//    keeps 4 loads of K and 4 of V in flight per lane. Dot products reduce over the 16 lanes with DPP (no LDS).
-//  * Online softmax in the log2 domain per lane (queries pre-scaled by log2(e)/sqrt(d)), merged across the
-//    wave's row groups with shuffles and across the workgroup's waves through LDS.
+//  * A 64-float K/V row is 8 lanes x 2 float4 (lane dl holds float4 columns dl and dl + 8, so each load
+//    instruction reads whole contiguous 128-byte halves of 8 rows); a wave covers 8 rows per load pair
+//    and keeps NBH_DECODE_UNROLL such row slots of K and of V in flight per lane, software-pipelined one iteration
+//    ahead, with non-temporal (streaming) loads. Dot products reduce over the 8 lanes with 3 DPP steps.
+//  * Online softmax in the log2 domain (queries pre-scaled by log2(e)/sqrt(d)) with raw v_exp_f32 and one running
+//    max per wave and query head, raised only when some score exceeds it by more than kLazy (log2 units) - a rare,
+//    wave-uniform branch - so unnormalised weights stay <= 2^kLazy and the wave's 8 row groups share one scale: at
+//    the end they are combined by plain sums (DPP), and only the workgroup's 4 waves need exp-weighted merges.
+//  * Row validity is only tested in a chunk's last, partial iteration.
 //  * Each workgroup writes an unnormalised partial (max, sum, weighted V) per query head; attn_decode_combine
 //    merges the chunks with a log-sum-exp reduction. With a single chunk the partial kernel writes the output.
 #include <hip/hip_runtime.h>
@@ -22,42 +29,82 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kDecodeThreads = 256;  // 4 waves
-constexpr int kUnroll = 4;           // row loads in flight per lane per tensor
-constexpr int kMaxChunks = 4096;     // partials per (row, head); bounds the combine kernel's LDS table
+// Row slots in flight per lane per tensor, and the split target in workgroups per CU. Compile-time so that tuning
+// sweeps can build variants; the defaults are the measured best on MI355X.
+#ifndef NBH_DECODE_UNROLL
+#define NBH_DECODE_UNROLL 1
+#endif
+#ifndef NBH_DECODE_WG_PER_CU
+#define NBH_DECODE_WG_PER_CU 2
+#endif
+// Software pipelining: the next iteration's K/V loads are issued before the current iteration is computed.
+#ifndef NBH_DECODE_PIPELINE
+#define NBH_DECODE_PIPELINE 0
+#endif
+// K/V rows are read exactly once per step: stream them past the caches (non-temporal loads) unless disabled.
+#ifndef NBH_DECODE_NT
+#define NBH_DECODE_NT 1
+#endif
+constexpr int kUnroll = NBH_DECODE_UNROLL;
+constexpr int kMaxChunks = 4096;  // partials per (row, head); bounds the combine kernel's LDS table
+constexpr float kLazy = 8.0f;     // allowed growth of scores over the running max before a rescale
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
 }
 
-// Sum over each aligned group of LPR lanes (16 or 32); every lane of the group gets the bit-identical sum
+// Sum over each aligned group of LPR lanes (8 or 16); every lane of the group gets the bit-identical sum
 // (each step adds a lane's value to its partner's, and a + b == b + a).
 template <int LPR>
 __device__ __forceinline__ float group_sum(float x) {
   x += dpp<0xB1>(x);   // quad_perm(1,0,3,2): lane ^ 1
   x += dpp<0x4E>(x);   // quad_perm(2,3,0,1): lane ^ 2
   x += dpp<0x141>(x);  // row_half_mirror: lane i <-> 7 - i within 8 (joins the two quads)
-  x += dpp<0x140>(x);  // row_mirror: lane i <-> 15 - i within 16 (joins the two halves)
-  if constexpr (LPR == 32) x += __shfl_xor(x, 16, 64);
+  if constexpr (LPR == 16) x += dpp<0x140>(x);  // row_mirror: lane i <-> 15 - i within 16
   return x;
 }
 
-// Merge (m, l, o) online-softmax states: the result describes the union of the rows both covered.
-__device__ __forceinline__ void merge_state(float& m, float& l, float4& o, float mo, float lo, float4 oo) {
-  const float mn = fmaxf(m, mo);
-  const float ms = mn == -INFINITY ? 0.0f : mn;
-  const float a = exp2f(m - ms), b = exp2f(mo - ms);
-  l = l * a + lo * b;
-  o.x = o.x * a + oo.x * b;
-  o.y = o.y * a + oo.y * b;
-  o.z = o.z * a + oo.z * b;
-  o.w = o.w * a + oo.w * b;
-  m = mn;
+// Sum of the values held by lanes l, l + LPR, l + 2 LPR, ... (the wave's row groups), in every lane.
+template <int LPR>
+__device__ __forceinline__ float row_group_sum(float x) {
+  if constexpr (LPR == 8) x += dpp<0x128>(x);  // row_ror:8 within 16 lanes: lane ^ 8
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
 }
 
-__device__ __forceinline__ float4 shfl_xor4(float4 v, int mask) {
-  return make_float4(__shfl_xor(v.x, mask, 64), __shfl_xor(v.y, mask, 64), __shfl_xor(v.z, mask, 64),
-                     __shfl_xor(v.w, mask, 64));
+__device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }  // v_exp_f32; -inf -> 0
+
+// One 16-byte K/V load.
+__device__ __forceinline__ f32x4 load4(const float* p) {
+#if NBH_DECODE_NT
+  return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+#else
+  return *reinterpret_cast<const f32x4*>(p);
+#endif
+}
+
+// Online-softmax state of one query head over some rows, as held by one lane: running max m (log2 domain), sum of
+// weights l, weighted V slice o (VPL float4 of the lane's dimensions).
+template <int VPL>
+struct State {
+  float m, l;
+  f32x4 o[VPL];
+};
+
+// Merges state b into a: the result covers the rows of both.
+template <int VPL>
+__device__ __forceinline__ void merge(State<VPL>& a, float bm, float bl, const f32x4* bo) {
+  const float mn = fmaxf(a.m, bm);
+  const float ms = mn == -INFINITY ? 0.0f : mn;
+  const float wa = exp2_raw(a.m - ms), wb = exp2_raw(bm - ms);
+  a.l = a.l * wa + bl * wb;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) a.o[i] = a.o[i] * wa + bo[i] * wb;
+  a.m = mn;
 }
 
 // HD: head_dim (64 or 128). GB: query heads per workgroup (the GQA group, or a slice of it).
@@ -65,13 +112,15 @@ template <int HD, int GB>
 __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ out,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, int64_t pos0, int n_heads, int n_kv, int group, int n_sub,
-    int64_t chunk_len, int n_chunks, float qscale) {
-  constexpr int LPR = HD / 4;                      // lanes per K/V row
-  constexpr int RPS = 64 / LPR;                    // rows per wave load
-  constexpr int WAVE_ROWS = RPS * kUnroll;         // rows per wave iteration
-  constexpr int NW = kDecodeThreads / 64;          // waves per workgroup
+    int n_chunks, int64_t groups_per_chunk, float qscale) {
+  constexpr int VPL = 2;                            // float4 per lane per row
+  constexpr int LPR = HD / (4 * VPL);               // lanes per K/V row: 8 (hd 64) or 16 (hd 128)
+  constexpr int RPS = 64 / LPR;                     // rows per wave load
+  constexpr int WAVE_ROWS = RPS * kUnroll;          // rows per wave iteration
+  constexpr int NW = kDecodeThreads / 64;           // waves per workgroup
+  constexpr int64_t kStep = NW * WAVE_ROWS;         // rows the workgroup covers per iteration
   __shared__ float sm_m[NW][GB], sm_l[NW][GB];
-  __shared__ float4 sm_o[NW][GB][LPR];
+  __shared__ f32x4 sm_o[NW][GB][LPR * VPL];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / LPR, dl = lane % LPR;
@@ -81,144 +130,236 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
   const int h0 = g * group + sg * GB;
   const int gcount = min(GB, group - sg * GB);
   const int64_t len = pos0 + t + 1;
-  const int64_t c0 = int64_t(chunk) * chunk_len;
-  const int64_t c1 = min(c0 + chunk_len, len);
-
-  float4 qv[GB];
-  float m[GB], l[GB];
-  float4 o[GB];
-#pragma unroll
-  for (int h = 0; h < GB; ++h) {
-    qv[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (h < gcount) {
-      const float4 x = *reinterpret_cast<const float4*>(q + (t * n_heads + h0 + h) * HD + 4 * dl);
-      qv[h] = make_float4(x.x * qscale, x.y * qscale, x.z * qscale, x.w * qscale);
-    }
-    m[h] = -INFINITY;
-    l[h] = 0.f;
-    o[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  // The chunk: row groups [g0, g1) of kStep consecutive rows each, clipped to this row's causal length.
+  const int64_t n_groups = (len + kStep - 1) / kStep;
+  const int64_t g0 = int64_t(chunk) * groups_per_chunk;
+  const int64_t g1 = min(g0 + groups_per_chunk, n_groups);
 
   const int64_t row_stride = int64_t(n_kv) * HD;
-  const float* kb = k + int64_t(g) * HD + 4 * dl;
+  const float* kb = k + int64_t(g) * HD + 4 * dl;  // float4 column dl + LPR * i of the row
   const float* vb = v + int64_t(g) * HD + 4 * dl;
-  for (int64_t base = c0 + wave * WAVE_ROWS; base < c1; base += NW * WAVE_ROWS) {
-    float4 kr[kUnroll], vr[kUnroll];
-    bool valid[kUnroll];
+
+  // One iteration's rows: kUnroll row slots, VPL float4 of K and of V each. Rows past the causal window are
+  // clamped to the last valid row (never read out of range) and masked in the partial iteration.
+  struct Rows {
+    f32x4 k[kUnroll][VPL], v[kUnroll][VPL];
+  };
+  auto row_of = [&](int64_t grp, int u) { return grp * kStep + wave * WAVE_ROWS + u * RPS + sub; };
+  auto load = [&](int64_t grp, Rows& r) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int64_t j = base + u * RPS + sub;
-      valid[u] = j < c1;
-      const int64_t jj = valid[u] ? j : c0;  // rows past the chunk are never read: clamp to a valid row
-      kr[u] = *reinterpret_cast<const float4*>(kb + jj * row_stride);
-      vr[u] = *reinterpret_cast<const float4*>(vb + jj * row_stride);
+      const int64_t j = min(row_of(grp, u), len - 1);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        r.k[u][i] = load4(kb + j * row_stride + 4 * LPR * i);
+        r.v[u][i] = load4(vb + j * row_stride + 4 * LPR * i);
+      }
     }
+  };
+
+  // The first K/V loads go out before the query loads, so the first HBM round trip is not spent on q alone.
+  int64_t grp = g0;
+  Rows ra, rb;
+  if (grp < g1) load(grp, ra);
+
+  f32x4 qv[GB][VPL];
+  State<VPL> st[GB];
+#pragma unroll
+  for (int h = 0; h < GB; ++h) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      qv[h][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      st[h].o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (h < gcount)
+        qv[h][i] = *reinterpret_cast<const f32x4*>(q + (t * n_heads + h0 + h) * HD + 4 * (dl + LPR * i)) * qscale;
+    }
+    st[h].m = -INFINITY;
+    st[h].l = 0.f;
+  }
+
+  auto compute = [&](const Rows& r, int64_t grp_idx) {
+    // Wave-uniform: does this iteration reach past the causal window?
+    const bool partial = grp_idx * kStep + wave * WAVE_ROWS + WAVE_ROWS > len;
 #pragma unroll
     for (int h = 0; h < GB; ++h) {
       if (h >= gcount) continue;
-      float s[kUnroll];
+      float sc[kUnroll];
       float mloc = -INFINITY;
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        float d = qv[h].x * kr[u].x;
-        d = fmaf(qv[h].y, kr[u].y, d);
-        d = fmaf(qv[h].z, kr[u].z, d);
-        d = fmaf(qv[h].w, kr[u].w, d);
+        f32x4 prod = qv[h][0] * r.k[u][0];
+#pragma unroll
+        for (int i = 1; i < VPL; ++i) prod += qv[h][i] * r.k[u][i];
+        float d = (prod[0] + prod[1]) + (prod[2] + prod[3]);
         d = group_sum<LPR>(d);
-        s[u] = valid[u] ? d : -INFINITY;
-        mloc = fmaxf(mloc, s[u]);
+        if (partial && row_of(grp_idx, u) >= len) d = -INFINITY;
+        sc[u] = d;
+        mloc = fmaxf(mloc, d);
       }
-      const float mn = fmaxf(m[h], mloc);
-      const float ms = mn == -INFINITY ? 0.0f : mn;
-      const float corr = exp2f(m[h] - ms);
-      float lh = l[h] * corr;
-      float4 oh = make_float4(o[h].x * corr, o[h].y * corr, o[h].z * corr, o[h].w * corr);
+      // The wave's reference max (identical in every lane) is raised only when some score outgrew it by more
+      // than kLazy; the first iteration always sets it (m = -inf).
+      if (__builtin_amdgcn_ballot_w64(mloc > st[h].m + kLazy)) {
+#pragma unroll
+        for (int mask = LPR; mask < 64; mask <<= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, mask, 64));
+        const float mn = fmaxf(st[h].m, mloc);
+        const float corr = exp2_raw(st[h].m - (mn == -INFINITY ? 0.0f : mn));
+        st[h].l *= corr;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) st[h].o[i] *= corr;
+        st[h].m = mn;
+      }
+      const float ms = st[h].m == -INFINITY ? 0.0f : st[h].m;
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        const float p = exp2f(s[u] - ms);
-        lh += p;
-        oh.x = fmaf(p, vr[u].x, oh.x);
-        oh.y = fmaf(p, vr[u].y, oh.y);
-        oh.z = fmaf(p, vr[u].z, oh.z);
-        oh.w = fmaf(p, vr[u].w, oh.w);
+        const float p = exp2_raw(sc[u] - ms);
+        st[h].l += p;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) st[h].o[i] += p * r.v[u][i];
       }
-      m[h] = mn;
-      l[h] = lh;
-      o[h] = oh;
     }
-  }
+  };
 
-  // Merge the wave's row groups (lanes dl, dl + LPR, ...), then the waves through LDS.
+#if NBH_DECODE_PIPELINE
+  while (grp < g1) {
+    const int64_t next = grp + 1;
+    if (next < g1) load(next, rb);
+    compute(ra, grp);
+    if (next >= g1) break;
+    grp = next + 1;
+    if (grp < g1) load(grp, ra);
+    compute(rb, next);
+  }
+#else
+  while (grp < g1) {
+    compute(ra, grp);
+    ++grp;
+    if (grp < g1) load(grp, ra);
+  }
+#endif
+
+  // The wave's row groups (lanes dl, dl + LPR, ...) share the wave's max: sum them, then merge the waves
+  // through LDS.
 #pragma unroll
   for (int h = 0; h < GB; ++h) {
+    st[h].l = row_group_sum<LPR>(st[h].l);
 #pragma unroll
-    for (int mask = LPR; mask < 64; mask <<= 1) {
-      const float mo = __shfl_xor(m[h], mask, 64), lo = __shfl_xor(l[h], mask, 64);
-      const float4 oo = shfl_xor4(o[h], mask);
-      merge_state(m[h], l[h], o[h], mo, lo, oo);
-    }
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) st[h].o[i][c] = row_group_sum<LPR>(st[h].o[i][c]);
     if (lane < LPR) {
-      sm_o[wave][h][dl] = o[h];
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) sm_o[wave][h][dl + LPR * i] = st[h].o[i];
       if (lane == 0) {
-        sm_m[wave][h] = m[h];
-        sm_l[wave][h] = l[h];
+        sm_m[wave][h] = st[h].m;
+        sm_l[wave][h] = st[h].l;
       }
     }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < GB * LPR; idx += kDecodeThreads) {
-    const int h = idx / LPR, d4 = idx % LPR;
+  constexpr int V4 = HD / 4;  // float4 columns of a head row
+  for (int idx = threadIdx.x; idx < GB * V4; idx += kDecodeThreads) {
+    const int h = idx / V4, c4 = idx % V4;
     if (h >= gcount) continue;
-    float mm = sm_m[0][h], ll = sm_l[0][h];
-    float4 oo = sm_o[0][h][d4];
+    State<1> acc;
+    acc.m = sm_m[0][h];
+    acc.l = sm_l[0][h];
+    acc.o[0] = sm_o[0][h][c4];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) merge_state(mm, ll, oo, sm_m[w][h], sm_l[w][h], sm_o[w][h][d4]);
+    for (int w = 1; w < NW; ++w) merge<1>(acc, sm_m[w][h], sm_l[w][h], &sm_o[w][h][c4]);
     const int64_t head = h0 + h;
     if (n_chunks == 1) {
-      const float inv = 1.0f / ll;
-      *reinterpret_cast<float4*>(out + (t * n_heads + head) * HD + 4 * d4) =
-          make_float4(oo.x * inv, oo.y * inv, oo.z * inv, oo.w * inv);
+      reinterpret_cast<f32x4*>(out + (t * n_heads + head) * HD)[c4] = acc.o[0] * (1.0f / acc.l);
     } else {
       const int64_t slot = (t * n_heads + head) * n_chunks + chunk;
-      *reinterpret_cast<float4*>(ws_o + slot * HD + 4 * d4) = oo;
-      if (d4 == 0) {
-        ws_ml[2 * slot] = mm;
-        ws_ml[2 * slot + 1] = ll;
+      reinterpret_cast<f32x4*>(ws_o + slot * HD)[c4] = acc.o[0];
+      if (c4 == 0) {
+        ws_ml[2 * slot] = acc.m;
+        ws_ml[2 * slot + 1] = acc.l;
       }
     }
   }
 }
 
-// Log-sum-exp merge of the chunk partials: one wave per (row, head).
+// Block-wide reduction of one float per thread (kDecodeThreads threads); every thread gets the result.
+template <bool MAX>
+__device__ __forceinline__ float block_reduce(float x, float* scratch) {
+#pragma unroll
+  for (int mask = 1; mask < 64; mask <<= 1) {
+    const float y = __shfl_xor(x, mask, 64);
+    x = MAX ? fmaxf(x, y) : x + y;
+  }
+  __syncthreads();  // scratch may still be read from a previous reduction
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = x;
+  __syncthreads();
+  float r = scratch[0];
+#pragma unroll
+  for (int w = 1; w < kDecodeThreads / 64; ++w) r = MAX ? fmaxf(r, scratch[w]) : r + scratch[w];
+  return r;
+}
+
+// Log-sum-exp merge of the chunk partials of one (row, head) per workgroup. Thread (chunk group cg, float4 column
+// c4) loads the max, sum and partial-output column of its chunks cg, cg + CG, ... all at once (one memory round
+// trip for up to kPer chunks each), the global max comes from a block reduction, and the weighted sums of the
+// chunk groups are added through LDS.
 template <int HD>
-__global__ __launch_bounds__(64) void attn_decode_combine(const float* __restrict__ ws_o,
-                                                          const float* __restrict__ ws_ml, float* __restrict__ out,
-                                                          int n_chunks) {
-  __shared__ float w[kMaxChunks];
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(kDecodeThreads) void attn_decode_combine(const float* __restrict__ ws_o,
+                                                                      const float* __restrict__ ws_ml,
+                                                                      float* __restrict__ out, int n_chunks) {
+  constexpr int V4 = HD / 4;                // float4 columns of one head row
+  constexpr int CG = kDecodeThreads / V4;   // chunk groups
+  constexpr int kPer = 16;                  // chunks per thread held in registers
+  __shared__ float red[kDecodeThreads / 64];
+  __shared__ f32x4 acc_s[CG][V4];
+  __shared__ float l_s[CG];
+  const int tid = threadIdx.x;
+  const int cg = tid / V4, c4 = tid % V4;
   const int64_t rh = blockIdx.x;  // t * n_heads + head
   const float* ml = ws_ml + rh * n_chunks * 2;
+  const f32x4* po = reinterpret_cast<const f32x4*>(ws_o + rh * n_chunks * HD) + c4;
+  float mv[kPer], lv[kPer];
+  f32x4 ov[kPer];
   float mx = -INFINITY;
-  for (int c = lane; c < n_chunks; c += 64) mx = fmaxf(mx, ml[2 * c]);
 #pragma unroll
-  for (int mask = 1; mask < 64; mask <<= 1) mx = fmaxf(mx, __shfl_xor(mx, mask, 64));
+  for (int i = 0; i < kPer; ++i) {
+    const int c = cg + i * CG;
+    mv[i] = -INFINITY;
+    lv[i] = 0.f;
+    ov[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (c < n_chunks) {
+      mv[i] = ml[2 * c];
+      lv[i] = ml[2 * c + 1];
+      ov[i] = po[int64_t(c) * V4];
+    }
+    mx = fmaxf(mx, mv[i]);
+  }
+  for (int c = cg + kPer * CG; c < n_chunks; c += CG) mx = fmaxf(mx, ml[2 * c]);  // beyond the register window
+  mx = block_reduce<true>(mx, red);
   const float ms = mx == -INFINITY ? 0.0f : mx;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
-  for (int c = lane; c < n_chunks; c += 64) {
-    const float wc = exp2f(ml[2 * c] - ms);
-    w[c] = wc;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const float wc = exp2_raw(mv[i] - ms);
+    acc += ov[i] * wc;
+    lsum += lv[i] * wc;
+  }
+  for (int c = cg + kPer * CG; c < n_chunks; c += CG) {
+    const float wc = exp2_raw(ml[2 * c] - ms);
+    acc += po[int64_t(c) * V4] * wc;
     lsum += ml[2 * c + 1] * wc;
   }
-#pragma unroll
-  for (int mask = 1; mask < 64; mask <<= 1) lsum += __shfl_xor(lsum, mask, 64);
+  acc_s[cg][c4] = acc;
+  if (c4 == 0) l_s[cg] = lsum;
   __syncthreads();
-  const float inv = 1.0f / lsum;
-  const float* po = ws_o + rh * n_chunks * HD;
+  if (tid < V4) {
+    f32x4 r = acc_s[0][tid];
+    float l = l_s[0];
 #pragma unroll
-  for (int d = lane; d < HD; d += 64) {
-    float acc = 0.f;
-    for (int c = 0; c < n_chunks; ++c) acc = fmaf(po[int64_t(c) * HD + d], w[c], acc);
-    out[rh * HD + d] = acc * inv;
+    for (int i = 1; i < CG; ++i) {
+      r += acc_s[i][tid];
+      l += l_s[i];
+    }
+    reinterpret_cast<f32x4*>(out + rh * HD)[tid] = r * (1.0f / l);
   }
 }
 
@@ -271,55 +412,85 @@ __global__ __launch_bounds__(64) void attn_generic(const float* __restrict__ q, 
 
 // Chunking plan shared by the workspace query and the launcher.
 struct Plan {
-  int gb;            // heads per workgroup (1, 2, 4 or 8)
-  int n_sub;         // head subgroups per KV head
-  int n_chunks;
-  int64_t chunk_len;
+  int gb;                     // query heads per workgroup (1, 2, 4 or 8)
+  int n_sub;                  // head subgroups per KV head
+  int n_chunks;               // chunks per (row, head subgroup); each writes one partial per query head
+  int64_t groups_per_chunk;   // row groups per chunk
 };
 
-Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int cu_count) {
+// Workgroups of attn_decode_partial<HD, GB> that fit on one CU at once (register and LDS limits), capped at
+// NBH_DECODE_WG_PER_CU; queried from the runtime once per instance.
+template <int HD, int GB>
+int resident_per_cu() {
+  static const int n = [] {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, attn_decode_partial<HD, GB>, kDecodeThreads, 0) !=
+            hipSuccess ||
+        b < 1)
+      b = 1;
+    return b < NBH_DECODE_WG_PER_CU ? b : NBH_DECODE_WG_PER_CU;
+  }();
+  return n;
+}
+
+int resident_per_cu(int64_t head_dim, int gb) {
+  if (head_dim == 64)
+    return gb == 1 ? resident_per_cu<64, 1>() : gb == 2 ? resident_per_cu<64, 2>()
+         : gb == 4 ? resident_per_cu<64, 4>() : resident_per_cu<64, 8>();
+  return gb == 1 ? resident_per_cu<128, 1>() : gb == 2 ? resident_per_cu<128, 2>()
+       : gb == 4 ? resident_per_cu<128, 4>() : resident_per_cu<128, 8>();
+}
+
+// As many workgroups as fit on the chip at once (one round, no tail of late starters). The row groups per chunk
+// are rounded to the nearest whole number and the chunk count derived from it, so the busiest chunk does that many
+// groups and no more: a context one row past a round size does not cost one workgroup an extra HBM round trip.
+Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t head_dim, int cu_count) {
   Plan p;
   const int64_t group = n_heads / n_kv;
   p.gb = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8;
   p.n_sub = int((group + p.gb - 1) / p.gb);
   const int64_t max_len = pos0 + n;
-  // Aim for ~4 workgroups per CU in total; chunks shorter than 64 rows do not pay for their partial.
-  const int64_t target = int64_t(cu_count > 0 ? cu_count : 256) * 4;
-  const int64_t per_chunk_groups = n * n_kv * p.n_sub;
-  int64_t chunks = (target + per_chunk_groups - 1) / per_chunk_groups;
-  const int64_t max_by_len = (max_len + 63) / 64;
-  if (chunks > max_by_len) chunks = max_by_len;
-  if (chunks < 1) chunks = 1;
-  if (chunks > kMaxChunks) chunks = kMaxChunks;
-  p.chunk_len = (max_len + chunks - 1) / chunks;
-  p.n_chunks = int((max_len + p.chunk_len - 1) / p.chunk_len);
+  const int64_t lpr = head_dim / 8;
+  const int64_t step = (64 / lpr) * kUnroll * (kDecodeThreads / 64);  // rows a workgroup covers per iteration
+  const int64_t units = (max_len + step - 1) / step;
+  int64_t slots = int64_t(cu_count > 0 ? cu_count : 256) * resident_per_cu(head_dim, p.gb) / (n * n_kv * p.n_sub);
+  if (slots < 1) slots = 1;
+  int64_t per = (units + slots / 2) / slots;
+  if (per < 1) per = 1;
+  int64_t chunks = (units + per - 1) / per;
+  if (chunks > kMaxChunks) {
+    per = (units + kMaxChunks - 1) / kMaxChunks;
+    chunks = (units + per - 1) / per;
+  }
+  p.n_chunks = int(chunks);
+  p.groups_per_chunk = per;
   return p;
 }
 
 template <int HD>
 int launch_decode(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0, int64_t H,
                   int64_t KV, float* ws, const Plan& p, float qscale, hipStream_t s) {
-  const dim3 grid(p.n_chunks, unsigned(KV * p.n_sub), unsigned(n));
   float* ws_o = ws;
   float* ws_ml = ws ? ws + n * H * p.n_chunks * HD : nullptr;
   const int group = int(H / KV);
+  const dim3 grid(p.n_chunks, unsigned(KV * p.n_sub), unsigned(n));
+  {
+    nbhs_timing::KernelTimer timer(NBHS_K_DECODE_PARTIAL, s);
 #define NBH_DECODE(GB)                                                                                              \
   attn_decode_partial<HD, GB><<<grid, kDecodeThreads, 0, s>>>(q, k, v, out, ws_o, ws_ml, pos0, int(H), int(KV), \
-                                                               group, p.n_sub, p.chunk_len, p.n_chunks, qscale)
-  {
-  nbhs_timing::KernelTimer timer(NBHS_K_DECODE_PARTIAL, s);
-  switch (p.gb) {
-    case 1: NBH_DECODE(1); break;
-    case 2: NBH_DECODE(2); break;
-    case 4: NBH_DECODE(4); break;
-    default: NBH_DECODE(8); break;
-  }
-  }
+                                                               group, p.n_sub, p.n_chunks, p.groups_per_chunk, qscale)
+    switch (p.gb) {
+      case 1: NBH_DECODE(1); break;
+      case 2: NBH_DECODE(2); break;
+      case 4: NBH_DECODE(4); break;
+      default: NBH_DECODE(8); break;
+    }
 #undef NBH_DECODE
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.n_chunks == 1) return e;
   nbhs_timing::KernelTimer timer(NBHS_K_DECODE_COMBINE, s);
-  attn_decode_combine<HD><<<unsigned(n * H), 64, 0, s>>>(ws_o, ws_ml, out, p.n_chunks);
+  attn_decode_combine<HD><<<unsigned(n * H), kDecodeThreads, 0, s>>>(ws_o, ws_ml, out, p.n_chunks);
   return hipGetLastError();
 }
 
@@ -333,9 +504,18 @@ int64_t nbhs_attn_decode_workspace(int64_t n, int64_t pos0, int64_t n_heads, int
                                    int cu_count) {
   if (n <= 0 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0) return -1;
   if (!tiled_head_dim(head_dim)) return 0;
-  const Plan p = make_plan(n, pos0, n_heads, n_kv_heads, cu_count);
+  const Plan p = make_plan(n, pos0, n_heads, n_kv_heads, head_dim, cu_count);
   if (p.n_chunks == 1) return 0;
   return n * n_heads * p.n_chunks * (head_dim + 2);
+}
+
+int64_t nbhs_attn_decode_workspace_bound(int64_t n_heads, int cu_count) {
+  // With T = the workgroup target, a call with n rows splits into chunks <= 1.5 * T / n + 1 (the nearest-whole
+  // rounding of the per-chunk work) whenever it splits at all (T / n >= 2), so n * chunks <= 2 * T; each partial
+  // holds at most 128 + 2 floats per query head.
+  if (n_heads <= 0) return -1;
+  const int64_t slots = int64_t(cu_count > 0 ? cu_count : 256) * NBH_DECODE_WG_PER_CU;
+  return n_heads * (2 * slots + 16) * (128 + 2);
 }
 
 int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
@@ -352,7 +532,7 @@ int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* 
                                                                      int(n_kv_heads), int(head_dim), qscale);
     return hipGetLastError();
   }
-  const Plan p = make_plan(n, pos0, n_heads, n_kv_heads, cu_count);
+  const Plan p = make_plan(n, pos0, n_heads, n_kv_heads, head_dim, cu_count);
   const int64_t need = p.n_chunks == 1 ? 0 : n * n_heads * p.n_chunks * (head_dim + 2);
   if (need > 0 && (!workspace || workspace_floats < need)) return NBHS_EINVAL;
   if (n_kv_heads * p.n_sub > 65535) return NBHS_EINVAL;
