@@ -3,8 +3,10 @@
 //
 // Numerics: Q is scaled by log2(e)/sqrt(d) and rounded to fp16, K and V come from fp16 copies of the fp32 cache
 // (stage_kv), QK^T and PV run on v_mfma_f32_32x32x16_f16 with fp32 accumulation, and the online softmax (max,
-// exp2, running sums, rescaling) is fp32. The host routes rows with fewer than 256 visible keys to the fp32
-// decode kernel, where fp16 rounding of a few V rows is not averaged away.
+// exp2, running sums, rescaling) is fp32 - the running max is raised lazily (only past a growth of kLazy), so the
+// O accumulators are rescaled in a rare wave-uniform branch and unnormalised weights stay <= 2^kLazy. The host
+// routes rows with fewer than 256 visible keys to the fp32 decode kernel, where fp16 rounding of a few V rows is
+// not averaged away.
 //
 // Layout (per wave, 32 query rows):
 //  * S^T = K Q^T: A = K tile rows from LDS ([key][d], 16 B per lane), B = the wave's Q fragment held in
@@ -31,6 +33,7 @@ namespace {
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBN = 64;          // keys per tile
@@ -38,6 +41,9 @@ constexpr int kRowsPerWave = 32;
 constexpr int kWaves = 4;
 constexpr int kRowsPerBlock = kRowsPerWave * kWaves;
 constexpr int kPad = 8;          // halves of LDS row padding (keeps rows 16-byte aligned, spreads banks)
+constexpr float kLazy = 8.0f;    // allowed growth of scores over the running max before the accumulators rescale
+
+__device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }  // v_exp_f32; -inf -> 0
 
 // ---- staging: fp32 cache rows -> fp16 K [KV][rows_pad][HD] and transposed V [KV][HD][rows_pad] ----
 template <int HD>
@@ -72,8 +78,15 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(const float* __restrict__
   }
 }
 
+// Occupancy cap (waves per SIMD) the register allocator plans for. The kernel is built with MFMA accumulators in
+// architectural VGPRs (-amdgpu-mfma-vgpr-form, see the Makefile), so the S^T and O^T accumulators both stay
+// resident with no per-tile copies through accumulation registers; head_dim 64 fits 3 waves per SIMD.
+#ifndef NBH_PREFILL_WAVES_PER_EU
+#define NBH_PREFILL_WAVES_PER_EU 3
+#endif
 template <int HD>
-__global__ __launch_bounds__(kWaves * 64) void attn_prefill_kernel(
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, NBH_PREFILL_WAVES_PER_EU)))
+void attn_prefill_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16,
     float* __restrict__ out, int64_t n, int64_t pos0, int n_heads, int n_kv, int group, int64_t rows_pad,
     int n_tiles, float qscale) {
@@ -172,26 +185,30 @@ __global__ __launch_bounds__(kWaves * 64) void attn_prefill_kernel(
     const int cur = kt & 1;
     if (kt + 1 < ntk) load_tile(kt + 1);
     if (wave_active && int64_t(kt) * kBN < wave_kend) {
+      // S^T for the tile's two 32-key halves; the two accumulator chains are interleaved so consecutive MFMAs do
+      // not wait on each other's results.
       floatx16 s[2];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
+      for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[kk][r] = 0.f;
 #pragma unroll
-        for (int c = 0; c < DC; ++c) {
+      for (int c = 0; c < DC; ++c)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
           const half8_t a = *reinterpret_cast<const half8_t*>(&ks[cur][kk * 32 + ql][16 * c + 8 * hf]);
           s[kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s[kk], 0, 0, 0);
         }
-      }
       // Causal mask (and inactive rows) only where some key of the tile lies past the wave's first row.
       if (int64_t(kt) * kBN + kBN > wave_kfull) {
+        // keys of this tile past the query's position (relative to the tile start; inactive rows mask all)
+        const int64_t rel64 = active ? qpos - int64_t(kt) * kBN : -1;
+        const int rel = int(rel64 < kBN ? rel64 : kBN);
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int64_t key = int64_t(kt) * kBN + kk * 32 + 8 * (r / 4) + 4 * hf + (r % 4);
-            if (!active || key > qpos) s[kk][r] = -INFINITY;
-          }
+          for (int r = 0; r < 16; ++r)
+            if (kk * 32 + 8 * (r / 4) + 4 * hf + (r % 4) > rel) s[kk][r] = -INFINITY;
       }
       float mt = -INFINITY;
 #pragma unroll
@@ -199,37 +216,42 @@ __global__ __launch_bounds__(kWaves * 64) void attn_prefill_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kk][r]);
       mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float m_new = fmaxf(m_run, mt);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float corr = exp2f(m_run - m_use);
-      float ls = 0.f;
+      // Lazy rescaling: the reference max moves only when some query's scores outgrew it by more than kLazy
+      // (wave-uniform branch, rare after the first tiles); weights then stay <= 2^kLazy, well inside fp16.
+      if (__builtin_amdgcn_ballot_w64(mt > m_run + kLazy)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float corr = exp2_raw(m_run - (m_new == -INFINITY ? 0.0f : m_new));
+        l_run *= corr;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          s[kk][r] = exp2f(s[kk][r] - m_use);
-          ls += s[kk][r];
-        }
-      l_run = l_run * corr + ls;
-      m_run = m_new;
+          for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
+        m_run = m_new;
+      }
+      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+      // P in fp16 (the MFMA B operand); the row sum is accumulated from the same fp16 values with v_dot2, so the
+      // normaliser matches the weights the MFMA actually multiplies.
+      half8_t pb[4];
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+      for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
-      // O^T += V^T P^T over 4 steps of 16 keys.
+        for (int e = 0; e < 8; ++e) pb[kc][e] = (_Float16)exp2_raw(s[kc >> 1][8 * (kc & 1) + e] - m_use);
+      const half2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+          l_run = __builtin_amdgcn_fdot2(half2_t{pb[kc][e], pb[kc][e + 1]}, ones, l_run, false);
+      // O^T += V^T P^T over 4 steps of 16 keys; the DT output tiles are independent chains.
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        const int kk = kc >> 1, ic = kc & 1;
-        half8_t pb;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pb[e] = (_Float16)s[kk][8 * ic + e];
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           const _Float16* vrow = &vs[cur][32 * dt + ql][16 * kc + 4 * hf];
           const half4_t lo = *reinterpret_cast<const half4_t*>(vrow);
           const half4_t hi = *reinterpret_cast<const half4_t*>(vrow + 8);
           const half8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, oacc[dt], 0, 0, 0);
+          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kc], oacc[dt], 0, 0, 0);
         }
       }
     }
