@@ -8,8 +8,11 @@ Workload (inputs resident in HBM before any timed region; synthetic N(0,1) data 
     all 16 layers (append with RoPE, then attention over 32769 + s rows). One "step" = one token through 16 layers.
 Printed: one JSON line. `value` = decode attention HBM GB/s (algorithmic bytes 8*KV*hd*L_ctx per layer-step over the
 timed wall time of the steps); `prefill` = prefill attention TFLOP/s (2*H*hd*n*(n+1) per layer). `roofline` is the
-decode kernel alone (algorithmic bytes per launch / its average event-timed duration), `prefill.roofline` the MFMA
-kernel alone. `cpu_baseline` is the reference's CpuBackend (compiled from its sources, oracle/_ref) on this host.
+decode partial kernel alone: algorithmic bytes per launch / its average duration, read from start/stop events that
+hipExtLaunchKernel stamps on each dispatch in a second pass over the same steps; `prefill.roofline` is the MFMA kernel
+alone. `traffic` = HBM bytes per launch from two `rocprofv3 --pmc` child runs (FETCH_SIZE, WRITE_SIZE) over
+`--probe`, scaled by what the counters read for a known-size copy. `cpu_baseline` is the reference's CpuBackend
+(compiled from its sources, oracle/_ref) timed on this host on bounded samples.
 """
 from __future__ import annotations
 
@@ -105,6 +108,110 @@ def cpu_baseline(be, shape, ck0, cv0, dq_dec, ctx, q_pre, budget_s):
     }
 
 
+COPY_CAL_BYTES = 1 << 30  # calibration copy for the HBM byte counters: 1 GiB read + 1 GiB written
+PROBE_DECODE_STEPS = 8
+
+
+def probe():
+    """Short run for one `rocprofv3 --pmc` pass: layer 0 of config 4 only. Dispatch order: fill kernels, then
+    PROBE_DECODE_STEPS decode steps at 32768+s ctx (append+rope, split-context partial, combine), then one
+    COPY_CAL_BYTES device copy (the calibration kernel of known size), then the 8192-row prefill (append+rope, fp16
+    staging, fp32 prefix rows, MFMA kernel). Counter values per dispatch do not depend on the data."""
+    shape = configs.LLAMA32_1B
+    H, KV, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
+    base, neox, ff = shape.rope_base, shape.neox, shape.freq_factors()
+    n_pre, ctx = 8192, 32768
+    cap, row = ctx + PROBE_DECODE_STEPS, KV * D
+    be = nibble_amd.HipBackend(0)
+    be.reserve(cap, H, n_pre, 8192)
+    be.reserve_attention(KV, D)
+    be.reserve_rope(D, base, neox, ff)
+    ck, cv = be.alloc(cap * row), be.alloc(cap * row)
+    be.fill_normal(ck, ctx * row, seed=1)
+    be.fill_normal(cv, ctx * row, seed=2)
+    qd, kd, vd = be.alloc(H * D), be.alloc(row), be.alloc(row)
+    for p_, n_ in ((qd, H * D), (kd, row), (vd, row)):
+        be.fill_normal(p_, n_, seed=3)
+    out = be.alloc(n_pre * H * D)
+    cal_floats = COPY_CAL_BYTES // 4
+    src, dst = be.alloc(cal_floats), be.alloc(cal_floats)
+    be.fill_normal(src, cal_floats, seed=4)
+    q_pre, k_pre, v_pre = be.alloc(n_pre * H * D), be.alloc(n_pre * row), be.alloc(n_pre * row)
+    for p_, n_ in ((q_pre, n_pre * H * D), (k_pre, n_pre * row), (v_pre, n_pre * row)):
+        be.fill_normal(p_, n_, seed=5)
+    be.sync()
+    for s in range(PROBE_DECODE_STEPS):
+        be.append_rope(qd, ck, cv, kd, vd, 1, ctx + s, H, KV, D, base, neox, ff)
+        be.attention(qd, ck, cv, out, 1, ctx + s, H, KV, D)
+    be.copy(dst, src, cal_floats)
+    be.append_rope(q_pre, ck, cv, k_pre, v_pre, n_pre, 0, H, KV, D, base, neox, ff)
+    be.attention(q_pre, ck, cv, out, n_pre, 0, H, KV, D)
+    be.sync()
+    be.close()
+    log("probe done")
+
+
+def _counter_rows(csv_path):
+    import csv
+    with open(csv_path, newline="") as f:
+        return [(int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])) for r in csv.DictReader(f)]
+
+
+def measure_traffic(out_dir, timeout_s=150):
+    """HBM bytes per launch of the decode partial kernel and the prefill MFMA kernel: two `rocprofv3 --pmc` passes
+    over probe() (FETCH_SIZE, then WRITE_SIZE, each in KiB per dispatch, summed over the dispatch's counter
+    instances), each scaled by the factor that makes the same counter read the known bytes of the calibration copy.
+    Runs the profiler as a child process; returns a dict, or None with a logged reason."""
+    import shutil
+    import subprocess
+
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        log("traffic: rocprofv3 not found")
+        return None
+    per = {}
+    env = dict(os.environ, TMPDIR="/tmp")
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = os.path.join(out_dir, f"pmc_{counter.lower()}")
+        cmd = [prof, "--pmc", counter, "-f", "csv", "-d", d, "-o", "run", "--",
+               sys.executable, "-u", os.path.abspath(__file__), "--probe"]
+        log("traffic: " + " ".join(cmd))
+        try:
+            r = subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout_s, stdout=subprocess.DEVNULL,
+                               stderr=subprocess.PIPE, text=True)
+        except subprocess.TimeoutExpired:
+            log(f"traffic: {counter} pass timed out")
+            return None
+        files = [os.path.join(dp, f) for dp, _, fs in os.walk(d) for f in fs if f.endswith("counter_collection.csv")]
+        if not files or "probe done" not in (r.stderr or ""):
+            log(f"traffic: {counter} pass failed (rc {r.returncode}): {(r.stderr or '')[-400:]}")
+            return None
+        sums = {}
+        for disp, name, val in _counter_rows(files[0]):
+            key = (disp, name)
+            sums[key] = sums.get(key, 0.0) + val
+        rows = sorted((disp, name, v) for (disp, name), v in sums.items())
+        cal = [x for x in rows if "copy_kernel" in x[1]]
+        if len(cal) != 1:
+            log(f"traffic: expected one calibration copy dispatch, found {len(cal)}")
+            return None
+        cal_disp = cal[0][0]
+        dec = [v for disp, name, v in rows if "attn_decode_partial" in name and disp < cal_disp]
+        pre = [v for disp, name, v in rows if "attn_prefill_kernel" in name and disp > cal_disp]
+        if len(dec) != PROBE_DECODE_STEPS or len(pre) != 1:
+            log(f"traffic: unexpected dispatch counts (decode {len(dec)}, prefill {len(pre)})")
+            return None
+        per[counter] = {"cal_kib": cal[0][2], "decode_kib": float(np.mean(dec)), "prefill_kib": pre[0]}
+    f_fetch = COPY_CAL_BYTES / 1024.0 / per["FETCH_SIZE"]["cal_kib"]
+    f_write = COPY_CAL_BYTES / 1024.0 / per["WRITE_SIZE"]["cal_kib"]
+
+    def traffic(key):
+        return 1024.0 * (per["FETCH_SIZE"][key] * f_fetch + per["WRITE_SIZE"][key] * f_write)
+
+    return {"decode_bytes": traffic("decode_kib"), "prefill_bytes": traffic("prefill_kib"),
+            "fetch_factor": f_fetch, "write_factor": f_write, "raw_kib": per}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -113,7 +220,15 @@ def main():
     ap.add_argument("--prefill-reps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=16.0, help="budget of the CPU baseline samples")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc passes (child processes, about 10 s each) that measure HBM "
+                         "bytes per launch for roofline.traffic")
+    ap.add_argument("--traffic-dir", default=os.path.join(ROOT, "gpurun_out", "traffic"))
+    ap.add_argument("--probe", action="store_true", help="internal: the short run the traffic passes profile")
     args = ap.parse_args()
+    if args.probe:
+        probe()
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
@@ -200,9 +315,11 @@ def main():
     dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
     log(f"decode: {dec_ms:.3f} ms for {args.steps} steps -> {dec_gbs:.1f} GB/s ({dec_gbs / HBM_PEAK_GBS:.1%})")
 
-    # ---------------- per-kernel durations (separate pass: event bracketing adds a little launch overhead)
+    # ---------------- per-kernel durations: a second pass over the same K decode steps (and one prefill) in which every
+    # launch carries a start/stop event pair stamped from the dispatch itself (hipExtLaunchKernel, on the launch's own
+    # stream); kept out of the timed region above, where the extra event work would sit between launches
     KernelTiming.enable(True)
-    n_roof = min(8, args.steps)
+    n_roof = args.steps
     for s in range(n_roof):
         decode_step(s)
     be.sync()
@@ -254,7 +371,10 @@ def main():
                                  "unit": "TFLOP/s", "frac": round(mfma_tflops / MFMA_F16_PEAK_TFLOPS, 4),
                                  "traffic": None, "kernel": "attn_prefill_kernel<64>",
                                  "avg_launch_us": round(mfma_ms / mfma_n * 1e3, 2), "launches": mfma_n,
-                                 "algorithmic_flops_per_launch": mfma_flops}},
+                                 "algorithmic_flops_per_launch": mfma_flops,
+                                 # fp32 Q rows read and output rows written, fp16 staged K and V^T read once
+                                 "algorithmic_bytes_per_launch": int(2 * 4 * (n_pre - FP32_PREFIX_ROWS) * H * D
+                                                                     + 2 * 2 * n_pre * KV * D)}},
         "kernels_us": {"decode_combine": round(comb_ms / max(comb_n, 1) * 1e3, 3),
                        "append_rope_decode": round(app_ms / max(app_n, 1) * 1e3, 3),
                        "append_rope_prefill": round(app2_ms / max(app2_n, 1) * 1e3, 2),
@@ -264,8 +384,19 @@ def main():
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(be, shape, ck[0], cv[0], qd, ctx, q_pre0_host, args.cpu_seconds)
-    print(json.dumps(result), flush=True)
     be.close()
+    if not args.no_traffic:
+        t = measure_traffic(args.traffic_dir)
+        if t is not None:
+            note = (f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch x calibration factors {t['fetch_factor']:.4f} "
+                    f"/ {t['write_factor']:.4f} (known-size {COPY_CAL_BYTES >> 20} MiB copy kernel)")
+            result["roofline"]["traffic"] = int(t["decode_bytes"])
+            result["roofline"]["traffic_method"] = note
+            result["prefill"]["roofline"]["traffic"] = int(t["prefill_bytes"])
+            log(f"traffic: decode partial {t['decode_bytes'] / 1e6:.2f} MB/launch (algorithmic "
+                f"{result['roofline']['algorithmic_bytes_per_launch'] / 1e6:.2f} MB), prefill mfma "
+                f"{t['prefill_bytes'] / 1e6:.2f} MB/launch; raw {json.dumps(t['raw_kib'])}")
+    print(json.dumps(result), flush=True)
 
 
 if __name__ == "__main__":

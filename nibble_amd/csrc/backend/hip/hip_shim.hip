@@ -4,6 +4,7 @@
 // include HIP; HipBackend (hip_backend.cpp) sees only nibble_hip_shim.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -18,7 +19,6 @@ struct Record {
 };
 bool g_enabled = false;
 std::vector<Record> g_records;
-hipEvent_t g_pending[NBHS_K_COUNT] = {};  // start event of the launch being bracketed, per kernel id
 
 void drop_all() {
   for (auto& r : g_records) {
@@ -31,25 +31,18 @@ void drop_all() {
 
 bool enabled() { return g_enabled; }
 
-void record_begin(int kernel, hipStream_t s) {
-  hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return;
-  (void)hipEventRecord(e, s);
-  g_pending[kernel] = e;
+hipError_t make_pair(hipEvent_t* start, hipEvent_t* end) {
+  hipError_t e = hipEventCreate(start);
+  if (e != hipSuccess) return e;
+  e = hipEventCreate(end);
+  if (e != hipSuccess) {
+    (void)hipEventDestroy(*start);
+    *start = nullptr;
+  }
+  return e;
 }
 
-void record_end(int kernel, hipStream_t s) {
-  hipEvent_t start = g_pending[kernel];
-  g_pending[kernel] = nullptr;
-  if (!start) return;
-  hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) {
-    (void)hipEventDestroy(start);
-    return;
-  }
-  (void)hipEventRecord(e, s);
-  g_records.push_back({kernel, start, e});
-}
+void push(int kernel, hipEvent_t start, hipEvent_t end) { g_records.push_back({kernel, start, end}); }
 
 }  // namespace nbhs_timing
 
@@ -140,6 +133,27 @@ __global__ void zero_kernel(uint8_t* __restrict__ p, int64_t bytes) {
   for (int64_t i = vecs * 16 + blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < bytes; i += stride) p[i] = 0;
 }
 
+// Device-to-device copy of non-overlapping ranges: 16-byte vectors when both ends are 16-byte aligned, else
+// 4-byte words when both are word aligned, else bytes; grid-stride over the vectors, then the tail.
+__global__ void copy_kernel(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, int64_t bytes) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  const int64_t tid = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src);
+  int64_t done = 0;
+  if ((a & 15) == 0) {
+    const int64_t vecs = bytes / 16;
+    for (int64_t i = tid; i < vecs; i += stride)
+      reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+    done = vecs * 16;
+  } else if ((a & 3) == 0) {
+    const int64_t words = bytes / 4;
+    for (int64_t i = tid; i < words; i += stride)
+      reinterpret_cast<uint32_t*>(dst)[i] = reinterpret_cast<const uint32_t*>(src)[i];
+    done = words * 4;
+  }
+  for (int64_t i = done + tid; i < bytes; i += stride) dst[i] = src[i];
+}
+
 // SplitMix64 finaliser.
 __device__ __forceinline__ uint64_t mix64(uint64_t z) {
   z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -227,7 +241,11 @@ int nbhs_memcpy_d2h(void* dst, const void* src, size_t bytes, nbhs_stream s) {
 }
 int nbhs_memcpy_d2d(void* dst, const void* src, size_t bytes, nbhs_stream s) {
   if (bytes == 0) return hipSuccess;
-  return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, S(s));
+  if (!dst || !src) return NBHS_EINVAL;
+  // At most 2048 blocks (8 per CU): a grid-stride loop at that occupancy saturates HBM.
+  copy_kernel<<<std::min(grid_for(int64_t(bytes / 16 + 1)), 2048u), kThreads, 0, S(s)>>>(
+      static_cast<uint8_t*>(dst), static_cast<const uint8_t*>(src), int64_t(bytes));
+  return hipGetLastError();
 }
 
 int nbhs_rope_f32(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0, const float* cs_table,
@@ -235,10 +253,8 @@ int nbhs_rope_f32(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_
   if (!x || !cs_table || n <= 0 || n_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || pos0 < 0 ||
       pos0 + n > table_rows)
     return NBHS_EINVAL;
-  nbhs_timing::KernelTimer timer(NBHS_K_ROPE, S(s));
-  rope_kernel<<<grid_for(n * n_heads * (head_dim / 2)), kThreads, 0, S(s)>>>(
-      x, n, n_heads, head_dim, pos0, reinterpret_cast<const float2*>(cs_table), neox);
-  return hipGetLastError();
+  return nbhs_timing::launch(NBHS_K_ROPE, rope_kernel, dim3(grid_for(n * n_heads * (head_dim / 2))), dim3(kThreads),
+                             S(s), x, n, n_heads, head_dim, pos0, reinterpret_cast<const float2*>(cs_table), neox);
 }
 
 int nbhs_append_rope_f32(float* q, float* cache_k, float* cache_v, const float* k_new, const float* v_new, int64_t n,
@@ -247,11 +263,10 @@ int nbhs_append_rope_f32(float* q, float* cache_k, float* cache_v, const float* 
   if (!q || !cache_k || !cache_v || !k_new || !v_new || !cs_table || n <= 0 || n_heads <= 0 || n_kv_heads <= 0 ||
       head_dim <= 0 || head_dim % 2 != 0 || pos0 < 0 || pos0 + n > table_rows)
     return NBHS_EINVAL;
-  nbhs_timing::KernelTimer timer(NBHS_K_APPEND_ROPE, S(s));
-  append_rope_kernel<<<grid_for(n * (n_heads + 2 * n_kv_heads) * (head_dim / 2)), kThreads, 0, S(s)>>>(
-      q, cache_k, cache_v, k_new, v_new, n, pos0, n_heads, n_kv_heads, head_dim,
-      reinterpret_cast<const float2*>(cs_table), neox);
-  return hipGetLastError();
+  return nbhs_timing::launch(NBHS_K_APPEND_ROPE, append_rope_kernel,
+                             dim3(grid_for(n * (n_heads + 2 * n_kv_heads) * (head_dim / 2))), dim3(kThreads), S(s), q,
+                             cache_k, cache_v, k_new, v_new, n, pos0, n_heads, n_kv_heads, head_dim,
+                             reinterpret_cast<const float2*>(cs_table), neox);
 }
 
 int nbhs_fill_normal_f32(float* dst, int64_t count, uint64_t seed, float scale, nbhs_stream s) {

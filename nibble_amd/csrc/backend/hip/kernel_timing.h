@@ -1,30 +1,44 @@
 #pragma once
-// Launch bracketing for nbhs_kernel_timing_* (see nibble_hip_shim.h): when timing is enabled, a KernelTimer
-// records a HIP event on the launch stream at construction and another at destruction, so the pair spans exactly
-// the kernel launched in between.
+// Kernel launches for the shim's launchers (nbhs_kernel_timing_* in nibble_hip_shim.h). With timing enabled, a
+// launch goes through hipExtLaunchKernel with a start and a stop event, which the runtime stamps from the
+// dispatch's own begin and end - the timestamps a kernel trace reads - so queueing and launch latency stay out of
+// the measured duration. Disabled, it is a plain hipLaunchKernel.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
+
+#include <tuple>
 
 namespace nbhs_timing {
 
 bool enabled();
-void record_begin(int kernel, hipStream_t s);
-void record_end(int kernel, hipStream_t s);
+// Creates the event pair for one timed dispatch.
+hipError_t make_pair(hipEvent_t* start, hipEvent_t* end);
+// Takes ownership of an event pair stamped around one dispatch of `kernel`.
+void push(int kernel, hipEvent_t start, hipEvent_t end);
 
-class KernelTimer {
- public:
-  KernelTimer(int kernel, hipStream_t s) : kernel_(kernel), s_(s), on_(enabled()) {
-    if (on_) record_begin(kernel_, s_);
+// Launches fn<<<grid, block, 0, s>>>(a...), converting each argument to the kernel's parameter type.
+template <typename... P, typename... A>
+hipError_t launch(int kernel, void (*fn)(P...), dim3 grid, dim3 block, hipStream_t s, A&&... a) {
+  static_assert(sizeof...(P) == sizeof...(A) && sizeof...(P) > 0, "argument count must match the kernel");
+  std::tuple<P...> args{static_cast<P>(a)...};
+  void* ptrs[sizeof...(P)];
+  std::apply([&ptrs](auto&... x) {
+    int i = 0;
+    ((ptrs[i++] = static_cast<void*>(&x)), ...);
+  }, args);
+  const void* f = reinterpret_cast<const void*>(fn);
+  if (!enabled()) return hipLaunchKernel(f, grid, block, ptrs, 0, s);
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t e = make_pair(&e0, &e1);
+  if (e != hipSuccess) return e;
+  e = hipExtLaunchKernel(f, grid, block, ptrs, 0, s, e0, e1, 0);
+  if (e != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return e;
   }
-  ~KernelTimer() {
-    if (on_) record_end(kernel_, s_);
-  }
-  KernelTimer(const KernelTimer&) = delete;
-  KernelTimer& operator=(const KernelTimer&) = delete;
-
- private:
-  int kernel_;
-  hipStream_t s_;
-  bool on_;
-};
+  push(kernel, e0, e1);
+  return hipSuccess;
+}
 
 }  // namespace nbhs_timing

@@ -474,24 +474,21 @@ int launch_decode(const float* q, const float* k, const float* v, float* out, in
   float* ws_ml = ws ? ws + n * H * p.n_chunks * HD : nullptr;
   const int group = int(H / KV);
   const dim3 grid(p.n_chunks, unsigned(KV * p.n_sub), unsigned(n));
-  {
-    nbhs_timing::KernelTimer timer(NBHS_K_DECODE_PARTIAL, s);
-#define NBH_DECODE(GB)                                                                                              \
-  attn_decode_partial<HD, GB><<<grid, kDecodeThreads, 0, s>>>(q, k, v, out, ws_o, ws_ml, pos0, int(H), int(KV), \
-                                                               group, p.n_sub, p.n_chunks, p.groups_per_chunk, qscale)
-    switch (p.gb) {
-      case 1: NBH_DECODE(1); break;
-      case 2: NBH_DECODE(2); break;
-      case 4: NBH_DECODE(4); break;
-      default: NBH_DECODE(8); break;
-    }
-#undef NBH_DECODE
+  hipError_t e;
+#define NBH_DECODE(GB)                                                                                             \
+  e = nbhs_timing::launch(NBHS_K_DECODE_PARTIAL, attn_decode_partial<HD, GB>, grid, dim3(kDecodeThreads), s, q, k, \
+                          v, out, ws_o, ws_ml, pos0, int(H), int(KV), group, p.n_sub, p.n_chunks,                   \
+                          p.groups_per_chunk, qscale)
+  switch (p.gb) {
+    case 1: NBH_DECODE(1); break;
+    case 2: NBH_DECODE(2); break;
+    case 4: NBH_DECODE(4); break;
+    default: NBH_DECODE(8); break;
   }
-  hipError_t e = hipGetLastError();
+#undef NBH_DECODE
   if (e != hipSuccess || p.n_chunks == 1) return e;
-  nbhs_timing::KernelTimer timer(NBHS_K_DECODE_COMBINE, s);
-  attn_decode_combine<HD><<<unsigned(n * H), kDecodeThreads, 0, s>>>(ws_o, ws_ml, out, p.n_chunks);
-  return hipGetLastError();
+  return nbhs_timing::launch(NBHS_K_DECODE_COMBINE, attn_decode_combine<HD>, dim3(unsigned(n * H)),
+                             dim3(kDecodeThreads), s, ws_o, ws_ml, out, p.n_chunks);
 }
 
 bool tiled_head_dim(int64_t hd) { return hd == 64 || hd == 128; }
@@ -527,10 +524,8 @@ int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* 
     return NBHS_EINVAL;
   const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
   if (!tiled_head_dim(head_dim)) {
-    nbhs_timing::KernelTimer timer(NBHS_K_GENERIC, s);
-    attn_generic<<<dim3(unsigned(n_heads), unsigned(n)), 64, 0, s>>>(q, k, v, out, pos0, int(n_heads),
-                                                                     int(n_kv_heads), int(head_dim), qscale);
-    return hipGetLastError();
+    return nbhs_timing::launch(NBHS_K_GENERIC, attn_generic, dim3(unsigned(n_heads), unsigned(n)), dim3(64), s, q, k,
+                               v, out, pos0, int(n_heads), int(n_kv_heads), int(head_dim), qscale);
   }
   const Plan p = make_plan(n, pos0, n_heads, n_kv_heads, head_dim, cu_count);
   const int64_t need = p.n_chunks == 1 ? 0 : n * n_heads * p.n_chunks * (head_dim + 2);

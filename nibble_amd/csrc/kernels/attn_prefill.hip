@@ -293,14 +293,10 @@ int nbhs_stage_kv_f16(const float* k, const float* v, void* k16, void* vt16, int
     return NBHS_EINVAL;
   const int64_t rows_pad = round_up(rows, kBN);
   const dim3 grid(unsigned(rows_pad / kBN), unsigned(n_kv_heads));
-  nbhs_timing::KernelTimer timer(NBHS_K_STAGE_KV, s);
-  if (head_dim == 64)
-    stage_kv_kernel<64><<<grid, 256, 0, s>>>(k, v, static_cast<_Float16*>(k16), static_cast<_Float16*>(vt16), rows,
-                                             rows_pad, int(n_kv_heads));
-  else
-    stage_kv_kernel<128><<<grid, 256, 0, s>>>(k, v, static_cast<_Float16*>(k16), static_cast<_Float16*>(vt16), rows,
-                                              rows_pad, int(n_kv_heads));
-  return hipGetLastError();
+  auto* const kh = static_cast<_Float16*>(k16);
+  auto* const vh = static_cast<_Float16*>(vt16);
+  return nbhs_timing::launch(NBHS_K_STAGE_KV, head_dim == 64 ? stage_kv_kernel<64> : stage_kv_kernel<128>, grid,
+                             dim3(256), s, k, v, kh, vh, rows, rows_pad, int(n_kv_heads));
 }
 
 int nbhs_attn_prefill_mfma(const float* q, const void* k16, const void* vt16, float* out, int64_t n, int64_t pos0,
@@ -316,18 +312,10 @@ int nbhs_attn_prefill_mfma(const float* q, const void* k16, const void* vt16, fl
   if (tiles * n_kv_heads > int64_t(1) << 31) return NBHS_EINVAL;
   const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
   const unsigned blocks = unsigned(tiles * n_kv_heads);
-  nbhs_timing::KernelTimer timer(NBHS_K_PREFILL_MFMA, s);
-  if (head_dim == 64)
-    attn_prefill_kernel<64><<<blocks, kWaves * 64, 0, s>>>(q, static_cast<const _Float16*>(k16),
-                                                           static_cast<const _Float16*>(vt16), out, n, pos0,
-                                                           int(n_heads), int(n_kv_heads), int(group), staged_rows_pad,
-                                                           int(tiles), qscale);
-  else
-    attn_prefill_kernel<128><<<blocks, kWaves * 64, 0, s>>>(q, static_cast<const _Float16*>(k16),
-                                                            static_cast<const _Float16*>(vt16), out, n, pos0,
-                                                            int(n_heads), int(n_kv_heads), int(group),
-                                                            staged_rows_pad, int(tiles), qscale);
-  return hipGetLastError();
+  return nbhs_timing::launch(NBHS_K_PREFILL_MFMA, head_dim == 64 ? attn_prefill_kernel<64> : attn_prefill_kernel<128>,
+                             dim3(blocks), dim3(kWaves * 64), s, q, static_cast<const _Float16*>(k16),
+                             static_cast<const _Float16*>(vt16), out, n, pos0, int(n_heads), int(n_kv_heads),
+                             int(group), staged_rows_pad, int(tiles), qscale);
 }
 
 }  // extern "C"

@@ -338,3 +338,36 @@ def test_reserve_prevents_workspace_growth(backend):
         assert be.internal_bytes() == cap
     finally:
         be.close()
+
+
+@pytest.mark.parametrize("count,src_off,dst_off", [(1, 0, 0), (5, 1, 3), (1000, 0, 0), (1003, 2, 1), (4097, 4, 8),
+                                                   (262147, 0, 4), (262147, 3, 0)])
+def test_copy_exact_and_neighbours_untouched(backend, count, src_off, dst_off):
+    """Backend::copy (backend.h:32) on the copy kernel: every alignment class (16-byte vectors, words), ragged
+    tails, and no write outside [dst, dst + count)."""
+    rng = np.random.default_rng(count + 7 * src_off + 13 * dst_off)
+    src = rng.standard_normal(count + 16).astype(np.float32)
+    dst0 = rng.standard_normal(count + 16).astype(np.float32)
+    with Buffers(backend) as B:
+        ds, dd = B.upload(src), B.upload(dst0)
+        backend.copy(dd.at(dst_off), ds.at(src_off), count)
+        got = backend.download(dd, dst0.shape)
+    want = dst0.copy()
+    want[dst_off:dst_off + count] = src[src_off:src_off + count]
+    assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("shift", [-5, -1, 1, 4, 1000])
+def test_copy_overlapping_is_memmove(backend, shift):
+    """Overlapping ranges copy as if through a temporary: the reference's Backend::copy is std::memmove
+    (cpu_backend.cpp:260-263)."""
+    n, count = 6000, 4000
+    x = np.random.default_rng(abs(shift)).standard_normal(n).astype(np.float32)
+    s0 = 1000
+    with Buffers(backend) as B:
+        dx = B.upload(x)
+        backend.copy(dx.at(s0 + shift), dx.at(s0), count)
+        got = backend.download(dx, x.shape)
+    want = x.copy()
+    want[s0 + shift:s0 + shift + count] = x[s0:s0 + count]
+    assert np.array_equal(bits(got), bits(want))
