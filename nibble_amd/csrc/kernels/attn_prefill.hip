@@ -2,11 +2,12 @@
 // semantics of ref_ops.cpp:188-214 (row t attends to cache rows 0..pos0+t; head h reads KV head h/(H/KV)).
 //
 // Numerics: Q is scaled by log2(e)/sqrt(d) and rounded to fp16, K and V come from fp16 copies of the fp32 cache
-// (stage_kv), QK^T and PV run on v_mfma_f32_32x32x16_f16 with fp32 accumulation, and the online softmax (max,
-// exp2, running sums, rescaling) is fp32 - the running max is raised lazily (only past a growth of kLazy), so the
-// O accumulators are rescaled in a rare wave-uniform branch and unnormalised weights stay <= 2^kLazy. The host
-// routes rows with fewer than 256 visible keys to the fp32 decode kernel, where fp16 rounding of a few V rows is
-// not averaged away.
+// (stage_kv), QK^T and PV run on v_mfma_f32_32x32x16_f16 with fp32 accumulation, and the online softmax (shift,
+// exp2, running sums, rescaling) is fp32. The softmax shift is not the running max: it is set from the first tile
+// and raised only when a tile's weights outgrow it (checked through their sum, see kPSumMax), so the per-tile
+// max, the subtraction (folded into the MFMA accumulator init) and the O rescale all leave the common path; the
+// result is the same normalised softmax, since any shift cancels. The host routes rows with fewer than 256
+// visible keys to the fp32 decode kernel, where fp16 rounding of a few V rows is not averaged away.
 //
 // Layout (per wave, 32 query rows):
 //  * S^T = K Q^T: A = K tile rows from LDS ([key][d], 16 B per lane), B = the wave's Q fragment held in
@@ -38,10 +39,15 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBN = 64;          // keys per tile
 constexpr int kRowsPerWave = 32;
-constexpr int kWaves = 4;
+#ifndef NBH_PREFILL_WAVES
+#define NBH_PREFILL_WAVES 4
+#endif
+constexpr int kWaves = NBH_PREFILL_WAVES;
 constexpr int kRowsPerBlock = kRowsPerWave * kWaves;
 constexpr int kPad = 8;          // halves of LDS row padding (keeps rows 16-byte aligned, spreads banks)
-constexpr float kLazy = 8.0f;    // allowed growth of scores over the running max before the accumulators rescale
+// Largest sum of one lane's 32 tile weights accepted without recomputing the tile against a raised shift: every
+// weight is then <= 2^12, far inside fp16 (max 65504).
+constexpr float kPSumMax = 4096.0f;
 
 __device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }  // v_exp_f32; -inf -> 0
 
@@ -84,16 +90,23 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(const float* __restrict__
 #ifndef NBH_PREFILL_WAVES_PER_EU
 #define NBH_PREFILL_WAVES_PER_EU 3
 #endif
+#ifndef NBH_PREFILL_MIN_WAVES_PER_EU
+#define NBH_PREFILL_MIN_WAVES_PER_EU 1
+#endif
 template <int HD>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, NBH_PREFILL_WAVES_PER_EU)))
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(NBH_PREFILL_MIN_WAVES_PER_EU, NBH_PREFILL_WAVES_PER_EU)))
 void attn_prefill_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16,
     float* __restrict__ out, int64_t n, int64_t pos0, int n_heads, int n_kv, int group, int64_t rows_pad,
     int n_tiles, float qscale) {
   constexpr int DC = HD / 16;  // 16-wide d chunks of the S^T contraction
   constexpr int DT = HD / 32;  // 32-row d tiles of O^T
+  // Row strides (halves). K rows are read 16 B per lane, 36 dwords apart: 8 (or 16) consecutive rows cover
+  // distinct 4-bank groups. V^T rows are read 8 B per lane, 34 dwords apart: 17 is odd, so any 16 (or 32)
+  // consecutive rows land on distinct even bank pairs - a 36-dword stride would put rows r and r + 8 on the same
+  // banks and serialise half of every V read.
   constexpr int KLD = HD + kPad;
-  constexpr int VLD = kBN + kPad;
+  constexpr int VLD = kBN + 4;
   constexpr int K_VECS = kBN * HD / 8;  // 16-byte vectors per K tile
   constexpr int V_VECS = HD * kBN / 8;
   constexpr int THREADS = kWaves * 64;
@@ -145,7 +158,11 @@ void attn_prefill_kernel(
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  // m_sh: the query's softmax shift (log2 domain); mneg: 16 copies of -m_sh, the accumulator block S^T starts from.
+  float m_sh = 0.f, l_run = 0.f;
+  floatx16 mneg;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) mneg[r] = 0.f;
 
   const _Float16* kg = k16 + int64_t(g) * rows_pad * HD;
   const _Float16* vg = vt16 + int64_t(g) * HD * rows_pad;
@@ -174,7 +191,9 @@ void attn_prefill_kernel(
     for (int i = 0; i < V_PER_T; ++i) {
       const int ci = threadIdx.x + THREADS * i;
       const int d = ci / (kBN / 8), c8 = ci % (kBN / 8);
-      *reinterpret_cast<half8_t*>(&vs[buf][d][8 * c8]) = vreg[i];
+      // V^T rows are 8-byte aligned (VLD = 68 halves): two 8-byte stores
+      *reinterpret_cast<half4_t*>(&vs[buf][d][8 * c8]) = half4_t{vreg[i][0], vreg[i][1], vreg[i][2], vreg[i][3]};
+      *reinterpret_cast<half4_t*>(&vs[buf][d][8 * c8 + 4]) = half4_t{vreg[i][4], vreg[i][5], vreg[i][6], vreg[i][7]};
     }
   };
 
@@ -185,19 +204,16 @@ void attn_prefill_kernel(
     const int cur = kt & 1;
     if (kt + 1 < ntk) load_tile(kt + 1);
     if (wave_active && int64_t(kt) * kBN < wave_kend) {
-      // S^T for the tile's two 32-key halves; the two accumulator chains are interleaved so consecutive MFMAs do
-      // not wait on each other's results.
+      // S^T - m for the tile's two 32-key halves: the first MFMA of each chain starts from the accumulator block
+      // mneg (every entry -m_sh, the lane's query shift), so the subtraction costs no instruction. The two chains
+      // are interleaved so consecutive MFMAs do not wait on each other's results.
       floatx16 s[2];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[kk][r] = 0.f;
 #pragma unroll
       for (int c = 0; c < DC; ++c)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const half8_t a = *reinterpret_cast<const half8_t*>(&ks[cur][kk * 32 + ql][16 * c + 8 * hf]);
-          s[kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s[kk], 0, 0, 0);
+          s[kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], c == 0 ? mneg : s[kk], 0, 0, 0);
         }
       // Causal mask (and inactive rows) only where some key of the tile lies past the wave's first row.
       if (int64_t(kt) * kBN + kBN > wave_kfull) {
@@ -210,38 +226,54 @@ void attn_prefill_kernel(
           for (int r = 0; r < 16; ++r)
             if (kk * 32 + 8 * (r / 4) + 4 * hf + (r % 4) > rel) s[kk][r] = -INFINITY;
       }
-      float mt = -INFINITY;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kk][r]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      // Lazy rescaling: the reference max moves only when some query's scores outgrew it by more than kLazy
-      // (wave-uniform branch, rare after the first tiles); weights then stay <= 2^kLazy, well inside fp16.
-      if (__builtin_amdgcn_ballot_w64(mt > m_run + kLazy)) {
-        const float m_new = fmaxf(m_run, mt);
-        const float corr = exp2_raw(m_run - (m_new == -INFINITY ? 0.0f : m_new));
-        l_run *= corr;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
-        m_run = m_new;
-      }
-      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-      // P in fp16 (the MFMA B operand); the row sum is accumulated from the same fp16 values with v_dot2, so the
-      // normaliser matches the weights the MFMA actually multiplies.
+      // P = exp2(S - m_sh) in fp16 (the MFMA B operand) and the lane's sum of it, taken from the same fp16 values
+      // with v_dot2 so the normaliser matches the weights the MFMA multiplies.
       half8_t pb[4];
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pb[kc][e] = (_Float16)exp2_raw(s[kc >> 1][8 * (kc & 1) + e] - m_use);
+      float l_tile = 0.f;
       const half2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
+      auto exps = [&](float shift) {
+        l_tile = 0.f;
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc)
+        for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
-        for (int e = 0; e < 8; e += 2)
-          l_run = __builtin_amdgcn_fdot2(half2_t{pb[kc][e], pb[kc][e + 1]}, ones, l_run, false);
+          for (int e = 0; e < 8; ++e) pb[kc][e] = (_Float16)exp2_raw(s[kc >> 1][8 * (kc & 1) + e] - shift);
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+          for (int e = 0; e < 8; e += 2)
+            l_tile = __builtin_amdgcn_fdot2(half2_t{pb[kc][e], pb[kc][e + 1]}, ones, l_tile, false);
+      };
+      // The shift is not raised per tile: the weights are computed against the current one, and only when some
+      // lane's sum leaves (0, kPSumMax] - a score grew past the shift by ~12 (log2), or inf/NaN from an fp16
+      // overflow - does the wave take the slow path below (always on its first tile, where no shift exists yet).
+      bool slow = kt == 0;
+      if (!slow) {
+        exps(0.0f);
+        slow = __builtin_amdgcn_ballot_w64(!(l_tile <= kPSumMax)) != 0;
+      }
+      if (slow) {
+        float mt = -INFINITY;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kk][r]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        // first tile: shift to the tile max (0 if every key is masked); later: raise by the excess only
+        const float d = kt == 0 ? (mt == -INFINITY ? 0.0f : mt) : fmaxf(mt, 0.0f);
+        exps(d);
+        if (kt != 0) {
+          const float corr = exp2_raw(-d);
+          l_run *= corr;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
+        }
+        m_sh += d;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mneg[r] = -m_sh;
+      }
+      l_run += l_tile;
       // O^T += V^T P^T over 4 steps of 16 keys; the DT output tiles are independent chains.
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
