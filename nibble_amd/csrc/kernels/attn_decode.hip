@@ -4,13 +4,15 @@
 // Design (CDNA4, wave64; HBM-bound: arithmetic intensity H/(2*KV) FLOP/B, far below the fp32 ridge). Measured on
 // MI355X: a pure read of this access pattern streams at ~6 TB/s; what separates the kernel from that is VALU work
 // per byte, so the loop is built to spend as few instructions per K/V byte as possible.
-//  * Grid = (context chunk, KV head x head subgroup, query row). A workgroup streams one contiguous chunk of one
-//    KV head and serves every query head of its GQA group from registers: each K/V byte is read from HBM once per
-//    step, not once per query head.
+//  * Grid = (context chunk, KV head x head subgroup, query row), sized to the workgroups that fit on the chip at
+//    once. A workgroup streams one chunk of one KV head - row groups c, c + n_chunks, ..., so that all workgroups
+//    sweep the cache together - and serves every query head of its GQA group from registers: each K/V byte is read
+//    from HBM once per step, not once per query head.
 //  * A 64-float K/V row is 8 lanes x 2 float4 (lane dl holds float4 columns dl and dl + 8, so each load
-//    instruction reads whole contiguous 128-byte halves of 8 rows); a wave covers 8 rows per load pair
-//    and keeps NBH_DECODE_UNROLL such row slots of K and of V in flight per lane, software-pipelined one iteration
-//    ahead, with non-temporal (streaming) loads. Dot products reduce over the 8 lanes with 3 DPP steps.
+//    instruction reads whole contiguous 128-byte halves of 8 rows); a wave covers 8 rows per load pair and keeps
+//    NBH_DECODE_UNROLL such row slots of K and of V in flight per lane, with non-temporal (streaming) loads; the
+//    next group's loads are issued right after the current group is consumed. Dot products reduce over the 8 lanes
+//    with 3 DPP steps.
 //  * Online softmax in the log2 domain (queries pre-scaled by log2(e)/sqrt(d)) with raw v_exp_f32 and one running
 //    max per wave and query head, raised only when some score exceeds it by more than kLazy (log2 units) - a rare,
 //    wave-uniform branch - so unnormalised weights stay <= 2^kLazy and the wave's 8 row groups share one scale: at
@@ -44,6 +46,11 @@ constexpr int kDecodeThreads = 256;  // 4 waves
 // K/V rows are read exactly once per step: stream them past the caches (non-temporal loads) unless disabled.
 #ifndef NBH_DECODE_NT
 #define NBH_DECODE_NT 1
+#endif
+// Chunk c of a head takes row groups c, c + n_chunks, c + 2 n_chunks, ... (1) instead of one contiguous range (0):
+// all workgroups then sweep the cache together, front to back.
+#ifndef NBH_DECODE_INTERLEAVE
+#define NBH_DECODE_INTERLEAVE 1
 #endif
 constexpr int kUnroll = NBH_DECODE_UNROLL;
 constexpr int kMaxChunks = 4096;  // partials per (row, head); bounds the combine kernel's LDS table
@@ -112,7 +119,7 @@ template <int HD, int GB>
 __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ out,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, int64_t pos0, int n_heads, int n_kv, int group, int n_sub,
-    int n_chunks, int64_t groups_per_chunk, float qscale) {
+    int n_chunks, int64_t groups_per_chunk, int64_t extra_groups, float qscale) {
   constexpr int VPL = 2;                            // float4 per lane per row
   constexpr int LPR = HD / (4 * VPL);               // lanes per K/V row: 8 (hd 64) or 16 (hd 128)
   constexpr int RPS = 64 / LPR;                     // rows per wave load
@@ -130,10 +137,18 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
   const int h0 = g * group + sg * GB;
   const int gcount = min(GB, group - sg * GB);
   const int64_t len = pos0 + t + 1;
-  // The chunk: row groups [g0, g1) of kStep consecutive rows each, clipped to this row's causal length.
+  // The chunk's row groups (kStep consecutive rows each), clipped to this row's causal length: iteration i takes
+  // group g0 + i * gstride, for i < gcnt. The first extra_groups chunks hold one group more than the others (the
+  // remainder of the even split).
   const int64_t n_groups = (len + kStep - 1) / kStep;
-  const int64_t g0 = int64_t(chunk) * groups_per_chunk;
-  const int64_t g1 = min(g0 + groups_per_chunk, n_groups);
+  const bool extra = chunk < extra_groups;
+#if NBH_DECODE_INTERLEAVE
+  const int64_t g0 = chunk, gstride = n_chunks;
+  const int64_t gcnt = g0 < n_groups ? min(groups_per_chunk + (extra ? 1 : 0), (n_groups - 1 - g0) / gstride + 1) : 0;
+#else
+  const int64_t g0 = int64_t(chunk) * groups_per_chunk + min(int64_t(chunk), extra_groups), gstride = 1;
+  const int64_t gcnt = max(int64_t(0), min(groups_per_chunk + (extra ? 1 : 0), n_groups - g0));
+#endif
 
   const int64_t row_stride = int64_t(n_kv) * HD;
   const float* kb = k + int64_t(g) * HD + 4 * dl;  // float4 column dl + LPR * i of the row
@@ -157,10 +172,14 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
     }
   };
 
-  // The first K/V loads go out before the query loads, so the first HBM round trip is not spent on q alone.
-  int64_t grp = g0;
+  // The first K/V loads go out before the query loads, so the first HBM round trip is not spent on q alone. A
+  // chunk holding an extra group loads its first two groups together: the extra group's round trip overlaps the
+  // first one instead of adding one, so every chunk takes groups_per_chunk round trips.
+  int64_t it = 0;  // iterations done
   Rows ra, rb;
-  if (grp < g1) load(grp, ra);
+  if (gcnt > 0) load(g0, ra);
+  const bool two = extra && gcnt > 1;
+  if (two) load(g0 + gstride, rb);
 
   f32x4 qv[GB][VPL];
   State<VPL> st[GB];
@@ -220,20 +239,25 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
   };
 
 #if NBH_DECODE_PIPELINE
-  while (grp < g1) {
-    const int64_t next = grp + 1;
-    if (next < g1) load(next, rb);
-    compute(ra, grp);
-    if (next >= g1) break;
-    grp = next + 1;
-    if (grp < g1) load(grp, ra);
-    compute(rb, next);
+  while (it < gcnt) {
+    if (it + 1 < gcnt) load(g0 + (it + 1) * gstride, rb);
+    compute(ra, g0 + it * gstride);
+    if (it + 1 >= gcnt) break;
+    if (it + 2 < gcnt) load(g0 + (it + 2) * gstride, ra);
+    compute(rb, g0 + (it + 1) * gstride);
+    it += 2;
   }
 #else
-  while (grp < g1) {
-    compute(ra, grp);
-    ++grp;
-    if (grp < g1) load(grp, ra);
+  if (two) {
+    compute(ra, g0);
+    compute(rb, g0 + gstride);
+    it = 2;
+    if (it < gcnt) load(g0 + it * gstride, ra);
+  }
+  while (it < gcnt) {
+    compute(ra, g0 + it * gstride);
+    ++it;
+    if (it < gcnt) load(g0 + it * gstride, ra);
   }
 #endif
 
@@ -416,6 +440,7 @@ struct Plan {
   int n_sub;                  // head subgroups per KV head
   int n_chunks;               // chunks per (row, head subgroup); each writes one partial per query head
   int64_t groups_per_chunk;   // row groups per chunk
+  int64_t extra_groups;       // the first extra_groups chunks take one group more
 };
 
 // Workgroups of attn_decode_partial<HD, GB> that fit on one CU at once (register and LDS limits), capped at
@@ -441,9 +466,10 @@ int resident_per_cu(int64_t head_dim, int gb) {
        : gb == 4 ? resident_per_cu<128, 4>() : resident_per_cu<128, 8>();
 }
 
-// As many workgroups as fit on the chip at once (one round, no tail of late starters). The row groups per chunk
-// are rounded to the nearest whole number and the chunk count derived from it, so the busiest chunk does that many
-// groups and no more: a context one row past a round size does not cost one workgroup an extra HBM round trip.
+// As many workgroups as fit on the chip at once: one round, no tail of late starters. The row groups are split
+// evenly over min(slots, groups) chunks; the remainder goes one group each to the first chunks, which load that
+// group together with their first one (see attn_decode_partial), so a context one row past a round size costs no
+// workgroup an extra HBM round trip and no workgroup waits for a free slot.
 Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t head_dim, int cu_count) {
   Plan p;
   const int64_t group = n_heads / n_kv;
@@ -455,15 +481,11 @@ Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t h
   const int64_t units = (max_len + step - 1) / step;
   int64_t slots = int64_t(cu_count > 0 ? cu_count : 256) * resident_per_cu(head_dim, p.gb) / (n * n_kv * p.n_sub);
   if (slots < 1) slots = 1;
-  int64_t per = (units + slots / 2) / slots;
-  if (per < 1) per = 1;
-  int64_t chunks = (units + per - 1) / per;
-  if (chunks > kMaxChunks) {
-    per = (units + kMaxChunks - 1) / kMaxChunks;
-    chunks = (units + per - 1) / per;
-  }
+  int64_t chunks = units < slots ? units : slots;
+  if (chunks > kMaxChunks) chunks = kMaxChunks;
   p.n_chunks = int(chunks);
-  p.groups_per_chunk = per;
+  p.groups_per_chunk = units / chunks;
+  p.extra_groups = units % chunks;
   return p;
 }
 
@@ -478,7 +500,7 @@ int launch_decode(const float* q, const float* k, const float* v, float* out, in
 #define NBH_DECODE(GB)                                                                                             \
   e = nbhs_timing::launch(NBHS_K_DECODE_PARTIAL, attn_decode_partial<HD, GB>, grid, dim3(kDecodeThreads), s, q, k, \
                           v, out, ws_o, ws_ml, pos0, int(H), int(KV), group, p.n_sub, p.n_chunks,                   \
-                          p.groups_per_chunk, qscale)
+                          p.groups_per_chunk, p.extra_groups, qscale)
   switch (p.gb) {
     case 1: NBH_DECODE(1); break;
     case 2: NBH_DECODE(2); break;
@@ -507,9 +529,8 @@ int64_t nbhs_attn_decode_workspace(int64_t n, int64_t pos0, int64_t n_heads, int
 }
 
 int64_t nbhs_attn_decode_workspace_bound(int64_t n_heads, int cu_count) {
-  // With T = the workgroup target, a call with n rows splits into chunks <= 1.5 * T / n + 1 (the nearest-whole
-  // rounding of the per-chunk work) whenever it splits at all (T / n >= 2), so n * chunks <= 2 * T; each partial
-  // holds at most 128 + 2 floats per query head.
+  // With T = the workgroup target, a call with n rows that splits at all uses at most T / n chunks per query head,
+  // so n * chunks <= T (the bound keeps twice that); each partial holds at most 128 + 2 floats per query head.
   if (n_heads <= 0) return -1;
   const int64_t slots = int64_t(cu_count > 0 ? cu_count : 256) * NBH_DECODE_WG_PER_CU;
   return n_heads * (2 * slots + 16) * (128 + 2);
