@@ -1,0 +1,124 @@
+"""GPU parity on BASELINE configs 2, 3 and 5 at their full shapes (configs 1 and 4 are in test_gpu_parity.py).
+
+Inputs are seeded N(0,1) from the device's counter-based generator (HipBackend.fill_normal, keyed per config,
+layer, sequence and tensor) and read back for the oracle, so the oracle sees exactly the values the GPU used.
+RoPE'd cache rows are compared bit for bit; attention meets the tolerance in gpu_util against the reference's AVX2
+attention (scalar where the host has no AVX2). The reference computes every query row independently of the others
+in the call, so one oracle call over all of a layer's decode steps equals the steps done one at a time.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from nibble_amd import configs, synth
+from tests.gpu_util import Buffers, assert_parity, bits
+
+pytestmark = pytest.mark.gpu
+
+
+def cpu_attention(q, k, v, pos0, kv):
+    if oracle.have_avx2():
+        return oracle.attention_parallel(q, k, v, pos0, kv, threads=min(16, os.cpu_count() or 1))
+    return oracle.attention_scalar(q, k, v, pos0, kv)
+
+
+def device_normal(be, B, shape, *key):
+    """A device buffer of seeded N(0,1) values and its host copy."""
+    count = int(np.prod(shape))
+    p = B.alloc(count)
+    be.fill_normal(p, count, seed=synth.stream_key(*key))
+    return p, be.download(p, shape)
+
+
+def test_config2_qwen_prefill_24_layers(backend):
+    """Config 2: Qwen2.5-0.5B shape, 2048-token prefill through all 24 layers. Every layer's filled cache (rotated K,
+    raw V) is bit-exact and every output row is within tolerance."""
+    s = configs.QWEN25_05B
+    H, KV, D, n = s.n_heads, s.n_kv_heads, s.head_dim, configs.CFG2["n"]
+    for layer in range(configs.CFG2["layers"]):
+        with Buffers(backend) as B:
+            dq, q = device_normal(backend, B, (n, H, D), 2, layer, configs.T_Q)
+            dk, kn = device_normal(backend, B, (n, KV, D), 2, layer, configs.T_K)
+            dv, vn = device_normal(backend, B, (n, KV, D), 2, layer, configs.T_V)
+            ck, cv, do = B.alloc(n * KV * D), B.alloc(n * KV * D), B.alloc(n * H * D)
+            backend.append_rope(dq, ck, cv, dk, dv, n, 0, H, KV, D, s.rope_base, s.neox, None)
+            backend.attention(dq, ck, cv, do, n, 0, H, KV, D)
+            got = backend.download(do, (n, H, D))
+            gk, gv = backend.download(ck, (n, KV, D)), backend.download(cv, (n, KV, D))
+        kr = oracle.rope(kn.copy(), 0, s.rope_base, s.neox)
+        qr = oracle.rope(q.copy(), 0, s.rope_base, s.neox)
+        assert np.array_equal(bits(gk), bits(kr)), f"layer {layer}: K cache rows"
+        assert np.array_equal(bits(gv), bits(vn)), f"layer {layer}: V cache rows"
+        assert_parity(got, cpu_attention(qr, kr, vn, 0, KV), f"config2 layer {layer}")
+
+
+def test_config3_tinyllama_decode_22_layers_256_steps(backend):
+    """Config 3: TinyLlama-1.1B shape, 256 single-token steps from a 1792-row seeded cache to 2048, all 22 layers.
+    Every step's output is within tolerance; the 256 appended rows are bit-exact in their cache positions and the
+    seeded rows are untouched."""
+    s = configs.TINYLLAMA_11B
+    H, KV, D = s.n_heads, s.n_kv_heads, s.head_dim
+    start, steps = configs.CFG3["start"], configs.CFG3["steps"]
+    cap = start + steps
+    for layer in range(configs.CFG3["layers"]):
+        with Buffers(backend) as B:
+            ck, k0 = device_normal(backend, B, (cap, KV, D), 3, layer, configs.T_KCACHE)
+            cv, v0 = device_normal(backend, B, (cap, KV, D), 3, layer, configs.T_VCACHE)
+            dq, q = device_normal(backend, B, (steps, H, D), 3, layer, configs.T_Q)
+            dk, kn = device_normal(backend, B, (steps, KV, D), 3, layer, configs.T_K)
+            dv, vn = device_normal(backend, B, (steps, KV, D), 3, layer, configs.T_V)
+            do = B.alloc(steps * H * D)
+            for st in range(steps):
+                pos = start + st
+                backend.append_rope(dq.at(st * H * D), ck, cv, dk.at(st * KV * D), dv.at(st * KV * D), 1, pos, H,
+                                    KV, D, s.rope_base, s.neox, None)
+                backend.attention(dq.at(st * H * D), ck, cv, do.at(st * H * D), 1, pos, H, KV, D)
+            got = backend.download(do, (steps, H, D))
+            gk, gv = backend.download(ck, (cap, KV, D)), backend.download(cv, (cap, KV, D))
+        kr = oracle.rope(kn.copy(), start, s.rope_base, s.neox)
+        qr = oracle.rope(q.copy(), start, s.rope_base, s.neox)
+        assert np.array_equal(bits(gk[:start]), bits(k0[:start])), f"layer {layer}: seeded K rows changed"
+        assert np.array_equal(bits(gv[:start]), bits(v0[:start])), f"layer {layer}: seeded V rows changed"
+        assert np.array_equal(bits(gk[start:]), bits(kr)), f"layer {layer}: appended K rows"
+        assert np.array_equal(bits(gv[start:]), bits(vn)), f"layer {layer}: appended V rows"
+        k_all = np.concatenate([k0[:start], kr])
+        v_all = np.concatenate([v0[:start], vn])
+        assert_parity(got, cpu_attention(qr, k_all, v_all, start, KV), f"config3 layer {layer}")
+
+
+@pytest.mark.parametrize("layer", [0, 15])
+def test_config5_ragged_long_context_decode(backend, layer):
+    """Config 5: 16 independent Llama-3.2-1B-shape sequences with ragged cache lengths (log-uniform 1024..131072,
+    seeded), 1% of each cache's K rows scaled x8 to stress the softmax range; two decode steps per sequence, each
+    sequence checked against the reference on that sequence alone (layers 0 and 15 of 16)."""
+    s = configs.LLAMA32_1B
+    H, KV, D = s.n_heads, s.n_kv_heads, s.head_dim
+    ff = s.freq_factors()
+    lengths = configs.cfg5_lengths()
+    assert len(lengths) == 16 and min(lengths) >= 1024 and max(lengths) <= 131072
+    for seq, L in enumerate(lengths):
+        with Buffers(backend) as B:
+            cap = L + 2
+            ck, k0 = device_normal(backend, B, (cap, KV, D), 5, layer, seq, configs.T_KCACHE)
+            cv, v0 = device_normal(backend, B, (cap, KV, D), 5, layer, seq, configs.T_VCACHE)
+            rows = configs.cfg5_scaled_rows(seq, L)
+            k0[rows] *= np.float32(configs.CFG5["scale"])
+            backend.write(ck, k0)
+            dq, q = device_normal(backend, B, (2, H, D), 5, layer, seq, configs.T_Q)
+            dk, kn = device_normal(backend, B, (2, KV, D), 5, layer, seq, configs.T_K)
+            dv, vn = device_normal(backend, B, (2, KV, D), 5, layer, seq, configs.T_V)
+            do = B.alloc(2 * H * D)
+            for st in range(2):
+                backend.append_rope(dq.at(st * H * D), ck, cv, dk.at(st * KV * D), dv.at(st * KV * D), 1, L + st,
+                                    H, KV, D, s.rope_base, s.neox, ff)
+                backend.attention(dq.at(st * H * D), ck, cv, do.at(st * H * D), 1, L + st, H, KV, D)
+            got = backend.download(do, (2, H, D))
+            gk = backend.download(ck.at(L * KV * D), (2, KV, D))
+        kr = oracle.rope(kn.copy(), L, s.rope_base, s.neox, ff)
+        qr = oracle.rope(q.copy(), L, s.rope_base, s.neox, ff)
+        assert np.array_equal(bits(gk), bits(kr)), f"seq {seq}: appended K rows"
+        k_all = np.concatenate([k0[:L], kr])
+        v_all = np.concatenate([v0[:L], vn])
+        assert_parity(got, cpu_attention(qr, k_all, v_all, L, KV), f"config5 layer {layer} seq {seq} (L={L})")
