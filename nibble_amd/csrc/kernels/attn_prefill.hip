@@ -14,8 +14,11 @@
 //    registers for the whole pass. The accumulator puts one query per lane column (lane % 32) and 16 keys per
 //    lane, so the row max needs one cross-half shuffle and the running (m, l) are per-lane scalars.
 //  * O^T = V^T P^T: B = P straight from the S^T accumulator registers (converted to fp16), A = V^T from LDS
-//    ([d][key]), with the key order inside each 16-key MFMA step permuted identically on both operands to match
-//    the accumulator's row interleave. O^T keeps one query per lane too, so rescaling O is a per-lane multiply.
+//    ([d][key]), whose keys are staged in the accumulator's row interleave (vt_key) so that a lane's 8 keys are
+//    one 16-byte read. O^T keeps one query per lane too, so rescaling O is a per-lane multiply.
+//  * K and V^T tiles of 64 keys go from global memory straight into LDS (global_load_lds, no register staging),
+//    XOR-swizzled instead of padded, through a 3-stage ring for head_dim 64: two tiles are in flight while one
+//    is computed, with one barrier per tile.
 //  * GQA packing: the G query heads sharing a KV head are interleaved into the row dimension (packed row
 //    p = t*G + head), so a workgroup's 128 rows span only 128/G positions and each K/V tile in LDS serves all G
 //    heads.
@@ -38,18 +41,52 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBN = 64;          // keys per tile
-constexpr int kRowsPerWave = 32;
+// Query column blocks of 32 per wave: with 2, every K and V^T fragment read from LDS feeds two MFMAs and each wave
+// keeps twice the independent MFMA chains in flight (at twice the accumulator registers).
+#ifndef NBH_PREFILL_QB
+#define NBH_PREFILL_QB 1
+#endif
+constexpr int kQB = NBH_PREFILL_QB;
+constexpr int kRowsPerWave = 32 * kQB;
 #ifndef NBH_PREFILL_WAVES
 #define NBH_PREFILL_WAVES 4
 #endif
 constexpr int kWaves = NBH_PREFILL_WAVES;
 constexpr int kRowsPerBlock = kRowsPerWave * kWaves;
-constexpr int kPad = 8;          // halves of LDS row padding (keeps rows 16-byte aligned, spreads banks)
+constexpr int kPad = 8;          // halves of LDS row padding of the staging transpose (spreads banks)
 // Largest sum of one lane's 32 tile weights accepted without recomputing the tile against a raised shift: every
 // weight is then <= 2^12, far inside fp16 (max 65504).
 constexpr float kPSumMax = 4096.0f;
 
 __device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }  // v_exp_f32; -inf -> 0
+
+// Chunk swizzle of LDS tile rows with CPR 16-byte chunks: rows 0..7 (and 0..15) map a given chunk to distinct
+// chunks, and for 8-chunk (128-byte) rows also the rows of equal parity among 16 consecutive ones (64-bank LDS
+// serves 16 lanes per cycle, and rows r, r + 2 share banks there).
+template <int CPR>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (CPR >= 16) return r & 15;
+  return (r ^ (r >> 3)) & 7;
+}
+
+// 16 bytes from global memory into LDS without passing through registers: lane l of the wave writes bytes
+// [16 l, 16 l + 16) after the wave-uniform LDS address (global_load_lds_dwordx4; completion counts in vmcnt). The
+// builtin is left out of the host compilation pass, where its presence makes clang drop the kernel's launch stub.
+__device__ __forceinline__ void load_lds16(const void* src, void* lds_wave_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, lds_wave_base, 16, 0, 0);
+#endif
+}
+
+// s_waitcnt immediate that waits for at most n outstanding vector-memory loads and nothing else (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int vmcnt_wait(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
+// The S^T accumulator gives lane (query, half hf) the 8 keys {4hf .. 4hf+3, 8+4hf .. 8+4hf+3} of each 16-key step,
+// and that register order is the B operand (P) of the PV MFMA, so its A operand (V^T) must hold the same keys at
+// k = 8hf + e. Staged V^T rows store each 16-key group as keys [0-3, 8-11, 4-7, 12-15]: a lane's 8 keys are then
+// 16 consecutive bytes. vt_key(p) is the key stored at position p of a 64-key tile row.
+__device__ __forceinline__ int vt_key(int p) { return (p & ~15) + (p & 3) + ((p >> 2) & 1) * 8 + ((p >> 3) & 1) * 4; }
 
 // ---- staging: fp32 cache rows -> fp16 K [KV][rows_pad][HD] and transposed V [KV][HD][rows_pad] ----
 template <int HD>
@@ -76,44 +113,51 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(const float* __restrict__
     tr[4 * d4 + 3][r] = (_Float16)y.w;
   }
   __syncthreads();
-  // V^T: each d row of the tile is 64 consecutive keys (128 B).
+  // V^T: each d row of the tile is 64 keys (128 B), stored in the key order of the PV MFMA operand (vt_key).
   for (int idx = threadIdx.x; idx < HD * kBN / 8; idx += 256) {
     const int d = idx / (kBN / 8), c8 = idx % (kBN / 8);
-    *reinterpret_cast<half8_t*>(vt16 + (int64_t(g) * HD + d) * rows_pad + r0 + 8 * c8) =
-        *reinterpret_cast<const half8_t*>(&tr[d][8 * c8]);
+    half8_t x;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = tr[d][vt_key(8 * c8 + e)];
+    *reinterpret_cast<half8_t*>(vt16 + (int64_t(g) * HD + d) * rows_pad + r0 + 8 * c8) = x;
   }
 }
 
-// Occupancy cap (waves per SIMD) the register allocator plans for. The kernel is built with MFMA accumulators in
+// Occupancy (waves per SIMD) the register allocator must reach. The kernel is built with MFMA accumulators in
 // architectural VGPRs (-amdgpu-mfma-vgpr-form, see the Makefile), so the S^T and O^T accumulators both stay
-// resident with no per-tile copies through accumulation registers; head_dim 64 fits 3 waves per SIMD.
+// resident with no per-tile copies through accumulation registers. head_dim 64 is held to 3 waves per SIMD
+// (<= 168 registers, measured fastest: 2 waves with more registers per wave lose more latency hiding than they
+// gain); head_dim 128 needs more registers and runs at what fits.
 #ifndef NBH_PREFILL_WAVES_PER_EU
 #define NBH_PREFILL_WAVES_PER_EU 3
 #endif
 #ifndef NBH_PREFILL_MIN_WAVES_PER_EU
-#define NBH_PREFILL_MIN_WAVES_PER_EU 1
+#define NBH_PREFILL_MIN_WAVES_PER_EU 3
 #endif
 template <int HD>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(NBH_PREFILL_MIN_WAVES_PER_EU, NBH_PREFILL_WAVES_PER_EU)))
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(
+    HD == 64 ? NBH_PREFILL_MIN_WAVES_PER_EU : 1, NBH_PREFILL_WAVES_PER_EU)))
 void attn_prefill_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16,
     float* __restrict__ out, int64_t n, int64_t pos0, int n_heads, int n_kv, int group, int64_t rows_pad,
     int n_tiles, float qscale) {
   constexpr int DC = HD / 16;  // 16-wide d chunks of the S^T contraction
   constexpr int DT = HD / 32;  // 32-row d tiles of O^T
-  // Row strides (halves). K rows are read 16 B per lane, 36 dwords apart: 8 (or 16) consecutive rows cover
-  // distinct 4-bank groups. V^T rows are read 8 B per lane, 34 dwords apart: 17 is odd, so any 16 (or 32)
-  // consecutive rows land on distinct even bank pairs - a 36-dword stride would put rows r and r + 8 on the same
-  // banks and serialise half of every V read.
-  constexpr int KLD = HD + kPad;
-  constexpr int VLD = kBN + 4;
-  constexpr int K_VECS = kBN * HD / 8;  // 16-byte vectors per K tile
-  constexpr int V_VECS = HD * kBN / 8;
+  // K and V^T tiles live in LDS unpadded, one row of 16-byte chunks per key (K) or per dimension (V^T), with chunk
+  // x of row r stored at chunk x ^ swz(r). The fragment reads (16 B per lane, one row per lane) then hit distinct
+  // bank groups for any 8 consecutive rows (32 banks) or 16 (64 banks), and the tiles can be filled by
+  // global_load_lds, which writes each wave's 64 lanes x 16 B to one contiguous kilobyte of LDS: the swizzle is
+  // applied on the global side, by choosing which chunk each lane fetches.
+  constexpr int KCPR = HD / 8;    // 16-byte chunks per K row
+  constexpr int VCPR = kBN / 8;   // 16-byte chunks per V^T row
   constexpr int THREADS = kWaves * 64;
-  constexpr int K_PER_T = K_VECS / THREADS;
-  constexpr int V_PER_T = V_VECS / THREADS;
-  __shared__ _Float16 ks[2][kBN][KLD];
-  __shared__ _Float16 vs[2][HD][VLD];
+  constexpr int K_LD = kBN * KCPR / THREADS;  // global_load_lds instructions per wave per K tile
+  constexpr int V_LD = HD * VCPR / THREADS;   // ... per V^T tile
+  static_assert(K_LD * THREADS == kBN * KCPR && V_LD * THREADS == HD * VCPR, "tiles split evenly over lanes");
+  // Pipeline depth: tiles in LDS at once (the current one and those being fetched).
+  constexpr int kStages = HD == 64 ? 3 : 2;
+  __shared__ _Float16 ks[kStages][kBN * HD];
+  __shared__ _Float16 vs[kStages][HD * kBN];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ql = lane & 31, hf = lane >> 5;
@@ -123,11 +167,18 @@ void attn_prefill_kernel(
   const int64_t P = n * group;
   const int64_t pb0 = int64_t(tile) * kRowsPerBlock;
   const int64_t wp0 = pb0 + wave * kRowsPerWave;
-  const int64_t p = wp0 + ql;
-  const bool active = p < P;
-  const int64_t t = active ? p / group : 0;
-  const int head = g * group + (active ? int(p % group) : 0);
-  const int64_t qpos = pos0 + t;
+  // The lane's query of column block qb: packed row wp0 + 32 qb + ql.
+  bool active[kQB];
+  int64_t t[kQB], qpos[kQB];
+  int head[kQB];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    const int64_t p = wp0 + 32 * qb + ql;
+    active[qb] = p < P;
+    t[qb] = active[qb] ? p / group : 0;
+    head[qb] = g * group + (active[qb] ? int(p % group) : 0);
+    qpos[qb] = pos0 + t[qb];
+  }
 
   const int64_t p_last = min(pb0 + kRowsPerBlock, P) - 1;
   const int64_t kend = pos0 + p_last / group + 1;  // the block's keys: [0, kend)
@@ -136,173 +187,226 @@ void attn_prefill_kernel(
   const int64_t wave_kend = wave_active ? pos0 + (min(wp0 + kRowsPerWave, P) - 1) / group + 1 : 0;
   const int64_t wave_kfull = wave_active ? pos0 + wp0 / group + 1 : 0;  // keys every row of the wave sees
 
-  // Q fragment (B operand of S^T): query ql, d = 16c + 8hf .. +8.
-  half8_t qf[DC];
-  {
-    const float* qrow = q + (t * n_heads + head) * HD;
+  // Q fragments (B operand of S^T): query of block qb, d = 16c + 8hf .. +8.
+  half8_t qf[kQB][DC];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    const float* qrow = q + (t[qb] * n_heads + head[qb]) * HD;
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
       float4 a = make_float4(0.f, 0.f, 0.f, 0.f), bb = a;
-      if (active) {
+      if (active[qb]) {
         a = *reinterpret_cast<const float4*>(qrow + 16 * c + 8 * hf);
         bb = *reinterpret_cast<const float4*>(qrow + 16 * c + 8 * hf + 4);
       }
-      qf[c] = half8_t{(_Float16)(a.x * qscale), (_Float16)(a.y * qscale), (_Float16)(a.z * qscale),
-                      (_Float16)(a.w * qscale), (_Float16)(bb.x * qscale), (_Float16)(bb.y * qscale),
-                      (_Float16)(bb.z * qscale), (_Float16)(bb.w * qscale)};
+      qf[qb][c] = half8_t{(_Float16)(a.x * qscale), (_Float16)(a.y * qscale), (_Float16)(a.z * qscale),
+                          (_Float16)(a.w * qscale), (_Float16)(bb.x * qscale), (_Float16)(bb.y * qscale),
+                          (_Float16)(bb.z * qscale), (_Float16)(bb.w * qscale)};
     }
   }
 
-  floatx16 oacc[DT];
+  floatx16 oacc[kQB][DT];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+  for (int qb = 0; qb < kQB; ++qb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
-  // m_sh: the query's softmax shift (log2 domain); mneg: 16 copies of -m_sh, the accumulator block S^T starts from.
-  float m_sh = 0.f, l_run = 0.f;
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[qb][dt][r] = 0.f;
+  // m_sh: the query's softmax shift (log2 domain). With one query block the subtraction is folded into the S^T
+  // MFMAs: their accumulator starts from mneg, 16 copies of -m_sh. With two blocks the registers are scarcer and
+  // the shift is subtracted on the VALU instead, which has slack.
+  constexpr bool kFold = kQB == 1;
+  float m_sh[kQB], l_run[kQB];
   floatx16 mneg;
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    m_sh[qb] = 0.f;
+    l_run[qb] = 0.f;
+  }
 #pragma unroll
   for (int r = 0; r < 16; ++r) mneg[r] = 0.f;
 
   const _Float16* kg = k16 + int64_t(g) * rows_pad * HD;
   const _Float16* vg = vt16 + int64_t(g) * HD * rows_pad;
-  half8_t kreg[K_PER_T], vreg[V_PER_T];
-  auto load_tile = [&](int kt) {
+  // Asynchronous fetch of key tile kt into LDS stage kt % kStages: each wave fills its share of 1 KB pieces.
+  auto fetch = [&](int kt) {
+    const int st = kt % kStages;
 #pragma unroll
-    for (int i = 0; i < K_PER_T; ++i) {
-      const int ci = threadIdx.x + THREADS * i;
-      kreg[i] = *reinterpret_cast<const half8_t*>(kg + (int64_t(kt) * kBN) * HD + int64_t(ci) * 8);
+    for (int i = 0; i < K_LD; ++i) {
+      const int piece = i * kWaves + wave, slot = piece * 64 + lane;  // 16-byte slot of the tile
+      const int r = slot / KCPR, x = (slot % KCPR) ^ swz<KCPR>(r);
+      load_lds16(kg + (int64_t(kt) * kBN + r) * HD + 8 * x, &ks[st][piece * 512]);
     }
 #pragma unroll
-    for (int i = 0; i < V_PER_T; ++i) {
-      const int ci = threadIdx.x + THREADS * i;
-      const int d = ci / (kBN / 8), c8 = ci % (kBN / 8);
-      vreg[i] = *reinterpret_cast<const half8_t*>(vg + int64_t(d) * rows_pad + int64_t(kt) * kBN + 8 * c8);
+    for (int i = 0; i < V_LD; ++i) {
+      const int piece = i * kWaves + wave, slot = piece * 64 + lane;
+      const int d = slot / VCPR, x = (slot % VCPR) ^ swz<VCPR>(d);
+      load_lds16(vg + int64_t(d) * rows_pad + int64_t(kt) * kBN + 8 * x, &vs[st][piece * 512]);
     }
   };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < K_PER_T; ++i) {
-      const int ci = threadIdx.x + THREADS * i;
-      const int r = ci / (HD / 8), c8 = ci % (HD / 8);
-      *reinterpret_cast<half8_t*>(&ks[buf][r][8 * c8]) = kreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < V_PER_T; ++i) {
-      const int ci = threadIdx.x + THREADS * i;
-      const int d = ci / (kBN / 8), c8 = ci % (kBN / 8);
-      // V^T rows are 8-byte aligned (VLD = 68 halves): two 8-byte stores
-      *reinterpret_cast<half4_t*>(&vs[buf][d][8 * c8]) = half4_t{vreg[i][0], vreg[i][1], vreg[i][2], vreg[i][3]};
-      *reinterpret_cast<half4_t*>(&vs[buf][d][8 * c8 + 4]) = half4_t{vreg[i][4], vreg[i][5], vreg[i][6], vreg[i][7]};
-    }
+  // Fragment reads: row r, logical chunk x of a stage.
+  auto k_frag = [&](int st, int r, int x) {
+    return *reinterpret_cast<const half8_t*>(&ks[st][r * HD + 8 * (x ^ swz<KCPR>(r))]);
+  };
+  auto v_frag = [&](int st, int d, int x) {
+    return *reinterpret_cast<const half8_t*>(&vs[st][d * kBN + 8 * (x ^ swz<VCPR>(d))]);
   };
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
+  // Tiles 0 .. kStages-2 are fetched ahead; step kt waits for its own tile (the later ones may still be in flight),
+  // then one barrier both publishes tile kt to every wave and certifies that all waves are done with tile kt - 1,
+  // whose stage the fetch of tile kt + kStages - 1 then refills. The barrier is the bare s_barrier: the LDS writes
+  // are ordered by the wait on vmcnt (global_load_lds completes when its data is in LDS), and a fence here would
+  // also wait for the fetches that are meant to stay in flight.
+#pragma unroll
+  for (int kt = 0; kt < kStages - 1; ++kt)
+    if (kt < ntk) fetch(kt);
   for (int kt = 0; kt < ntk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < ntk) load_tile(kt + 1);
+    const int cur = kt % kStages;
+    constexpr int ahead = (kStages - 2) * (K_LD + V_LD);  // this wave's loads of the tiles after kt
+    if (kStages > 2 && kt + 1 < ntk)
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait(ahead));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + kStages - 1 < ntk) fetch(kt + kStages - 1);
     if (wave_active && int64_t(kt) * kBN < wave_kend) {
-      // S^T - m for the tile's two 32-key halves: the first MFMA of each chain starts from the accumulator block
-      // mneg (every entry -m_sh, the lane's query shift), so the subtraction costs no instruction. The two chains
-      // are interleaved so consecutive MFMAs do not wait on each other's results.
-      floatx16 s[2];
+      // S^T for the tile's two 32-key halves and every query block; each K fragment read from LDS serves all
+      // blocks, and the chains are interleaved so consecutive MFMAs do not wait on each other's results. The
+      // raised wave priority keeps the MFMA pipe fed while other waves of the SIMD run their softmax VALU work.
+      floatx16 s[kQB][2];
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int c = 0; c < DC; ++c)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const half8_t a = *reinterpret_cast<const half8_t*>(&ks[cur][kk * 32 + ql][16 * c + 8 * hf]);
-          s[kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], c == 0 ? mneg : s[kk], 0, 0, 0);
+          const half8_t a = k_frag(cur, kk * 32 + ql, 2 * c + hf);
+#pragma unroll
+          for (int qb = 0; qb < kQB; ++qb) {
+            floatx16 c0;
+            if (c == 0) {
+              if constexpr (kFold) {
+                c0 = mneg;
+              } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) c0[r] = 0.f;
+              }
+            } else {
+              c0 = s[qb][kk];
+            }
+            s[qb][kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[qb][c], c0, 0, 0, 0);
+          }
         }
+      __builtin_amdgcn_s_setprio(0);
       // Causal mask (and inactive rows) only where some key of the tile lies past the wave's first row.
       if (int64_t(kt) * kBN + kBN > wave_kfull) {
-        // keys of this tile past the query's position (relative to the tile start; inactive rows mask all)
-        const int64_t rel64 = active ? qpos - int64_t(kt) * kBN : -1;
-        const int rel = int(rel64 < kBN ? rel64 : kBN);
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
+        for (int qb = 0; qb < kQB; ++qb) {
+          // keys of this tile past the query's position (relative to the tile start; inactive rows mask all)
+          const int64_t rel64 = active[qb] ? qpos[qb] - int64_t(kt) * kBN : -1;
+          const int rel = int(rel64 < kBN ? rel64 : kBN);
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (kk * 32 + 8 * (r / 4) + 4 * hf + (r % 4) > rel) s[kk][r] = -INFINITY;
+          for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if (kk * 32 + 8 * (r / 4) + 4 * hf + (r % 4) > rel) s[qb][kk][r] = -INFINITY;
+        }
       }
       // P = exp2(S - m_sh) in fp16 (the MFMA B operand) and the lane's sum of it, taken from the same fp16 values
       // with v_dot2 so the normaliser matches the weights the MFMA multiplies.
-      half8_t pb[4];
-      float l_tile = 0.f;
+      half8_t pb[kQB][4];
+      float l_tile[kQB];
       const half2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
-      auto exps = [&](float shift) {
-        l_tile = 0.f;
+      auto exps = [&](int qb, float shift) {
+        l_tile[qb] = 0.f;
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) pb[kc][e] = (_Float16)exp2_raw(s[kc >> 1][8 * (kc & 1) + e] - shift);
+          for (int e = 0; e < 8; ++e)
+            pb[qb][kc][e] = (_Float16)exp2_raw(s[qb][kc >> 1][8 * (kc & 1) + e] - shift);
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
           for (int e = 0; e < 8; e += 2)
-            l_tile = __builtin_amdgcn_fdot2(half2_t{pb[kc][e], pb[kc][e + 1]}, ones, l_tile, false);
+            l_tile[qb] = __builtin_amdgcn_fdot2(half2_t{pb[qb][kc][e], pb[qb][kc][e + 1]}, ones, l_tile[qb], false);
       };
       // The shift is not raised per tile: the weights are computed against the current one, and only when some
       // lane's sum leaves (0, kPSumMax] - a score grew past the shift by ~12 (log2), or inf/NaN from an fp16
       // overflow - does the wave take the slow path below (always on its first tile, where no shift exists yet).
       bool slow = kt == 0;
       if (!slow) {
-        exps(0.0f);
-        slow = __builtin_amdgcn_ballot_w64(!(l_tile <= kPSumMax)) != 0;
+        bool bad = false;
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+          exps(qb, kFold ? 0.0f : m_sh[qb]);
+          bad = bad || !(l_tile[qb] <= kPSumMax);
+        }
+        slow = __builtin_amdgcn_ballot_w64(bad) != 0;
       }
       if (slow) {
-        float mt = -INFINITY;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
+        for (int qb = 0; qb < kQB; ++qb) {
+          const float base = kFold ? 0.0f : m_sh[qb];  // s holds S - base
+          float mt = -INFINITY;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kk][r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        // first tile: shift to the tile max (0 if every key is masked); later: raise by the excess only
-        const float d = kt == 0 ? (mt == -INFINITY ? 0.0f : mt) : fmaxf(mt, 0.0f);
-        exps(d);
-        if (kt != 0) {
-          const float corr = exp2_raw(-d);
-          l_run *= corr;
+          for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[qb][kk][r]);
+          mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) - base;  // tile max relative to the current shift
+          // first tile: shift to the tile max (0 if every key is masked); later: raise by the excess only
+          const float d = kt == 0 ? (mt == -INFINITY ? 0.0f : mt) : fmaxf(mt, 0.0f);
+          exps(qb, base + d);
+          if (kt != 0) {
+            const float corr = exp2_raw(-d);
+            l_run[qb] *= corr;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) oacc[qb][dt][r] *= corr;
+          }
+          m_sh[qb] += d;
+          if constexpr (kFold) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mneg[r] = -m_sh[qb];
+          }
         }
-        m_sh += d;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mneg[r] = -m_sh;
       }
-      l_run += l_tile;
-      // O^T += V^T P^T over 4 steps of 16 keys; the DT output tiles are independent chains.
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) l_run[qb] += l_tile[qb];
+      // O^T += V^T P^T over 4 steps of 16 keys; each V^T fragment read from LDS serves every query block, and the
+      // DT x kQB output tiles are independent chains.
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const _Float16* vrow = &vs[cur][32 * dt + ql][16 * kc + 4 * hf];
-          const half4_t lo = *reinterpret_cast<const half4_t*>(vrow);
-          const half4_t hi = *reinterpret_cast<const half4_t*>(vrow + 8);
-          const half8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kc], oacc[dt], 0, 0, 0);
+          const half8_t a = v_frag(cur, 32 * dt + ql, 2 * kc + hf);
+#pragma unroll
+          for (int qb = 0; qb < kQB; ++qb)
+            oacc[qb][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[qb][kc], oacc[qb][dt], 0, 0, 0);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
     }
-    if (kt + 1 < ntk) store_tile(cur ^ 1);
-    __syncthreads();
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if (active) {
-    const float inv = 1.0f / l_tot;
-    float* orow = out + (t * n_heads + head) * HD;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int qb = 0; qb < kQB; ++qb) {
+    const float l_tot = l_run[qb] + __shfl_xor(l_run[qb], 32, 64);
+    if (active[qb]) {
+      const float inv = 1.0f / l_tot;
+      float* orow = out + (t[qb] * n_heads + head[qb]) * HD;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = 32 * dt + 8 * i + 4 * hf;
-        *reinterpret_cast<float4*>(orow + d) = make_float4(oacc[dt][4 * i] * inv, oacc[dt][4 * i + 1] * inv,
-                                                           oacc[dt][4 * i + 2] * inv, oacc[dt][4 * i + 3] * inv);
-      }
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 32 * dt + 8 * i + 4 * hf;
+          *reinterpret_cast<float4*>(orow + d) =
+              make_float4(oacc[qb][dt][4 * i] * inv, oacc[qb][dt][4 * i + 1] * inv, oacc[qb][dt][4 * i + 2] * inv,
+                          oacc[qb][dt][4 * i + 3] * inv);
+        }
+    }
   }
 }
 
