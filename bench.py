@@ -114,9 +114,9 @@ PROBE_DECODE_STEPS = 8
 
 def probe():
     """Short run for one `rocprofv3 --pmc` pass: layer 0 of config 4 only. Dispatch order: fill kernels, then
-    PROBE_DECODE_STEPS decode steps at 32768+s ctx (append+rope, split-context partial, combine), then one
-    COPY_CAL_BYTES device copy (the calibration kernel of known size), then the 8192-row prefill (append+rope, fp16
-    staging, fp32 prefix rows, MFMA kernel). Counter values per dispatch do not depend on the data."""
+    PROBE_DECODE_STEPS decode steps at 32768+s ctx (K/V append with RoPE, split-context partial, combine), then one
+    COPY_CAL_BYTES device copy (the calibration kernel of known size), then the 8192-row prefill (K/V append fused
+    with the fp16 staging, fp32 prefix rows, MFMA kernel). Counter values per dispatch do not depend on the data."""
     shape = configs.LLAMA32_1B
     H, KV, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
     base, neox, ff = shape.rope_base, shape.neox, shape.freq_factors()
@@ -141,11 +141,9 @@ def probe():
         be.fill_normal(p_, n_, seed=5)
     be.sync()
     for s in range(PROBE_DECODE_STEPS):
-        be.append_rope(qd, ck, cv, kd, vd, 1, ctx + s, H, KV, D, base, neox, ff)
-        be.attention(qd, ck, cv, out, 1, ctx + s, H, KV, D)
+        be.append_rope_attention(qd, ck, cv, kd, vd, out, 1, ctx + s, H, KV, D, base, neox, ff)
     be.copy(dst, src, cal_floats)
-    be.append_rope(q_pre, ck, cv, k_pre, v_pre, n_pre, 0, H, KV, D, base, neox, ff)
-    be.attention(q_pre, ck, cv, out, n_pre, 0, H, KV, D)
+    be.append_rope_attention(q_pre, ck, cv, k_pre, v_pre, out, n_pre, 0, H, KV, D, base, neox, ff)
     be.sync()
     be.close()
     log("probe done")
@@ -270,21 +268,22 @@ def main():
     be.fill_normal(kd, max_steps * NL * row, seed=(4 << 32) | (1 << 20) | configs.T_K)
     be.fill_normal(vd, max_steps * NL * row, seed=(4 << 32) | (1 << 20) | configs.T_V)
     out_dec = be.alloc(H * D)
-    q_pre0_host = be.download(q_pre[0], (n_pre, H, D))  # layer-0 queries before any rotation (CPU baseline)
+    q_pre0_host = be.download(q_pre[0], (n_pre, H, D))  # layer-0 queries (CPU baseline sample)
     be.sync()
 
+    # One layer = KV append with RoPE + attention, through the fused entry point (q rotated on load; on the prefill
+    # route the append shares one pass with the fp16 staging).
     def prefill_pass():
         for l in range(NL):
-            be.append_rope(q_pre[l], ck[l], cv[l], k_pre[l], v_pre[l], n_pre, 0, H, KV, D, base, neox, ff)
-            be.attention(q_pre[l], ck[l], cv[l], out_pre, n_pre, 0, H, KV, D)
+            be.append_rope_attention(q_pre[l], ck[l], cv[l], k_pre[l], v_pre[l], out_pre, n_pre, 0, H, KV, D, base,
+                                     neox, ff)
 
     def decode_step(s):
         pos0 = ctx + s
         for l in range(NL):
             i = s * NL + l
-            be.append_rope(qd.at(i * H * D), ck[l], cv[l], kd.at(i * row), vd.at(i * row), 1, pos0, H, KV, D,
-                           base, neox, ff)
-            be.attention(qd.at(i * H * D), ck[l], cv[l], out_dec, 1, pos0, H, KV, D)
+            be.append_rope_attention(qd.at(i * H * D), ck[l], cv[l], kd.at(i * row), vd.at(i * row), out_dec, 1,
+                                     pos0, H, KV, D, base, neox, ff)
 
     # ---------------- prefill (also fills cache rows 0..8191 of every layer)
     prefill_pass()  # warm-up
@@ -339,7 +338,7 @@ def main():
     mfma_tflops = mfma_flops * mfma_n / (mfma_ms * 1e-3) / 1e12
     log(f"kernels: decode partial avg {part_ms / part_n * 1e3:.2f} us ({dec_kernel_gbs:.0f} GB/s), combine avg "
         f"{comb_ms / max(comb_n, 1) * 1e3:.2f} us, append+rope avg {app_ms / max(app_n, 1) * 1e3:.2f} us; "
-        f"prefill mfma avg {mfma_ms / mfma_n:.3f} ms ({mfma_tflops:.1f} TFLOP/s), stage avg "
+        f"prefill mfma avg {mfma_ms / mfma_n:.3f} ms ({mfma_tflops:.1f} TFLOP/s), append+stage avg "
         f"{stage_ms / max(stage_n, 1) * 1e3:.1f} us, fp32 prefix avg {pref32_ms / max(pref32_n, 1) * 1e3:.1f} us")
 
     result = {
@@ -378,7 +377,7 @@ def main():
         "kernels_us": {"decode_combine": round(comb_ms / max(comb_n, 1) * 1e3, 3),
                        "append_rope_decode": round(app_ms / max(app_n, 1) * 1e3, 3),
                        "append_rope_prefill": round(app2_ms / max(app2_n, 1) * 1e3, 2),
-                       "stage_kv_f16": round(stage_ms / max(stage_n, 1) * 1e3, 2),
+                       "append_stage_kv_f16": round(stage_ms / max(stage_n, 1) * 1e3, 2),
                        "prefill_fp32_prefix": round(pref32_ms / max(pref32_n, 1) * 1e3, 2)},
     }
     if not args.no_cpu_baseline:

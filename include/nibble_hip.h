@@ -83,6 +83,16 @@ int nbh_backend_append_rope(nbh_backend* be, float* q, float* k_cache, float* v_
                             const float* v_new, int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads,
                             int64_t head_dim, float freq_base, int neox, const float* freq_factors);
 
+/* KV-cache append with RoPE fused into attention: the per-layer sequence of src/model/transformer.cpp:171-202
+ * (K/V rows into cache rows pos0.., rope(q), rope(k rows), Backend::attention at backend.h:68-69) in one call.
+ * Results are bit-identical to nbh_backend_append_rope followed by nbh_backend_attention, except that q is read
+ * unrotated and left unchanged: it is rotated in registers as the attention kernels load it, and on the prefill
+ * (MFMA) route the K/V append shares one pass with the fp16 operand staging. out [n, n_heads, head_dim]. */
+int nbh_backend_append_rope_attention(nbh_backend* be, const float* q, float* k_cache, float* v_cache,
+                                      const float* k_new, const float* v_new, float* out, int64_t n, int64_t pos0,
+                                      int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float freq_base, int neox,
+                                      const float* freq_factors);
+
 /* Extension of Backend::reserve for shapes ReserveParams does not carry: sizes the prefill operand staging
  * (n_kv_heads x head_dim at the reserved n_ctx) so that the first prefill allocates nothing. */
 int nbh_backend_reserve_attention(nbh_backend* be, int64_t n_kv_heads, int64_t head_dim);

@@ -58,7 +58,8 @@ int nbhs_rope_f32(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_
 /* KV-cache append fused with RoPE (transformer.cpp:171-198: K/V rows land in cache rows pos0.., then rope(q) and
  * rope(k) in place): q[n, n_heads, head_dim] is rotated in place; cache_k rows pos0..pos0+n-1 receive
  * rope(k_new) and cache_v rows receive v_new, for caches laid out [rows, n_kv_heads, head_dim]. Bit-identical to
- * copying the rows and calling nbhs_rope_f32 on q and on the cache rows. */
+ * copying the rows and calling nbhs_rope_f32 on q and on the cache rows. q = NULL with n_heads = 0 appends the
+ * K/V rows only. */
 int nbhs_append_rope_f32(float* q, float* cache_k, float* cache_v, const float* k_new, const float* v_new, int64_t n,
                          int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const float* cs_table,
                          int64_t table_rows, int neox, nbhs_stream s);
@@ -75,9 +76,13 @@ int64_t nbhs_attn_decode_workspace(int64_t n, int64_t pos0, int64_t n_heads, int
 /* Upper bound of nbhs_attn_decode_workspace over every call shape with n_heads query heads (any context length,
  * row count, KV-head count and head_dim), for sizing the workspace once. */
 int64_t nbhs_attn_decode_workspace_bound(int64_t n_heads, int cu_count);
+/* q_rope_cs: NULL when q is already rotated; otherwise the RoPE (cos, sin) table (as for nbhs_rope_f32, covering
+ * positions pos0..pos0+n-1; q_rope_rows rows) and q is given unrotated and rotated on load, bit-identically to
+ * rotating it first (head_dim 64 and 128 only). */
 int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
                          int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float* workspace,
-                         int64_t workspace_floats, int cu_count, nbhs_stream s);
+                         int64_t workspace_floats, int cu_count, const float* q_rope_cs, int64_t q_rope_rows,
+                         int q_rope_neox, nbhs_stream s);
 
 /* Operand staging for the MFMA prefill: cache rows [0, rows) of k and v [rows, n_kv_heads, head_dim] fp32 are
  * rounded to fp16 into k16 [n_kv_heads, rows_pad, head_dim] and vt16 [n_kv_heads, head_dim, rows_pad]
@@ -85,13 +90,20 @@ int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* 
 int64_t nbhs_prefill_staging_halves(int64_t rows, int64_t n_kv_heads, int64_t head_dim); /* per tensor */
 int nbhs_stage_kv_f16(const float* k, const float* v, void* k16, void* vt16, int64_t rows, int64_t n_kv_heads,
                       int64_t head_dim, nbhs_stream s);
+/* KV append fused with the staging: cache rows pos0..pos0+n-1 receive rope(k_new) and v_new (as
+ * nbhs_append_rope_f32 with no q), and k16 / vt16 are staged for rows [0, pos0+n) as nbhs_stage_kv_f16 would
+ * after the append - one pass instead of two over the new rows. */
+int nbhs_append_stage_kv_f16(float* cache_k, float* cache_v, const float* k_new, const float* v_new, int64_t n,
+                             int64_t pos0, int64_t n_kv_heads, int64_t head_dim, const float* cs_table,
+                             int64_t table_rows, int neox, void* k16, void* vt16, nbhs_stream s);
 
 /* Causal GQA attention for n query rows at positions pos0.. on gfx950 MFMA (v_mfma_f32_32x32x16_f16): Q rounded
  * to fp16 after scaling by log2(e)/sqrt(head_dim), K/V from the staged fp16 copies, softmax and accumulators in
- * fp32. head_dim 64 or 128. The staged copies must cover rows [0, pos0+n). */
+ * fp32. head_dim 64 or 128. The staged copies must cover rows [0, pos0+n). q_rope_cs as for
+ * nbhs_attn_decode_f32. */
 int nbhs_attn_prefill_mfma(const float* q, const void* k16, const void* vt16, float* out, int64_t n, int64_t pos0,
                            int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t staged_rows_pad,
-                           nbhs_stream s);
+                           const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, nbhs_stream s);
 
 /* Synthetic N(0,1)*scale data for benchmarks: counter-based (SplitMix64 of seed and index), Box-Muller in fp32. */
 int nbhs_fill_normal_f32(float* dst, int64_t count, uint64_t seed, float scale, nbhs_stream s);

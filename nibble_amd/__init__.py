@@ -35,6 +35,8 @@ _SIGNATURES = {
     "nbh_backend_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, _I, _I, _I, _I, _I]),
     "nbh_backend_append_rope": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, _I, _I, _I, _I,
                                         _I, c_float, c_int, c_void_p]),
+    "nbh_backend_append_rope_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                                  c_void_p, _I, _I, _I, _I, _I, c_float, c_int, c_void_p]),
     "nbh_backend_reserve_attention": (c_int, [c_void_p, _I, _I]),
     "nbh_backend_reserve_rope": (c_int, [c_void_p, _I, c_float, c_int, c_void_p]),
     "nbh_backend_sync": (c_int, [c_void_p]),
@@ -144,6 +146,15 @@ class HipBackend:
                                              c_void_p(int(v_cache)), c_void_p(int(k_new)), c_void_p(int(v_new)), n,
                                              pos0, n_heads, n_kv_heads, head_dim, freq_base, int(bool(neox)),
                                              None if ff is None else _host_ptr(ff)))
+
+    def append_rope_attention(self, q, k_cache, v_cache, k_new, v_new, out, n, pos0, n_heads, n_kv_heads, head_dim,
+                              freq_base, neox, freq_factors=None):
+        """append_rope then attention in one call, q read unrotated and left unchanged (bit-identical results)."""
+        ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
+        _check(lib().nbh_backend_append_rope_attention(
+            self._h, c_void_p(int(q)), c_void_p(int(k_cache)), c_void_p(int(v_cache)), c_void_p(int(k_new)),
+            c_void_p(int(v_new)), c_void_p(int(out)), n, pos0, n_heads, n_kv_heads, head_dim, freq_base,
+            int(bool(neox)), None if ff is None else _host_ptr(ff)))
 
     def reserve_attention(self, n_kv_heads: int, head_dim: int):
         _check(lib().nbh_backend_reserve_attention(self._h, n_kv_heads, head_dim))

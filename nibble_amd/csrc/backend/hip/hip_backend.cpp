@@ -271,44 +271,107 @@ void HipBackend::append_rope(float* q, float* k_cache, float* v_cache, const flo
 
 void HipBackend::attention(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
                            int64_t n_heads, int64_t n_kv_heads, int64_t head_dim) {
+  check_attention_args(q, k, v, out, n, pos0, n_heads, n_kv_heads, head_dim, "attention");
+  run_attention(q, k, v, out, n, pos0, n_heads, n_kv_heads, head_dim, nullptr, 0, false, nullptr, nullptr);
+}
+
+void HipBackend::append_rope_attention(const float* q, float* k_cache, float* v_cache, const float* k_new,
+                                       const float* v_new, float* out, int64_t n, int64_t pos0, int64_t n_heads,
+                                       int64_t n_kv_heads, int64_t head_dim, const RopeParams& p) {
+  if (head_dim % 2 != 0) throw Error("append_rope_attention: head_dim must be even, got " + str(head_dim));
+  check_attention_args(q, k_cache, v_cache, out, n, pos0, n_heads, n_kv_heads, head_dim, "append_rope_attention");
+  int64_t kvf;
+  if (overflow_mul(n * n_kv_heads, head_dim, &kvf)) throw Error("append_rope_attention: size overflows");
+  check_range(k_new, kvf, "append_rope_attention", "k_new");
+  check_range(v_new, kvf, "append_rope_attention", "v_new");
+  int64_t rows;
+  const float* table = rope_table(head_dim, pos0 + n, p, &rows);
+  if (head_dim != 64 && head_dim != 128) {
+    // No rotation-on-load for other head sizes: rotate a copy of q.
+    int64_t qf = n * n_heads * head_dim;
+    ensure(copy_tmp_, copy_tmp_bytes_, size_t(qf) * sizeof(float));
+    check(nbhs_memcpy_d2d(copy_tmp_, q, size_t(qf) * sizeof(float), stream_), "append_rope_attention");
+    check(nbhs_append_rope_f32(copy_tmp_, k_cache, v_cache, k_new, v_new, n, pos0, n_heads, n_kv_heads, head_dim,
+                               table, rows, p.neox ? 1 : 0, stream_),
+          "append_rope_attention (append)");
+    run_attention(copy_tmp_, k_cache, v_cache, out, n, pos0, n_heads, n_kv_heads, head_dim, nullptr, 0, false,
+                  nullptr, nullptr);
+    return;
+  }
+  AppendRows app{k_new, v_new};
+  run_attention(q, k_cache, v_cache, out, n, pos0, n_heads, n_kv_heads, head_dim, table, rows, p.neox, &app, &p);
+}
+
+void HipBackend::check_attention_args(const float* q, const float* k, const float* v, const float* out, int64_t n,
+                                      int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                      const char* op) const {
   if (n <= 0 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || head_dim <= 0 ||
       head_dim > 256)
-    throw Error("attention: invalid shape n=" + str(n) + " pos0=" + str(pos0) + " n_heads=" + str(n_heads) +
+    throw Error(std::string(op) + ": invalid shape n=" + str(n) + " pos0=" + str(pos0) + " n_heads=" + str(n_heads) +
                 " n_kv_heads=" + str(n_kv_heads) + " head_dim=" + str(head_dim) +
                 " (n_heads must be a multiple of n_kv_heads, head_dim at most 256)");
   int64_t qf, cachef;
   if (overflow_mul(n * n_heads, head_dim, &qf) || overflow_mul((pos0 + n) * n_kv_heads, head_dim, &cachef))
-    throw Error("attention: size overflows");
-  check_range(q, qf, "attention", "q");
-  check_range(out, qf, "attention", "out");
-  check_range(k, cachef, "attention", "k");
-  check_range(v, cachef, "attention", "v");
+    throw Error(std::string(op) + ": size overflows");
+  check_range(q, qf, op, "q");
+  check_range(out, qf, op, "out");
+  check_range(k, cachef, op, "k");
+  check_range(v, cachef, op, "v");
+}
 
+// Attention over cache rows 0..pos0+t for q rows t. With rope_table set, q is unrotated and rotated on load, and
+// with `app` set the rows pos0..pos0+n-1 are appended first (rope(k_new), v_new) - fused with the fp16 staging
+// on the MFMA route.
+void HipBackend::run_attention(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                               int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const float* rope_table,
+                               int64_t rope_rows, bool neox, const AppendRows* app, const RopeParams* rp) {
+  (void)rp;
   auto decode_rows = [&](const float* qq, float* oo, int64_t rows, int64_t p0) {
     const int64_t ws = nbhs_attn_decode_workspace(rows, p0, n_heads, n_kv_heads, head_dim, cu_count_);
     if (ws < 0) throw Error("attention: invalid decode shape");
     ensure(decode_ws_, decode_ws_bytes_, size_t(ws) * sizeof(float));
     check(nbhs_attn_decode_f32(qq, k, v, oo, rows, p0, n_heads, n_kv_heads, head_dim, decode_ws_,
-                               int64_t(decode_ws_bytes_ / sizeof(float)), cu_count_, stream_),
+                               int64_t(decode_ws_bytes_ / sizeof(float)), cu_count_, rope_table, rope_rows,
+                               neox ? 1 : 0, stream_),
           "attention (decode kernel)");
+  };
+  // K/V rows only (q stays as given; it is rotated on load)
+  auto append_kv = [&]() {
+    check(nbhs_append_rope_f32(nullptr, const_cast<float*>(k), const_cast<float*>(v), app->k_new, app->v_new, n,
+                               pos0, 0, n_kv_heads, head_dim, rope_table, rope_rows, neox ? 1 : 0, stream_),
+          "attention (append)");
   };
 
   const bool mfma_shape = head_dim == 64 || head_dim == 128;
   if (!mfma_shape || n <= kDecodeMaxRows) {
+    if (app) append_kv();
     decode_rows(q, out, n, pos0);
     return;
   }
   const int64_t split = std::clamp<int64_t>(kFp32PrefixRows - pos0, 0, n);
-  if (split > 0) decode_rows(q, out, split, pos0);
-  if (split == n) return;
   const int64_t rows = pos0 + n;
   const int64_t halves = nbhs_prefill_staging_halves(rows, n_kv_heads, head_dim);
-  ensure(k16_, k16_bytes_, size_t(halves) * 2);
-  ensure(vt16_, vt16_bytes_, size_t(halves) * 2);
-  check(nbhs_stage_kv_f16(k, v, k16_, vt16_, rows, n_kv_heads, head_dim, stream_), "attention (staging)");
+  if (split < n) {
+    ensure(k16_, k16_bytes_, size_t(halves) * 2);
+    ensure(vt16_, vt16_bytes_, size_t(halves) * 2);
+  }
+  if (app) {
+    if (split < n)
+      check(nbhs_append_stage_kv_f16(const_cast<float*>(k), const_cast<float*>(v), app->k_new, app->v_new, n, pos0,
+                                     n_kv_heads, head_dim, rope_table, rope_rows, neox ? 1 : 0, k16_, vt16_,
+                                     stream_),
+            "attention (append and staging)");
+    else
+      append_kv();
+  } else if (split < n) {
+    check(nbhs_stage_kv_f16(k, v, k16_, vt16_, rows, n_kv_heads, head_dim, stream_), "attention (staging)");
+  }
+  if (split > 0) decode_rows(q, out, split, pos0);
+  if (split == n) return;
   const int64_t rows_pad = halves / (n_kv_heads * head_dim);
   check(nbhs_attn_prefill_mfma(q + split * n_heads * head_dim, k16_, vt16_, out + split * n_heads * head_dim,
-                               n - split, pos0 + split, n_heads, n_kv_heads, head_dim, rows_pad, stream_),
+                               n - split, pos0 + split, n_heads, n_kv_heads, head_dim, rows_pad, rope_table, rope_rows,
+                               neox ? 1 : 0, stream_),
         "attention (prefill kernel)");
 }
 

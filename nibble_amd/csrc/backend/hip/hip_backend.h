@@ -58,6 +58,12 @@ class HipBackend final : public Backend {
   // transformer.cpp:171-198 for K/V rows arriving in a separate buffer. k_cache/v_cache are layer bases.
   void append_rope(float* q, float* k_cache, float* v_cache, const float* k_new, const float* v_new, int64_t n,
                    int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const RopeParams& p);
+  // KV-cache append with RoPE fused into attention: the same results, bit for bit, as append_rope(q, ...) followed
+  // by attention(q, ...), except that q is read unrotated and left unchanged (it is rotated on load). On the MFMA
+  // route the append shares one pass with the fp16 operand staging, and q is never rewritten in memory.
+  void append_rope_attention(const float* q, float* k_cache, float* v_cache, const float* k_new, const float* v_new,
+                             float* out, int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads,
+                             int64_t head_dim, const RopeParams& p);
   void fill_normal(float* dst, int64_t count, uint64_t seed, float scale);
   void sync();
   nbhs_stream stream() const { return stream_; }
@@ -75,7 +81,16 @@ class HipBackend final : public Backend {
     float* dev = nullptr;  // [rows, head_dim/2] (cos, sin) float pairs
   };
 
+  struct AppendRows {
+    const float* k_new;
+    const float* v_new;
+  };
   [[noreturn]] static void not_on_gpu(const char* op);
+  void check_attention_args(const float* q, const float* k, const float* v, const float* out, int64_t n,
+                            int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const char* op) const;
+  void run_attention(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                     int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const float* rope_table,
+                     int64_t rope_rows, bool neox, const AppendRows* app, const RopeParams* rp);
   void check(int code, const char* what) const;
   // Throws unless [p, p + n_floats) lies inside one buffer from alloc().
   void check_range(const void* p, int64_t n_floats, const char* op, const char* arg) const;

@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "backend/hip/kernel_timing.h"
+#include "kernels/rope_device.h"
 #include "nibble_hip_shim.h"
 
 namespace nbhs_timing {
@@ -64,12 +65,6 @@ inline unsigned grid_for(int64_t items) {
   return static_cast<unsigned>(blocks < 1 ? 1 : (blocks > 65536 ? 65536 : blocks));
 }
 
-// One (a, b) pair rotated by the tabulated angle: a*c - b*s, a*s + b*c, each op rounded on its own.
-__device__ __forceinline__ void rotate(float& a, float& b, float c, float s) {
-  const float a0 = a, b0 = b;
-  a = __fsub_rn(__fmul_rn(a0, c), __fmul_rn(b0, s));
-  b = __fadd_rn(__fmul_rn(a0, s), __fmul_rn(b0, c));
-}
 
 // x[n, heads, hd] in place, one thread per (row, head, pair). Pair i of a row is (i, i + hd/2) for NeoX, else
 // (2i, 2i + 1) (ref_ops.cpp:177-178).
@@ -83,14 +78,14 @@ __global__ void rope_kernel(float* __restrict__ x, int64_t n, int64_t heads, int
     const float2 c = cs[(pos0 + t) * half + i];
     const int64_t ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
     float a = row[ia], b = row[ib];
-    rotate(a, b, c.x, c.y);
+    rope_rotate(a, b, c);
     row[ia] = a;
     row[ib] = b;
   }
 }
 
 // Fused append: per row t, slots [0, H) rotate q heads in place, [H, H+KV) rotate k_new heads into the cache,
-// [H+KV, H+2KV) copy v_new heads into the cache; one thread per (row, slot, pair).
+// [H+KV, H+2KV) copy v_new heads into the cache; one thread per (row, slot, pair). H = 0 appends K/V only.
 __global__ void append_rope_kernel(float* __restrict__ q, float* __restrict__ ck, float* __restrict__ cv,
                                    const float* __restrict__ kn, const float* __restrict__ vn, int64_t n, int64_t pos0,
                                    int64_t H, int64_t KV, int64_t hd, const float2* __restrict__ cs, int neox) {
@@ -103,7 +98,7 @@ __global__ void append_rope_kernel(float* __restrict__ q, float* __restrict__ ck
       float* row = q + (t * H + slot) * hd;
       const float2 c = cs[(pos0 + t) * half + i];
       float a = row[ia], b = row[ib];
-      rotate(a, b, c.x, c.y);
+      rope_rotate(a, b, c);
       row[ia] = a;
       row[ib] = b;
     } else if (slot < H + KV) {
@@ -112,7 +107,7 @@ __global__ void append_rope_kernel(float* __restrict__ q, float* __restrict__ ck
       float* dst = ck + ((pos0 + t) * KV + g) * hd;
       const float2 c = cs[(pos0 + t) * half + i];
       float a = src[ia], b = src[ib];
-      rotate(a, b, c.x, c.y);
+      rope_rotate(a, b, c);
       dst[ia] = a;
       dst[ib] = b;
     } else {
@@ -260,8 +255,8 @@ int nbhs_rope_f32(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_
 int nbhs_append_rope_f32(float* q, float* cache_k, float* cache_v, const float* k_new, const float* v_new, int64_t n,
                          int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const float* cs_table,
                          int64_t table_rows, int neox, nbhs_stream s) {
-  if (!q || !cache_k || !cache_v || !k_new || !v_new || !cs_table || n <= 0 || n_heads <= 0 || n_kv_heads <= 0 ||
-      head_dim <= 0 || head_dim % 2 != 0 || pos0 < 0 || pos0 + n > table_rows)
+  if ((q ? n_heads <= 0 : n_heads != 0) || !cache_k || !cache_v || !k_new || !v_new || !cs_table || n <= 0 ||
+      n_kv_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || pos0 < 0 || pos0 + n > table_rows)
     return NBHS_EINVAL;
   return nbhs_timing::launch(NBHS_K_APPEND_ROPE, append_rope_kernel,
                              dim3(grid_for(n * (n_heads + 2 * n_kv_heads) * (head_dim / 2))), dim3(kThreads), S(s), q,

@@ -119,6 +119,16 @@ int nbh_backend_append_rope(nbh_backend* be, float* q, float* k_cache, float* v_
   });
 }
 
+int nbh_backend_append_rope_attention(nbh_backend* be, const float* q, float* k_cache, float* v_cache,
+                                      const float* k_new, const float* v_new, float* out, int64_t n, int64_t pos0,
+                                      int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float freq_base, int neox,
+                                      const float* freq_factors) {
+  return guarded([&] {
+    B(be).append_rope_attention(q, k_cache, v_cache, k_new, v_new, out, n, pos0, n_heads, n_kv_heads, head_dim,
+                                RopeParams{freq_base, neox != 0, freq_factors});
+  });
+}
+
 int nbh_backend_reserve_attention(nbh_backend* be, int64_t n_kv_heads, int64_t head_dim) {
   return guarded([&] { B(be).reserve_attention(n_kv_heads, head_dim); });
 }

@@ -25,6 +25,7 @@
 #include <cmath>
 
 #include "backend/hip/kernel_timing.h"
+#include "kernels/rope_device.h"
 #include "nibble_hip_shim.h"
 
 namespace {
@@ -119,7 +120,8 @@ template <int HD, int GB>
 __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ out,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, int64_t pos0, int n_heads, int n_kv, int group, int n_sub,
-    int n_chunks, int64_t groups_per_chunk, int64_t extra_groups, float qscale) {
+    int n_chunks, int64_t groups_per_chunk, int64_t extra_groups, float qscale, const float2* __restrict__ q_rope,
+    int q_rope_neox) {
   constexpr int VPL = 2;                            // float4 per lane per row
   constexpr int LPR = HD / (4 * VPL);               // lanes per K/V row: 8 (hd 64) or 16 (hd 128)
   constexpr int RPS = 64 / LPR;                     // rows per wave load
@@ -189,9 +191,33 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
     for (int i = 0; i < VPL; ++i) {
       qv[h][i] = f32x4{0.f, 0.f, 0.f, 0.f};
       st[h].o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (h < gcount)
-        qv[h][i] = *reinterpret_cast<const f32x4*>(q + (t * n_heads + h0 + h) * HD + 4 * (dl + LPR * i)) * qscale;
+      if (h < gcount) qv[h][i] = *reinterpret_cast<const f32x4*>(q + (t * n_heads + h0 + h) * HD + 4 * (dl + LPR * i));
     }
+    // Unrotated q (q_rope = the position-major (cos, sin) table): rotate here, exactly as the RoPE kernel would
+    // have in memory. The lane holds both members of each of its pairs: adjacent pairs sit in one float4, and with
+    // NeoX pairing (j, j + HD/2) float4 i = 1 is float4 i = 0 shifted by 4 LPR = HD/2 floats.
+    if (q_rope && h < gcount) {
+      const float2* cs = q_rope + (pos0 + t) * (HD / 2);
+      if (q_rope_neox) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float2 r = rope_pair(qv[h][0][e], qv[h][1][e], cs[4 * dl + e]);
+          qv[h][0][e] = r.x;
+          qv[h][1][e] = r.y;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i)
+#pragma unroll
+          for (int pr = 0; pr < 2; ++pr) {
+            const float2 r = rope_pair(qv[h][i][2 * pr], qv[h][i][2 * pr + 1], cs[2 * (dl + LPR * i) + pr]);
+            qv[h][i][2 * pr] = r.x;
+            qv[h][i][2 * pr + 1] = r.y;
+          }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) qv[h][i] *= qscale;
     st[h].m = -INFINITY;
     st[h].l = 0.f;
   }
@@ -491,7 +517,8 @@ Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t h
 
 template <int HD>
 int launch_decode(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0, int64_t H,
-                  int64_t KV, float* ws, const Plan& p, float qscale, hipStream_t s) {
+                  int64_t KV, float* ws, const Plan& p, float qscale, const float2* q_rope, int q_rope_neox,
+                  hipStream_t s) {
   float* ws_o = ws;
   float* ws_ml = ws ? ws + n * H * p.n_chunks * HD : nullptr;
   const int group = int(H / KV);
@@ -500,7 +527,7 @@ int launch_decode(const float* q, const float* k, const float* v, float* out, in
 #define NBH_DECODE(GB)                                                                                             \
   e = nbhs_timing::launch(NBHS_K_DECODE_PARTIAL, attn_decode_partial<HD, GB>, grid, dim3(kDecodeThreads), s, q, k, \
                           v, out, ws_o, ws_ml, pos0, int(H), int(KV), group, p.n_sub, p.n_chunks,                   \
-                          p.groups_per_chunk, p.extra_groups, qscale)
+                          p.groups_per_chunk, p.extra_groups, qscale, q_rope, q_rope_neox)
   switch (p.gb) {
     case 1: NBH_DECODE(1); break;
     case 2: NBH_DECODE(2); break;
@@ -538,11 +565,15 @@ int64_t nbhs_attn_decode_workspace_bound(int64_t n_heads, int cu_count) {
 
 int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
                          int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float* workspace,
-                         int64_t workspace_floats, int cu_count, nbhs_stream stream) {
+                         int64_t workspace_floats, int cu_count, const float* q_rope_cs, int64_t q_rope_rows,
+                         int q_rope_neox, nbhs_stream stream) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (!q || !k || !v || !out || n <= 0 || n > 65535 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 ||
       n_heads % n_kv_heads != 0 || head_dim <= 0 || head_dim > 256 || n_heads > 65535)
     return NBHS_EINVAL;
+  // q rotation on load is implemented for the tiled head sizes only, over table rows covering pos0 .. pos0+n-1
+  if (q_rope_cs && (!tiled_head_dim(head_dim) || pos0 + n > q_rope_rows)) return NBHS_EINVAL;
+  const float2* q_rope = reinterpret_cast<const float2*>(q_rope_cs);
   const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
   if (!tiled_head_dim(head_dim)) {
     return nbhs_timing::launch(NBHS_K_GENERIC, attn_generic, dim3(unsigned(n_heads), unsigned(n)), dim3(64), s, q, k,
@@ -552,8 +583,9 @@ int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* 
   const int64_t need = p.n_chunks == 1 ? 0 : n * n_heads * p.n_chunks * (head_dim + 2);
   if (need > 0 && (!workspace || workspace_floats < need)) return NBHS_EINVAL;
   if (n_kv_heads * p.n_sub > 65535) return NBHS_EINVAL;
-  if (head_dim == 64) return launch_decode<64>(q, k, v, out, n, pos0, n_heads, n_kv_heads, workspace, p, qscale, s);
-  return launch_decode<128>(q, k, v, out, n, pos0, n_heads, n_kv_heads, workspace, p, qscale, s);
+  if (head_dim == 64)
+    return launch_decode<64>(q, k, v, out, n, pos0, n_heads, n_kv_heads, workspace, p, qscale, q_rope, q_rope_neox, s);
+  return launch_decode<128>(q, k, v, out, n, pos0, n_heads, n_kv_heads, workspace, p, qscale, q_rope, q_rope_neox, s);
 }
 
 }  // extern "C"

@@ -30,6 +30,7 @@
 #include <cmath>
 
 #include "backend/hip/kernel_timing.h"
+#include "kernels/rope_device.h"
 #include "nibble_hip_shim.h"
 
 namespace {
@@ -89,28 +90,67 @@ constexpr int vmcnt_wait(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >
 __device__ __forceinline__ int vt_key(int p) { return (p & ~15) + (p & 3) + ((p >> 2) & 1) * 8 + ((p >> 3) & 1) * 4; }
 
 // ---- staging: fp32 cache rows -> fp16 K [KV][rows_pad][HD] and transposed V [KV][HD][rows_pad] ----
+// Rows [0, pos0) come from the cache ck/cv; rows [pos0, rows), when kn/vn are given, are the appended rows: K
+// rotated by RoPE at its position (cs, neox), and both written into the fp32 cache as well as staged - the KV
+// append and the staging in one pass. A thread takes one row and dimensions [4 d4, 4 d4 + 4) and the same four
+// HD/2 further on, so both RoPE pairings (adjacent, and NeoX's (j, j + HD/2)) stay within the thread. Rows past
+// `rows` (padding up to rows_pad) are staged as zeros.
 template <int HD>
-__global__ __launch_bounds__(256) void stage_kv_kernel(const float* __restrict__ k, const float* __restrict__ v,
-                                                       _Float16* __restrict__ k16, _Float16* __restrict__ vt16,
-                                                       int64_t rows, int64_t rows_pad, int n_kv) {
+__global__ __launch_bounds__(256) void stage_kv_kernel(float* ck, float* cv, const float* __restrict__ kn,
+                                                       const float* __restrict__ vn, _Float16* __restrict__ k16,
+                                                       _Float16* __restrict__ vt16, int64_t pos0, int64_t rows,
+                                                       int64_t rows_pad, int n_kv, const float2* __restrict__ cs,
+                                                       int neox) {
   __shared__ _Float16 tr[HD][kBN + kPad];
   const int g = blockIdx.y;
   const int64_t r0 = int64_t(blockIdx.x) * kBN;
-  // K: straight conversion, 4 floats per thread step.
-  for (int idx = threadIdx.x; idx < kBN * HD / 4; idx += 256) {
-    const int r = idx / (HD / 4), d4 = idx % (HD / 4);
+  constexpr int H2 = HD / 2;
+  for (int idx = threadIdx.x; idx < kBN * HD / 8; idx += 256) {
+    const int r = idx / (HD / 8), d4 = idx % (HD / 8);
     const int64_t row = r0 + r;
-    float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+    float4 k0 = make_float4(0.f, 0.f, 0.f, 0.f), k1 = k0, v0 = k0, v1 = k0;
     if (row < rows) {
-      x = *reinterpret_cast<const float4*>(k + (row * n_kv + g) * HD + 4 * d4);
-      y = *reinterpret_cast<const float4*>(v + (row * n_kv + g) * HD + 4 * d4);
+      const int64_t at = (row * n_kv + g) * HD + 4 * d4;
+      if (row < pos0 || !kn) {
+        k0 = *reinterpret_cast<const float4*>(ck + at);
+        k1 = *reinterpret_cast<const float4*>(ck + at + H2);
+        v0 = *reinterpret_cast<const float4*>(cv + at);
+        v1 = *reinterpret_cast<const float4*>(cv + at + H2);
+      } else {
+        const int64_t src = ((row - pos0) * n_kv + g) * HD + 4 * d4;
+        k0 = *reinterpret_cast<const float4*>(kn + src);
+        k1 = *reinterpret_cast<const float4*>(kn + src + H2);
+        v0 = *reinterpret_cast<const float4*>(vn + src);
+        v1 = *reinterpret_cast<const float4*>(vn + src + H2);
+        const float2* c = cs + row * H2;
+        if (neox) {
+          rope_rotate(k0.x, k1.x, c[4 * d4 + 0]);
+          rope_rotate(k0.y, k1.y, c[4 * d4 + 1]);
+          rope_rotate(k0.z, k1.z, c[4 * d4 + 2]);
+          rope_rotate(k0.w, k1.w, c[4 * d4 + 3]);
+        } else {
+          rope_rotate(k0.x, k0.y, c[2 * d4]);
+          rope_rotate(k0.z, k0.w, c[2 * d4 + 1]);
+          rope_rotate(k1.x, k1.y, c[H2 / 2 + 2 * d4]);
+          rope_rotate(k1.z, k1.w, c[H2 / 2 + 2 * d4 + 1]);
+        }
+        *reinterpret_cast<float4*>(ck + at) = k0;
+        *reinterpret_cast<float4*>(ck + at + H2) = k1;
+        *reinterpret_cast<float4*>(cv + at) = v0;
+        *reinterpret_cast<float4*>(cv + at + H2) = v1;
+      }
     }
-    half4_t hk = {(_Float16)x.x, (_Float16)x.y, (_Float16)x.z, (_Float16)x.w};
-    *reinterpret_cast<half4_t*>(k16 + (int64_t(g) * rows_pad + row) * HD + 4 * d4) = hk;
-    tr[4 * d4 + 0][r] = (_Float16)y.x;
-    tr[4 * d4 + 1][r] = (_Float16)y.y;
-    tr[4 * d4 + 2][r] = (_Float16)y.z;
-    tr[4 * d4 + 3][r] = (_Float16)y.w;
+    _Float16* kd = k16 + (int64_t(g) * rows_pad + row) * HD + 4 * d4;
+    *reinterpret_cast<half4_t*>(kd) = half4_t{(_Float16)k0.x, (_Float16)k0.y, (_Float16)k0.z, (_Float16)k0.w};
+    *reinterpret_cast<half4_t*>(kd + H2) = half4_t{(_Float16)k1.x, (_Float16)k1.y, (_Float16)k1.z, (_Float16)k1.w};
+    tr[4 * d4 + 0][r] = (_Float16)v0.x;
+    tr[4 * d4 + 1][r] = (_Float16)v0.y;
+    tr[4 * d4 + 2][r] = (_Float16)v0.z;
+    tr[4 * d4 + 3][r] = (_Float16)v0.w;
+    tr[H2 + 4 * d4 + 0][r] = (_Float16)v1.x;
+    tr[H2 + 4 * d4 + 1][r] = (_Float16)v1.y;
+    tr[H2 + 4 * d4 + 2][r] = (_Float16)v1.z;
+    tr[H2 + 4 * d4 + 3][r] = (_Float16)v1.w;
   }
   __syncthreads();
   // V^T: each d row of the tile is 64 keys (128 B), stored in the key order of the PV MFMA operand (vt_key).
@@ -140,7 +180,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(
 void attn_prefill_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16,
     float* __restrict__ out, int64_t n, int64_t pos0, int n_heads, int n_kv, int group, int64_t rows_pad,
-    int n_tiles, float qscale) {
+    int n_tiles, float qscale, const float2* __restrict__ q_rope, int q_rope_neox) {
   constexpr int DC = HD / 16;  // 16-wide d chunks of the S^T contraction
   constexpr int DT = HD / 32;  // 32-row d tiles of O^T
   // K and V^T tiles live in LDS unpadded, one row of 16-byte chunks per key (K) or per dimension (V^T), with chunk
@@ -187,11 +227,15 @@ void attn_prefill_kernel(
   const int64_t wave_kend = wave_active ? pos0 + (min(wp0 + kRowsPerWave, P) - 1) / group + 1 : 0;
   const int64_t wave_kfull = wave_active ? pos0 + wp0 / group + 1 : 0;  // keys every row of the wave sees
 
-  // Q fragments (B operand of S^T): query of block qb, d = 16c + 8hf .. +8.
+  // Q fragments (B operand of S^T): query of block qb, d = 16c + 8hf .. +8. Unrotated q (q_rope = the
+  // position-major (cos, sin) table) is rotated here, exactly as the RoPE kernel would have in memory: the lane
+  // holds both members of every pair it needs - adjacent pairs within its 8 dimensions, NeoX pairs (j, j + HD/2)
+  // in chunks c and c + DC/2.
   half8_t qf[kQB][DC];
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
     const float* qrow = q + (t[qb] * n_heads + head[qb]) * HD;
+    float x[DC][8];
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
       float4 a = make_float4(0.f, 0.f, 0.f, 0.f), bb = a;
@@ -199,10 +243,27 @@ void attn_prefill_kernel(
         a = *reinterpret_cast<const float4*>(qrow + 16 * c + 8 * hf);
         bb = *reinterpret_cast<const float4*>(qrow + 16 * c + 8 * hf + 4);
       }
-      qf[qb][c] = half8_t{(_Float16)(a.x * qscale), (_Float16)(a.y * qscale), (_Float16)(a.z * qscale),
-                          (_Float16)(a.w * qscale), (_Float16)(bb.x * qscale), (_Float16)(bb.y * qscale),
-                          (_Float16)(bb.z * qscale), (_Float16)(bb.w * qscale)};
+      x[c][0] = a.x, x[c][1] = a.y, x[c][2] = a.z, x[c][3] = a.w;
+      x[c][4] = bb.x, x[c][5] = bb.y, x[c][6] = bb.z, x[c][7] = bb.w;
     }
+    if (q_rope && active[qb]) {
+      const float2* cs = q_rope + qpos[qb] * (HD / 2);
+      if (q_rope_neox) {
+#pragma unroll
+        for (int c = 0; c < DC / 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) rope_rotate(x[c][e], x[c + DC / 2][e], cs[16 * c + 8 * hf + e]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < DC; ++c)
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) rope_rotate(x[c][e], x[c][e + 1], cs[(16 * c + 8 * hf + e) / 2]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < DC; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[qb][c][e] = (_Float16)(x[c][e] * qscale);
   }
 
   floatx16 oacc[kQB][DT];
@@ -431,17 +492,35 @@ int nbhs_stage_kv_f16(const float* k, const float* v, void* k16, void* vt16, int
   const dim3 grid(unsigned(rows_pad / kBN), unsigned(n_kv_heads));
   auto* const kh = static_cast<_Float16*>(k16);
   auto* const vh = static_cast<_Float16*>(vt16);
+  // read-only use of the cache: no new rows (kn = vn = NULL), so ck/cv are only read
   return nbhs_timing::launch(NBHS_K_STAGE_KV, head_dim == 64 ? stage_kv_kernel<64> : stage_kv_kernel<128>, grid,
-                             dim3(256), s, k, v, kh, vh, rows, rows_pad, int(n_kv_heads));
+                             dim3(256), s, const_cast<float*>(k), const_cast<float*>(v),
+                             static_cast<const float*>(nullptr), static_cast<const float*>(nullptr), kh, vh, rows,
+                             rows, rows_pad, int(n_kv_heads), static_cast<const float2*>(nullptr), 0);
+}
+
+int nbhs_append_stage_kv_f16(float* cache_k, float* cache_v, const float* k_new, const float* v_new, int64_t n,
+                             int64_t pos0, int64_t n_kv_heads, int64_t head_dim, const float* cs_table,
+                             int64_t table_rows, int neox, void* k16, void* vt16, nbhs_stream stream) {
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (!cache_k || !cache_v || !k_new || !v_new || !cs_table || !k16 || !vt16 || n <= 0 || pos0 < 0 ||
+      n_kv_heads <= 0 || n_kv_heads > 65535 || (head_dim != 64 && head_dim != 128) || pos0 + n > table_rows)
+    return NBHS_EINVAL;
+  const int64_t rows = pos0 + n, rows_pad = round_up(rows, kBN);
+  const dim3 grid(unsigned(rows_pad / kBN), unsigned(n_kv_heads));
+  return nbhs_timing::launch(NBHS_K_STAGE_KV, head_dim == 64 ? stage_kv_kernel<64> : stage_kv_kernel<128>, grid,
+                             dim3(256), s, cache_k, cache_v, k_new, v_new, static_cast<_Float16*>(k16),
+                             static_cast<_Float16*>(vt16), pos0, rows, rows_pad, int(n_kv_heads),
+                             reinterpret_cast<const float2*>(cs_table), neox);
 }
 
 int nbhs_attn_prefill_mfma(const float* q, const void* k16, const void* vt16, float* out, int64_t n, int64_t pos0,
                            int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t staged_rows_pad,
-                           nbhs_stream stream) {
+                           const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, nbhs_stream stream) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (!q || !k16 || !vt16 || !out || n <= 0 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 ||
       n_heads % n_kv_heads != 0 || (head_dim != 64 && head_dim != 128) || staged_rows_pad % kBN != 0 ||
-      staged_rows_pad < round_up(pos0 + n, kBN))
+      staged_rows_pad < round_up(pos0 + n, kBN) || (q_rope_cs && pos0 + n > q_rope_rows))
     return NBHS_EINVAL;
   const int64_t group = n_heads / n_kv_heads;
   const int64_t tiles = (n * group + kRowsPerBlock - 1) / kRowsPerBlock;
@@ -451,7 +530,8 @@ int nbhs_attn_prefill_mfma(const float* q, const void* k16, const void* vt16, fl
   return nbhs_timing::launch(NBHS_K_PREFILL_MFMA, head_dim == 64 ? attn_prefill_kernel<64> : attn_prefill_kernel<128>,
                              dim3(blocks), dim3(kWaves * 64), s, q, static_cast<const _Float16*>(k16),
                              static_cast<const _Float16*>(vt16), out, n, pos0, int(n_heads), int(n_kv_heads),
-                             int(group), staged_rows_pad, int(tiles), qscale);
+                             int(group), staged_rows_pad, int(tiles), qscale,
+                             reinterpret_cast<const float2*>(q_rope_cs), q_rope_neox);
 }
 
 }  // extern "C"

@@ -371,3 +371,34 @@ def test_copy_overlapping_is_memmove(backend, shift):
     want = x.copy()
     want[s0 + shift:s0 + shift + count] = x[s0:s0 + count]
     assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("H,KV,D,neox,llama3", [(32, 8, 64, False, True), (14, 2, 64, True, False),
+                                                 (32, 4, 64, False, False), (16, 8, 128, True, False),
+                                                 (16, 4, 128, False, True), (8, 2, 24, True, False)])
+@pytest.mark.parametrize("n,pos0", [(1, 1000), (7, 333), (600, 0), (300, 100), (512, 4096)])
+def test_append_rope_attention_equals_unfused(backend, H, KV, D, neox, llama3, n, pos0):
+    """The fused op (K/V append with RoPE, q rotated on load, append fused with the fp16 staging on the MFMA route)
+    gives bit-identical outputs and caches to append_rope followed by attention, and leaves q unrotated."""
+    base = 5e5 if llama3 else 1e4
+    ff = synth.llama3_freq_factors(D, base) if llama3 else None
+    rng = np.random.default_rng(n * 31 + pos0 + D)
+    q = rng.standard_normal((n, H, D)).astype(np.float32)
+    kn = rng.standard_normal((n, KV, D)).astype(np.float32)
+    vn = rng.standard_normal((n, KV, D)).astype(np.float32)
+    k0 = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+    v0 = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+    with Buffers(backend) as B:
+        dq1, dq2, dkn, dvn = B.upload(q), B.upload(q), B.upload(kn), B.upload(vn)
+        ck1, cv1, ck2, cv2 = B.upload(k0), B.upload(v0), B.upload(k0), B.upload(v0)
+        o1, o2 = B.alloc(q.size), B.alloc(q.size)
+        backend.append_rope(dq1, ck1, cv1, dkn, dvn, n, pos0, H, KV, D, base, neox, ff)
+        backend.attention(dq1, ck1, cv1, o1, n, pos0, H, KV, D)
+        backend.append_rope_attention(dq2, ck2, cv2, dkn, dvn, o2, n, pos0, H, KV, D, base, neox, ff)
+        r1, r2 = backend.download(o1, q.shape), backend.download(o2, q.shape)
+        gk1, gk2 = backend.download(ck1, k0.shape), backend.download(ck2, k0.shape)
+        gv1, gv2 = backend.download(cv1, v0.shape), backend.download(cv2, v0.shape)
+        gq2 = backend.download(dq2, q.shape)
+    assert np.array_equal(bits(r1), bits(r2)), "outputs differ"
+    assert np.array_equal(bits(gk1), bits(gk2)) and np.array_equal(bits(gv1), bits(gv2)), "caches differ"
+    assert np.array_equal(bits(gq2), bits(q)), "fused op modified q"
