@@ -337,7 +337,7 @@ def main():
     mfma_flops = prefill_flops(H, D, FP32_PREFIX_ROWS, n_pre - FP32_PREFIX_ROWS)  # rows the MFMA kernel computes
     mfma_tflops = mfma_flops * mfma_n / (mfma_ms * 1e-3) / 1e12
     log(f"kernels: decode partial avg {part_ms / part_n * 1e3:.2f} us ({dec_kernel_gbs:.0f} GB/s), combine avg "
-        f"{comb_ms / max(comb_n, 1) * 1e3:.2f} us, append+rope avg {app_ms / max(app_n, 1) * 1e3:.2f} us; "
+        f"{comb_ms / max(comb_n, 1) * 1e3:.2f} us, separate append launches {app_n}; "
         f"prefill mfma avg {mfma_ms / mfma_n:.3f} ms ({mfma_tflops:.1f} TFLOP/s), append+stage avg "
         f"{stage_ms / max(stage_n, 1) * 1e3:.1f} us, fp32 prefix avg {pref32_ms / max(pref32_n, 1) * 1e3:.1f} us")
 
@@ -375,8 +375,9 @@ def main():
                                  "algorithmic_bytes_per_launch": int(2 * 4 * (n_pre - FP32_PREFIX_ROWS) * H * D
                                                                      + 2 * 2 * n_pre * KV * D)}},
         "kernels_us": {"decode_combine": round(comb_ms / max(comb_n, 1) * 1e3, 3),
-                       "append_rope_decode": round(app_ms / max(app_n, 1) * 1e3, 3),
-                       "append_rope_prefill": round(app2_ms / max(app2_n, 1) * 1e3, 2),
+                       # the decode step's K/V append rides in the partial kernel: no launches of its own
+                       "append_rope_decode": round(app_ms / app_n * 1e3, 3) if app_n else None,
+                       "append_rope_prefill": round(app2_ms / app2_n * 1e3, 2) if app2_n else None,
                        "append_stage_kv_f16": round(stage_ms / max(stage_n, 1) * 1e3, 2),
                        "prefill_fp32_prefix": round(pref32_ms / max(pref32_n, 1) * 1e3, 2)},
     }

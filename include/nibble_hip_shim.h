@@ -83,6 +83,14 @@ int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* 
                          int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float* workspace,
                          int64_t workspace_floats, int cu_count, const float* q_rope_cs, int64_t q_rope_rows,
                          int q_rope_neox, nbhs_stream s);
+/* One decode step with its KV append (the single-row case of transformer.cpp:171-202: cache rows written, rope(q),
+ * rope(kc), attention): cache row pos0 receives rope(k_new) and v_new (as nbhs_append_rope_f32 with no q), and
+ * out receives the attention of the unrotated query row q, rotated on load, over rows 0..pos0 - bit-identical to
+ * the append followed by nbhs_attn_decode_f32, in one launch fewer. head_dim 64 or 128; rope_cs covers pos0. */
+int nbhs_append_attn_decode_f32(const float* q, float* k_cache, float* v_cache, const float* k_new,
+                                const float* v_new, float* out, int64_t pos0, int64_t n_heads, int64_t n_kv_heads,
+                                int64_t head_dim, float* workspace, int64_t workspace_floats, int cu_count,
+                                const float* rope_cs, int64_t rope_rows, int neox, nbhs_stream s);
 
 /* Operand staging for the MFMA prefill: cache rows [0, rows) of k and v [rows, n_kv_heads, head_dim] fp32 are
  * rounded to fp16 into k16 [n_kv_heads, rows_pad, head_dim] and vt16 [n_kv_heads, head_dim, rows_pad]

@@ -343,6 +343,17 @@ void HipBackend::run_attention(const float* q, const float* k, const float* v, f
   };
 
   const bool mfma_shape = head_dim == 64 || head_dim == 128;
+  if (app && mfma_shape && n == 1) {  // decode step: the append rides in the attention launch
+    const int64_t ws = nbhs_attn_decode_workspace(1, pos0, n_heads, n_kv_heads, head_dim, cu_count_);
+    if (ws < 0) throw Error("attention: invalid decode shape");
+    ensure(decode_ws_, decode_ws_bytes_, size_t(ws) * sizeof(float));
+    check(nbhs_append_attn_decode_f32(q, const_cast<float*>(k), const_cast<float*>(v), app->k_new, app->v_new, out,
+                                      pos0, n_heads, n_kv_heads, head_dim, decode_ws_,
+                                      int64_t(decode_ws_bytes_ / sizeof(float)), cu_count_, rope_table, rope_rows,
+                                      neox ? 1 : 0, stream_),
+          "attention (append and decode kernel)");
+    return;
+  }
   if (!mfma_shape || n <= kDecodeMaxRows) {
     if (app) append_kv();
     decode_rows(q, out, n, pos0);

@@ -20,6 +20,10 @@
 //  * Row validity is only tested in a chunk's last, partial iteration.
 //  * Each workgroup writes an unnormalised partial (max, sum, weighted V) per query head; attn_decode_combine
 //    merges the chunks with a log-sum-exp reduction. With a single chunk the partial kernel writes the output.
+//  * Single-row append (decode step of the fused append + attention op): the new K/V row is not in the cache yet.
+//    The workgroup whose chunk ends with row pos0 loads it from k_new / v_new, rotates K in registers and uses it
+//    in place of cache row pos0; it writes the row into the cache in its epilogue. No other workgroup reads that
+//    row, so the separate append launch disappears.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -121,7 +125,8 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ out,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, int64_t pos0, int n_heads, int n_kv, int group, int n_sub,
     int n_chunks, int64_t groups_per_chunk, int64_t extra_groups, float qscale, const float2* __restrict__ q_rope,
-    int q_rope_neox) {
+    int q_rope_neox, const float* __restrict__ k_new, const float* __restrict__ v_new, float* __restrict__ k_dst,
+    float* __restrict__ v_dst) {
   constexpr int VPL = 2;                            // float4 per lane per row
   constexpr int LPR = HD / (4 * VPL);               // lanes per K/V row: 8 (hd 64) or 16 (hd 128)
   constexpr int RPS = 64 / LPR;                     // rows per wave load
@@ -156,8 +161,17 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
   const float* kb = k + int64_t(g) * HD + 4 * dl;  // float4 column dl + LPR * i of the row
   const float* vb = v + int64_t(g) * HD + 4 * dl;
 
+  // Single-row append: the workgroup whose last row group holds row pos0 (= len - 1, n is 1) owns the new row.
+  const bool append = k_new != nullptr;
+  const int64_t new_grp = pos0 / kStep;
+  const bool owner = append && gcnt > 0 && g0 + (gcnt - 1) * gstride == new_grp;
+  const float* knb = append ? k_new + int64_t(g) * HD + 4 * dl : kb;  // the new row's lane slice
+  const float* vnb = append ? v_new + int64_t(g) * HD + 4 * dl : vb;
+
   // One iteration's rows: kUnroll row slots, VPL float4 of K and of V each. Rows past the causal window are
-  // clamped to the last valid row (never read out of range) and masked in the partial iteration.
+  // clamped to the last valid row (never read out of range) and masked in the partial iteration. When appending,
+  // lanes on row pos0 (and those clamped to it) read k_new / v_new instead of the cache row, which this kernel
+  // writes; compute() replaces those values with the rotated row.
   struct Rows {
     f32x4 k[kUnroll][VPL], v[kUnroll][VPL];
   };
@@ -166,10 +180,13 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t j = min(row_of(grp, u), len - 1);
+      const bool fresh = append && j >= pos0;
+      const float* kr = fresh ? knb : kb + j * row_stride;
+      const float* vr = fresh ? vnb : vb + j * row_stride;
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
-        r.k[u][i] = load4(kb + j * row_stride + 4 * LPR * i);
-        r.v[u][i] = load4(vb + j * row_stride + 4 * LPR * i);
+        r.k[u][i] = load4(kr + 4 * LPR * i);
+        r.v[u][i] = load4(vr + 4 * LPR * i);
       }
     }
   };
@@ -183,6 +200,43 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
   const bool two = extra && gcnt > 1;
   if (two) load(g0 + gstride, rb);
 
+  // Rotates a lane's slice of a row at position pos (cs = the position-major (cos, sin) table), exactly as the RoPE
+  // kernel does in memory. The lane holds both members of each of its pairs: adjacent pairs sit in one float4, and
+  // with NeoX pairing (j, j + HD/2) float4 i = 1 is float4 i = 0 shifted by 4 LPR = HD/2 floats.
+  auto rotate = [&](f32x4 (&x)[VPL], int64_t pos) {
+    const float2* cs = q_rope + pos * (HD / 2);
+    if (q_rope_neox) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float2 r = rope_pair(x[0][e], x[1][e], cs[4 * dl + e]);
+        x[0][e] = r.x;
+        x[1][e] = r.y;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i)
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          const float2 r = rope_pair(x[i][2 * pr], x[i][2 * pr + 1], cs[2 * (dl + LPR * i) + pr]);
+          x[i][2 * pr] = r.x;
+          x[i][2 * pr + 1] = r.y;
+        }
+    }
+  };
+
+  // The appended row, rotated (owner only; consumed in the chunk's last iteration and the epilogue).
+  f32x4 nk[VPL], nv[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) nk[i] = nv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (owner) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      nk[i] = *reinterpret_cast<const f32x4*>(knb + 4 * LPR * i);
+      nv[i] = *reinterpret_cast<const f32x4*>(vnb + 4 * LPR * i);
+    }
+    rotate(nk, pos0);
+  }
+
   f32x4 qv[GB][VPL];
   State<VPL> st[GB];
 #pragma unroll
@@ -193,38 +247,28 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
       st[h].o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
       if (h < gcount) qv[h][i] = *reinterpret_cast<const f32x4*>(q + (t * n_heads + h0 + h) * HD + 4 * (dl + LPR * i));
     }
-    // Unrotated q (q_rope = the position-major (cos, sin) table): rotate here, exactly as the RoPE kernel would
-    // have in memory. The lane holds both members of each of its pairs: adjacent pairs sit in one float4, and with
-    // NeoX pairing (j, j + HD/2) float4 i = 1 is float4 i = 0 shifted by 4 LPR = HD/2 floats.
-    if (q_rope && h < gcount) {
-      const float2* cs = q_rope + (pos0 + t) * (HD / 2);
-      if (q_rope_neox) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float2 r = rope_pair(qv[h][0][e], qv[h][1][e], cs[4 * dl + e]);
-          qv[h][0][e] = r.x;
-          qv[h][1][e] = r.y;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < VPL; ++i)
-#pragma unroll
-          for (int pr = 0; pr < 2; ++pr) {
-            const float2 r = rope_pair(qv[h][i][2 * pr], qv[h][i][2 * pr + 1], cs[2 * (dl + LPR * i) + pr]);
-            qv[h][i][2 * pr] = r.x;
-            qv[h][i][2 * pr + 1] = r.y;
-          }
-      }
-    }
+    if (q_rope && h < gcount) rotate(qv[h], pos0 + t);  // unrotated q: rotate on load
 #pragma unroll
     for (int i = 0; i < VPL; ++i) qv[h][i] *= qscale;
     st[h].m = -INFINITY;
     st[h].l = 0.f;
   }
 
-  auto compute = [&](const Rows& r, int64_t grp_idx) {
+  auto compute = [&](Rows& r, int64_t grp_idx) {
     // Wave-uniform: does this iteration reach past the causal window?
     const bool partial = grp_idx * kStep + wave * WAVE_ROWS + WAVE_ROWS > len;
+    // Wave-uniform: does it hold the appended row? Then its lanes take the rotated row from registers.
+    if (owner && grp_idx == new_grp && grp_idx * kStep + wave * WAVE_ROWS + WAVE_ROWS > pos0) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const bool fresh = row_of(grp_idx, u) >= pos0;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+          r.k[u][i] = fresh ? nk[i] : r.k[u][i];
+          r.v[u][i] = fresh ? nv[i] : r.v[u][i];
+        }
+      }
+    }
 #pragma unroll
     for (int h = 0; h < GB; ++h) {
       if (h >= gcount) continue;
@@ -286,6 +330,17 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
     if (it < gcnt) load(g0 + it * gstride, ra);
   }
 #endif
+
+  // The appended row goes into its cache row once per KV head (head subgroup 0 of the owner).
+  if (owner && sg == 0 && wave == 0 && lane < LPR) {
+    float* kd = k_dst + pos0 * row_stride + int64_t(g) * HD + 4 * dl;
+    float* vd = v_dst + pos0 * row_stride + int64_t(g) * HD + 4 * dl;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      *reinterpret_cast<f32x4*>(kd + 4 * LPR * i) = nk[i];
+      *reinterpret_cast<f32x4*>(vd + 4 * LPR * i) = nv[i];
+    }
+  }
 
   // The wave's row groups (lanes dl, dl + LPR, ...) share the wave's max: sum them, then merge the waves
   // through LDS.
@@ -515,10 +570,18 @@ Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t h
   return p;
 }
 
+// Appended row of a single-row call: new K/V rows in, cache rows out (all null when nothing is appended).
+struct Append {
+  const float* k_new = nullptr;
+  const float* v_new = nullptr;
+  float* k_dst = nullptr;
+  float* v_dst = nullptr;
+};
+
 template <int HD>
 int launch_decode(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0, int64_t H,
                   int64_t KV, float* ws, const Plan& p, float qscale, const float2* q_rope, int q_rope_neox,
-                  hipStream_t s) {
+                  const Append& app, hipStream_t s) {
   float* ws_o = ws;
   float* ws_ml = ws ? ws + n * H * p.n_chunks * HD : nullptr;
   const int group = int(H / KV);
@@ -527,7 +590,8 @@ int launch_decode(const float* q, const float* k, const float* v, float* out, in
 #define NBH_DECODE(GB)                                                                                             \
   e = nbhs_timing::launch(NBHS_K_DECODE_PARTIAL, attn_decode_partial<HD, GB>, grid, dim3(kDecodeThreads), s, q, k, \
                           v, out, ws_o, ws_ml, pos0, int(H), int(KV), group, p.n_sub, p.n_chunks,                   \
-                          p.groups_per_chunk, p.extra_groups, qscale, q_rope, q_rope_neox)
+                          p.groups_per_chunk, p.extra_groups, qscale, q_rope, q_rope_neox, app.k_new, app.v_new,  \
+                          app.k_dst, app.v_dst)
   switch (p.gb) {
     case 1: NBH_DECODE(1); break;
     case 2: NBH_DECODE(2); break;
@@ -541,6 +605,31 @@ int launch_decode(const float* q, const float* k, const float* v, float* out, in
 }
 
 bool tiled_head_dim(int64_t hd) { return hd == 64 || hd == 128; }
+
+int decode(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0, int64_t n_heads,
+           int64_t n_kv_heads, int64_t head_dim, float* workspace, int64_t workspace_floats, int cu_count,
+           const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, const Append& app, hipStream_t s) {
+  if (!q || !k || !v || !out || n <= 0 || n > 65535 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 ||
+      n_heads % n_kv_heads != 0 || head_dim <= 0 || head_dim > 256 || n_heads > 65535)
+    return NBHS_EINVAL;
+  // q rotation on load is implemented for the tiled head sizes only, over table rows covering pos0 .. pos0+n-1
+  if (q_rope_cs && (!tiled_head_dim(head_dim) || pos0 + n > q_rope_rows)) return NBHS_EINVAL;
+  const float2* q_rope = reinterpret_cast<const float2*>(q_rope_cs);
+  const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
+  if (!tiled_head_dim(head_dim)) {
+    return nbhs_timing::launch(NBHS_K_GENERIC, attn_generic, dim3(unsigned(n_heads), unsigned(n)), dim3(64), s, q, k,
+                               v, out, pos0, int(n_heads), int(n_kv_heads), int(head_dim), qscale);
+  }
+  const Plan p = make_plan(n, pos0, n_heads, n_kv_heads, head_dim, cu_count);
+  const int64_t need = p.n_chunks == 1 ? 0 : n * n_heads * p.n_chunks * (head_dim + 2);
+  if (need > 0 && (!workspace || workspace_floats < need)) return NBHS_EINVAL;
+  if (n_kv_heads * p.n_sub > 65535) return NBHS_EINVAL;
+  if (head_dim == 64)
+    return launch_decode<64>(q, k, v, out, n, pos0, n_heads, n_kv_heads, workspace, p, qscale, q_rope, q_rope_neox,
+                             app, s);
+  return launch_decode<128>(q, k, v, out, n, pos0, n_heads, n_kv_heads, workspace, p, qscale, q_rope, q_rope_neox,
+                            app, s);
+}
 
 }  // namespace
 
@@ -567,25 +656,23 @@ int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* 
                          int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float* workspace,
                          int64_t workspace_floats, int cu_count, const float* q_rope_cs, int64_t q_rope_rows,
                          int q_rope_neox, nbhs_stream stream) {
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (!q || !k || !v || !out || n <= 0 || n > 65535 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 ||
-      n_heads % n_kv_heads != 0 || head_dim <= 0 || head_dim > 256 || n_heads > 65535)
-    return NBHS_EINVAL;
-  // q rotation on load is implemented for the tiled head sizes only, over table rows covering pos0 .. pos0+n-1
-  if (q_rope_cs && (!tiled_head_dim(head_dim) || pos0 + n > q_rope_rows)) return NBHS_EINVAL;
-  const float2* q_rope = reinterpret_cast<const float2*>(q_rope_cs);
-  const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
-  if (!tiled_head_dim(head_dim)) {
-    return nbhs_timing::launch(NBHS_K_GENERIC, attn_generic, dim3(unsigned(n_heads), unsigned(n)), dim3(64), s, q, k,
-                               v, out, pos0, int(n_heads), int(n_kv_heads), int(head_dim), qscale);
-  }
-  const Plan p = make_plan(n, pos0, n_heads, n_kv_heads, head_dim, cu_count);
-  const int64_t need = p.n_chunks == 1 ? 0 : n * n_heads * p.n_chunks * (head_dim + 2);
-  if (need > 0 && (!workspace || workspace_floats < need)) return NBHS_EINVAL;
-  if (n_kv_heads * p.n_sub > 65535) return NBHS_EINVAL;
-  if (head_dim == 64)
-    return launch_decode<64>(q, k, v, out, n, pos0, n_heads, n_kv_heads, workspace, p, qscale, q_rope, q_rope_neox, s);
-  return launch_decode<128>(q, k, v, out, n, pos0, n_heads, n_kv_heads, workspace, p, qscale, q_rope, q_rope_neox, s);
+  return decode(q, k, v, out, n, pos0, n_heads, n_kv_heads, head_dim, workspace, workspace_floats, cu_count,
+                q_rope_cs, q_rope_rows, q_rope_neox, Append{}, reinterpret_cast<hipStream_t>(stream));
+}
+
+int nbhs_append_attn_decode_f32(const float* q, float* k_cache, float* v_cache, const float* k_new,
+                                const float* v_new, float* out, int64_t pos0, int64_t n_heads, int64_t n_kv_heads,
+                                int64_t head_dim, float* workspace, int64_t workspace_floats, int cu_count,
+                                const float* rope_cs, int64_t rope_rows, int neox, nbhs_stream stream) {
+  // One query row, tiled head sizes, RoPE table required (it rotates q and the new K row alike).
+  if (!k_new || !v_new || !rope_cs || !tiled_head_dim(head_dim)) return NBHS_EINVAL;
+  Append app;
+  app.k_new = k_new;
+  app.v_new = v_new;
+  app.k_dst = k_cache;
+  app.v_dst = v_cache;
+  return decode(q, k_cache, v_cache, out, 1, pos0, n_heads, n_kv_heads, head_dim, workspace, workspace_floats,
+                cu_count, rope_cs, rope_rows, neox, app, reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -402,3 +402,73 @@ def test_append_rope_attention_equals_unfused(backend, H, KV, D, neox, llama3, n
     assert np.array_equal(bits(r1), bits(r2)), "outputs differ"
     assert np.array_equal(bits(gk1), bits(gk2)) and np.array_equal(bits(gv1), bits(gv2)), "caches differ"
     assert np.array_equal(bits(gq2), bits(q)), "fused op modified q"
+
+
+@pytest.mark.parametrize("H,KV,D,neox,llama3", [(32, 8, 64, False, True), (14, 2, 64, True, False),
+                                                 (16, 8, 128, True, False), (16, 4, 128, False, True)])
+@pytest.mark.parametrize("pos0", [0, 1, 31, 32, 33, 255, 1023, 4113, 32768])
+def test_append_rope_attention_decode_single_row(backend, H, KV, D, neox, llama3, pos0):
+    """Decode step of the fused op: the new row rides in the attention launch (the workgroup owning row pos0 takes it
+    from k_new / v_new). Output and caches are bit-identical to append_rope + attention at positions on both sides
+    of the 32-row group and chunk boundaries, and q is left unrotated."""
+    base = 5e5 if llama3 else 1e4
+    ff = synth.llama3_freq_factors(D, base) if llama3 else None
+    rng = np.random.default_rng(pos0 * 7 + D + H)
+    q = rng.standard_normal((1, H, D)).astype(np.float32)
+    kn = rng.standard_normal((1, KV, D)).astype(np.float32)
+    vn = rng.standard_normal((1, KV, D)).astype(np.float32)
+    k0 = rng.standard_normal((pos0 + 3, KV, D)).astype(np.float32)
+    v0 = rng.standard_normal((pos0 + 3, KV, D)).astype(np.float32)
+    with Buffers(backend) as B:
+        dq1, dq2, dkn, dvn = B.upload(q), B.upload(q), B.upload(kn), B.upload(vn)
+        ck1, cv1, ck2, cv2 = B.upload(k0), B.upload(v0), B.upload(k0), B.upload(v0)
+        o1, o2 = B.alloc(q.size), B.alloc(q.size)
+        backend.append_rope(dq1, ck1, cv1, dkn, dvn, 1, pos0, H, KV, D, base, neox, ff)
+        backend.attention(dq1, ck1, cv1, o1, 1, pos0, H, KV, D)
+        backend.append_rope_attention(dq2, ck2, cv2, dkn, dvn, o2, 1, pos0, H, KV, D, base, neox, ff)
+        r1, r2 = backend.download(o1, q.shape), backend.download(o2, q.shape)
+        gk1, gk2 = backend.download(ck1, k0.shape), backend.download(ck2, k0.shape)
+        gv1, gv2 = backend.download(cv1, v0.shape), backend.download(cv2, v0.shape)
+        gq2 = backend.download(dq2, q.shape)
+    assert np.array_equal(bits(r1), bits(r2)), "outputs differ"
+    assert np.array_equal(bits(gk1), bits(gk2)), "K caches differ"
+    assert np.array_equal(bits(gv1), bits(gv2)), "V caches differ"
+    assert np.array_equal(bits(gq2), bits(q)), "fused op modified q"
+    assert np.array_equal(bits(gk2[pos0 + 1:]), bits(k0[pos0 + 1:])), "rows after pos0 changed"
+    if pos0 <= 1023:
+        kr = oracle.rope(kn.copy(), pos0, base, neox, ff)
+        qr = oracle.rope(q.copy(), pos0, base, neox, ff)
+        assert np.array_equal(bits(gk2[pos0]), bits(kr[0])), "appended K row"
+        assert_parity(r2, cpu_attention(qr, np.concatenate([k0[:pos0], kr]), np.concatenate([v0[:pos0], vn]), pos0,
+                                        KV), f"fused decode pos0={pos0}")
+
+
+@pytest.mark.parametrize("pos0", [0, 5, 40, 20000])
+def test_append_rope_attention_decode_never_reads_the_unwritten_row(backend, pos0):
+    """The fused decode step must take row pos0 from k_new / v_new, not from the cache it is about to write: with
+    cache rows pos0.. poisoned with NaN the output is finite and bitwise equal to the unpoisoned run, row pos0 holds
+    the new row afterwards and the rows after it keep their NaN."""
+    H, KV, D = 32, 8, 64
+    rng = np.random.default_rng(pos0 + 99)
+    q = rng.standard_normal((1, H, D)).astype(np.float32)
+    kn = rng.standard_normal((1, KV, D)).astype(np.float32)
+    vn = rng.standard_normal((1, KV, D)).astype(np.float32)
+    k0 = rng.standard_normal((pos0 + 40, KV, D)).astype(np.float32)
+    v0 = rng.standard_normal((pos0 + 40, KV, D)).astype(np.float32)
+    kp, vp = k0.copy(), v0.copy()
+    kp[pos0:] = np.nan
+    vp[pos0:] = np.nan
+    with Buffers(backend) as B:
+        dq, dkn, dvn = B.upload(q), B.upload(kn), B.upload(vn)
+        ck1, cv1, ck2, cv2 = B.upload(k0), B.upload(v0), B.upload(kp), B.upload(vp)
+        o1, o2 = B.alloc(q.size), B.alloc(q.size)
+        backend.append_rope_attention(dq, ck1, cv1, dkn, dvn, o1, 1, pos0, H, KV, D, 1e4, False, None)
+        backend.append_rope_attention(dq, ck2, cv2, dkn, dvn, o2, 1, pos0, H, KV, D, 1e4, False, None)
+        r1, r2 = backend.download(o1, q.shape), backend.download(o2, q.shape)
+        gk1, gk2 = backend.download(ck1, k0.shape), backend.download(ck2, k0.shape)
+        gv2 = backend.download(cv2, v0.shape)
+    assert np.all(np.isfinite(r2))
+    assert np.array_equal(bits(r1), bits(r2))
+    assert np.array_equal(bits(gk1[pos0]), bits(gk2[pos0]))
+    assert np.array_equal(bits(gv2[pos0]), bits(vn[0]))
+    assert np.all(np.isnan(gk2[pos0 + 1:])) and np.all(np.isnan(gv2[pos0 + 1:]))
