@@ -36,18 +36,20 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kDecodeThreads = 256;  // 4 waves
-// Row slots in flight per lane per tensor, and the split target in workgroups per CU. Compile-time so that tuning
-// sweeps can build variants; the defaults are the measured best on MI355X.
+// Row slots in flight per lane per tensor, and the split targets in workgroups per CU: short contexts use
+// NBH_DECODE_WG_PER_CU, long ones (at least kLongGroups row groups per chunk at the higher count) up to
+// NBH_DECODE_WG_PER_CU_LONG. Compile-time so that tuning sweeps can build variants; the defaults are the measured
+// best on MI355X (3 per CU streams 128k contexts 6 % faster, is even at 32k and 7 % slower at 8k).
 #ifndef NBH_DECODE_UNROLL
 #define NBH_DECODE_UNROLL 1
 #endif
 #ifndef NBH_DECODE_WG_PER_CU
 #define NBH_DECODE_WG_PER_CU 2
 #endif
-// Software pipelining: the next iteration's K/V loads are issued before the current iteration is computed.
-#ifndef NBH_DECODE_PIPELINE
-#define NBH_DECODE_PIPELINE 0
+#ifndef NBH_DECODE_WG_PER_CU_LONG
+#define NBH_DECODE_WG_PER_CU_LONG 3
 #endif
+constexpr int64_t kLongGroups = 12;
 // K/V rows are read exactly once per step: stream them past the caches (non-temporal loads) unless disabled.
 #ifndef NBH_DECODE_NT
 #define NBH_DECODE_NT 1
@@ -191,11 +193,11 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
     }
   };
 
+  Rows ra, rb;
   // The first K/V loads go out before the query loads, so the first HBM round trip is not spent on q alone. A
   // chunk holding an extra group loads its first two groups together: the extra group's round trip overlaps the
   // first one instead of adding one, so every chunk takes groups_per_chunk round trips.
   int64_t it = 0;  // iterations done
-  Rows ra, rb;
   if (gcnt > 0) load(g0, ra);
   const bool two = extra && gcnt > 1;
   if (two) load(g0 + gstride, rb);
@@ -308,16 +310,6 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
     }
   };
 
-#if NBH_DECODE_PIPELINE
-  while (it < gcnt) {
-    if (it + 1 < gcnt) load(g0 + (it + 1) * gstride, rb);
-    compute(ra, g0 + it * gstride);
-    if (it + 1 >= gcnt) break;
-    if (it + 2 < gcnt) load(g0 + (it + 2) * gstride, ra);
-    compute(rb, g0 + (it + 1) * gstride);
-    it += 2;
-  }
-#else
   if (two) {
     compute(ra, g0);
     compute(rb, g0 + gstride);
@@ -329,7 +321,6 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
     ++it;
     if (it < gcnt) load(g0 + it * gstride, ra);
   }
-#endif
 
   // The appended row goes into its cache row once per KV head (head subgroup 0 of the owner).
   if (owner && sg == 0 && wave == 0 && lane < LPR) {
@@ -525,7 +516,7 @@ struct Plan {
 };
 
 // Workgroups of attn_decode_partial<HD, GB> that fit on one CU at once (register and LDS limits), capped at
-// NBH_DECODE_WG_PER_CU; queried from the runtime once per instance.
+// NBH_DECODE_WG_PER_CU_LONG; queried from the runtime once per instance.
 template <int HD, int GB>
 int resident_per_cu() {
   static const int n = [] {
@@ -534,7 +525,7 @@ int resident_per_cu() {
             hipSuccess ||
         b < 1)
       b = 1;
-    return b < NBH_DECODE_WG_PER_CU ? b : NBH_DECODE_WG_PER_CU;
+    return b < NBH_DECODE_WG_PER_CU_LONG ? b : NBH_DECODE_WG_PER_CU_LONG;
   }();
   return n;
 }
@@ -560,7 +551,12 @@ Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t h
   const int64_t lpr = head_dim / 8;
   const int64_t step = (64 / lpr) * kUnroll * (kDecodeThreads / 64);  // rows a workgroup covers per iteration
   const int64_t units = (max_len + step - 1) / step;
-  int64_t slots = int64_t(cu_count > 0 ? cu_count : 256) * resident_per_cu(head_dim, p.gb) / (n * n_kv * p.n_sub);
+  const int64_t cus = cu_count > 0 ? cu_count : 256;
+  const int64_t streams = n * n_kv * p.n_sub;  // workgroups per chunk index
+  const int resident = resident_per_cu(head_dim, p.gb);
+  int64_t slots = cus * resident / streams;
+  if (resident > NBH_DECODE_WG_PER_CU && units < kLongGroups * slots)
+    slots = cus * NBH_DECODE_WG_PER_CU / streams;  // short context: fewer, longer workgroups
   if (slots < 1) slots = 1;
   int64_t chunks = units < slots ? units : slots;
   if (chunks > kMaxChunks) chunks = kMaxChunks;
@@ -648,7 +644,9 @@ int64_t nbhs_attn_decode_workspace_bound(int64_t n_heads, int cu_count) {
   // With T = the workgroup target, a call with n rows that splits at all uses at most T / n chunks per query head,
   // so n * chunks <= T (the bound keeps twice that); each partial holds at most 128 + 2 floats per query head.
   if (n_heads <= 0) return -1;
-  const int64_t slots = int64_t(cu_count > 0 ? cu_count : 256) * NBH_DECODE_WG_PER_CU;
+  const int64_t slots = int64_t(cu_count > 0 ? cu_count : 256) *
+                        (NBH_DECODE_WG_PER_CU_LONG > NBH_DECODE_WG_PER_CU ? NBH_DECODE_WG_PER_CU_LONG
+                                                                         : NBH_DECODE_WG_PER_CU);
   return n_heads * (2 * slots + 16) * (128 + 2);
 }
 
