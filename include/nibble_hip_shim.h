@@ -105,21 +105,25 @@ int nbhs_append_stage_kv_f16(float* cache_k, float* cache_v, const float* k_new,
                              int64_t pos0, int64_t n_kv_heads, int64_t head_dim, const float* cs_table,
                              int64_t table_rows, int neox, void* k16, void* vt16, nbhs_stream s);
 
-/* Causal GQA attention for n query rows at positions pos0.. on gfx950 MFMA (v_mfma_f32_32x32x16_f16): Q rounded
- * to fp16 after scaling by log2(e)/sqrt(head_dim), K/V from the staged fp16 copies, softmax and accumulators in
- * fp32. head_dim 64 or 128. The staged copies must cover rows [0, pos0+n). q_rope_cs as for
- * nbhs_attn_decode_f32. */
+/* Causal GQA attention for n query rows at positions pos0.. (the prefill case of CpuBackend::attention,
+ * cpu_backend.cpp:271-290). Rows [fp32_rows, n) run on gfx950 MFMA (v_mfma_f32_32x32x16_f16): Q rounded to fp16
+ * after scaling by log2(e)/sqrt(head_dim), K/V from the staged fp16 copies, softmax and accumulators in fp32. Rows
+ * [0, fp32_rows) (0 <= fp32_rows < n) are computed in fp32 from the caches k_cache / v_cache, exactly as
+ * nbhs_attn_decode_f32 computes a single-chunk row, by workgroups of the same launch. head_dim 64 or 128. The
+ * staged copies must cover rows [0, pos0+n). q_rope_cs as for nbhs_attn_decode_f32. */
 int nbhs_attn_prefill_mfma(const float* q, const void* k16, const void* vt16, float* out, int64_t n, int64_t pos0,
                            int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t staged_rows_pad,
-                           const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, nbhs_stream s);
+                           const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, const float* k_cache,
+                           const float* v_cache, int64_t fp32_rows, nbhs_stream s);
 
 /* Synthetic N(0,1)*scale data for benchmarks: counter-based (SplitMix64 of seed and index), Box-Muller in fp32. */
 int nbhs_fill_normal_f32(float* dst, int64_t count, uint64_t seed, float scale, nbhs_stream s);
 
 /* ---- per-kernel timing (measurement only) ----
- * While enabled, every launcher records a HIP event pair on its own stream around each launch of its kernel, so
- * the average device duration of one kernel can be read back live (bench.py's roofline figures). Off by default;
- * enabling it adds two event records per launch. Not thread-safe. */
+ * While enabled for a kernel, its launcher launches it with a HIP event pair (hipExtLaunchKernel) stamped from the
+ * dispatch itself, so the average device duration of that kernel can be read back live (bench.py's roofline
+ * figures); the other kernels launch as usual. Timing a kernel alone keeps the event handling of its neighbours'
+ * launches from changing what it is measured against. Off by default. Not thread-safe. */
 enum nbhs_kernel_id {
   NBHS_K_ROPE = 0,
   NBHS_K_APPEND_ROPE = 1,
@@ -130,7 +134,8 @@ enum nbhs_kernel_id {
   NBHS_K_PREFILL_MFMA = 6,
   NBHS_K_COUNT = 7
 };
-int nbhs_kernel_timing_enable(int on); /* on != 0: start recording (clears what was recorded) */
+int nbhs_kernel_timing_enable(int on); /* on != 0: time every kernel; 0: none (clears what was recorded) */
+int nbhs_kernel_timing_select(uint32_t kernel_mask); /* time the kernels whose bit (1 << id) is set; clears */
 /* Waits for the recorded launches of `kernel` and returns their summed duration and count, then clears them. */
 int nbhs_kernel_timing_read(int kernel, double* total_ms, int64_t* launches);
 

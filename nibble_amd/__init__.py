@@ -224,12 +224,14 @@ class KernelTiming:
     ROPE, APPEND_ROPE, DECODE_PARTIAL, DECODE_COMBINE, GENERIC, STAGE_KV, PREFILL_MFMA = range(7)
 
     @staticmethod
-    def enable(on: bool = True):
+    def enable(on: bool = True, only: int | None = None):
+        """Time every kernel (on), none (not on), or - with `only` - that one kernel alone."""
         L = lib()
-        L.nbhs_kernel_timing_enable.argtypes = [c_int]
-        L.nbhs_kernel_timing_enable.restype = c_int
-        if L.nbhs_kernel_timing_enable(int(on)) != 0:
-            raise BackendError("nbhs_kernel_timing_enable failed")
+        L.nbhs_kernel_timing_select.argtypes = [ctypes.c_uint32]
+        L.nbhs_kernel_timing_select.restype = c_int
+        mask = 0 if not on else (1 << only if only is not None else 0xFFFFFFFF)
+        if L.nbhs_kernel_timing_select(mask) != 0:
+            raise BackendError("nbhs_kernel_timing_select failed")
 
     @staticmethod
     def read(kernel: int) -> tuple[float, int]:

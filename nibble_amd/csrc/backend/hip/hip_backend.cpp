@@ -377,12 +377,14 @@ void HipBackend::run_attention(const float* q, const float* k, const float* v, f
   } else if (split < n) {
     check(nbhs_stage_kv_f16(k, v, k16_, vt16_, rows, n_kv_heads, head_dim, stream_), "attention (staging)");
   }
-  if (split > 0) decode_rows(q, out, split, pos0);
-  if (split == n) return;
+  if (split == n) {
+    decode_rows(q, out, split, pos0);
+    return;
+  }
+  // rows [0, split) in fp32 and the rest on MFMA, in one launch
   const int64_t rows_pad = halves / (n_kv_heads * head_dim);
-  check(nbhs_attn_prefill_mfma(q + split * n_heads * head_dim, k16_, vt16_, out + split * n_heads * head_dim,
-                               n - split, pos0 + split, n_heads, n_kv_heads, head_dim, rows_pad, rope_table, rope_rows,
-                               neox ? 1 : 0, stream_),
+  check(nbhs_attn_prefill_mfma(q, k16_, vt16_, out, n, pos0, n_heads, n_kv_heads, head_dim, rows_pad, rope_table,
+                               rope_rows, neox ? 1 : 0, k, v, split, stream_),
         "attention (prefill kernel)");
 }
 

@@ -18,7 +18,7 @@ struct Record {
   int kernel;
   hipEvent_t start, end;
 };
-bool g_enabled = false;
+uint32_t g_mask = 0;  // bit k: launches of kernel k are timed
 std::vector<Record> g_records;
 
 void drop_all() {
@@ -30,7 +30,7 @@ void drop_all() {
 }
 }  // namespace
 
-bool enabled() { return g_enabled; }
+bool enabled(int kernel) { return kernel >= 0 && kernel < 32 && ((g_mask >> kernel) & 1u) != 0; }
 
 hipError_t make_pair(hipEvent_t* start, hipEvent_t* end) {
   hipError_t e = hipEventCreate(start);
@@ -271,9 +271,11 @@ int nbhs_fill_normal_f32(float* dst, int64_t count, uint64_t seed, float scale, 
   return hipGetLastError();
 }
 
-int nbhs_kernel_timing_enable(int on) {
+int nbhs_kernel_timing_enable(int on) { return nbhs_kernel_timing_select(on ? ~0u : 0u); }
+
+int nbhs_kernel_timing_select(uint32_t kernel_mask) {
   nbhs_timing::drop_all();
-  nbhs_timing::g_enabled = on != 0;
+  nbhs_timing::g_mask = kernel_mask;
   return hipSuccess;
 }
 

@@ -10,7 +10,7 @@
 
 namespace nbhs_timing {
 
-bool enabled();
+bool enabled(int kernel);  // are launches of `kernel` timed?
 // Creates the event pair for one timed dispatch.
 hipError_t make_pair(hipEvent_t* start, hipEvent_t* end);
 // Takes ownership of an event pair stamped around one dispatch of `kernel`.
@@ -27,7 +27,7 @@ hipError_t launch(int kernel, void (*fn)(P...), dim3 grid, dim3 block, hipStream
     ((ptrs[i++] = static_cast<void*>(&x)), ...);
   }, args);
   const void* f = reinterpret_cast<const void*>(fn);
-  if (!enabled()) return hipLaunchKernel(f, grid, block, ptrs, 0, s);
+  if (!enabled(kernel)) return hipLaunchKernel(f, grid, block, ptrs, 0, s);
   hipEvent_t e0 = nullptr, e1 = nullptr;
   hipError_t e = make_pair(&e0, &e1);
   if (e != hipSuccess) return e;

@@ -25,11 +25,15 @@
 //  * Scheduling: workgroup b takes KV head b % KV and row tiles from the longest (last) to the shortest, so
 //    long causal rows start first and, with workgroups dispatched round-robin over the 8 XCDs, one KV head's
 //    tiles stay in one XCD's L2.
+//  * Rows kept in fp32 (the first ones, whose few keys do not average out fp16 rounding of V) ride in the same
+//    launch: workgroups after the MFMA tiles run the fp32 split-context body (nbh_decode::partial_block, one
+//    chunk per row) from the fp32 cache, in the tail the shortest MFMA tiles leave.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 
 #include "backend/hip/kernel_timing.h"
+#include "kernels/decode_block.h"
 #include "kernels/rope_device.h"
 #include "nibble_hip_shim.h"
 
@@ -180,7 +184,23 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(
 void attn_prefill_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16,
     float* __restrict__ out, int64_t n, int64_t pos0, int n_heads, int n_kv, int group, int64_t rows_pad,
-    int n_tiles, float qscale, const float2* __restrict__ q_rope, int q_rope_neox) {
+    int n_tiles, float qscale, const float2* __restrict__ q_rope, int q_rope_neox, const float* __restrict__ kc,
+    const float* __restrict__ vc, int64_t fp32_rows, int fp32_n_sub) {
+  // Workgroups past the MFMA tiles: query row t < fp32_rows of the call (q and out start fp32_rows rows before
+  // this launch's MFMA rows) for KV head x head subgroup `by`, in fp32 over its whole causal window.
+  static_assert(kWaves * 64 == nbh_decode::kDecodeThreads, "the fp32 rows' body runs on the MFMA workgroup size");
+  if (int64_t(blockIdx.x) >= int64_t(n_tiles) * n_kv) {
+    const int64_t e = int64_t(blockIdx.x) - int64_t(n_tiles) * n_kv;
+    const int streams = n_kv * fp32_n_sub;
+    const int64_t p0 = pos0 - fp32_rows;
+    constexpr int64_t kStepRows = (nbh_decode::kDecodeThreads / 64) * (64 / (HD / 8)) * nbh_decode::kUnroll;
+    nbh_decode::partial_block<HD, 4>(q - fp32_rows * n_heads * HD, kc, vc, out - fp32_rows * n_heads * HD, nullptr,
+                                     nullptr, p0, n_heads, n_kv, group, fp32_n_sub, 1,
+                                     (p0 + fp32_rows + kStepRows - 1) / kStepRows, 0, qscale, q_rope, q_rope_neox,
+                                     nullptr, nullptr, nullptr, nullptr, 0, int(e % streams),
+                                     fp32_rows - 1 - e / streams);  // longest rows first
+    return;
+  }
   constexpr int DC = HD / 16;  // 16-wide d chunks of the S^T contraction
   constexpr int DT = HD / 32;  // 32-row d tiles of O^T
   // K and V^T tiles live in LDS unpadded, one row of 16-byte chunks per key (K) or per dimension (V^T), with chunk
@@ -516,22 +536,28 @@ int nbhs_append_stage_kv_f16(float* cache_k, float* cache_v, const float* k_new,
 
 int nbhs_attn_prefill_mfma(const float* q, const void* k16, const void* vt16, float* out, int64_t n, int64_t pos0,
                            int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t staged_rows_pad,
-                           const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, nbhs_stream stream) {
+                           const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, const float* k_cache,
+                           const float* v_cache, int64_t fp32_rows, nbhs_stream stream) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (!q || !k16 || !vt16 || !out || n <= 0 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 ||
       n_heads % n_kv_heads != 0 || (head_dim != 64 && head_dim != 128) || staged_rows_pad % kBN != 0 ||
-      staged_rows_pad < round_up(pos0 + n, kBN) || (q_rope_cs && pos0 + n > q_rope_rows))
+      staged_rows_pad < round_up(pos0 + n, kBN) || (q_rope_cs && pos0 + n > q_rope_rows) || fp32_rows < 0 ||
+      fp32_rows >= n || (fp32_rows > 0 && (!k_cache || !v_cache)))
     return NBHS_EINVAL;
   const int64_t group = n_heads / n_kv_heads;
-  const int64_t tiles = (n * group + kRowsPerBlock - 1) / kRowsPerBlock;
-  if (tiles * n_kv_heads > int64_t(1) << 31) return NBHS_EINVAL;
+  const int64_t n_mfma = n - fp32_rows;
+  const int64_t tiles = (n_mfma * group + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int64_t fp32_sub = (group + 3) / 4;  // head subgroups of the fp32 rows' workgroups (4 query heads each)
+  const int64_t blocks = tiles * n_kv_heads + fp32_rows * n_kv_heads * fp32_sub;
+  if (blocks >= int64_t(1) << 31) return NBHS_EINVAL;
   const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
-  const unsigned blocks = unsigned(tiles * n_kv_heads);
+  const int64_t off = fp32_rows * n_heads * head_dim;  // the MFMA rows start fp32_rows rows in
   return nbhs_timing::launch(NBHS_K_PREFILL_MFMA, head_dim == 64 ? attn_prefill_kernel<64> : attn_prefill_kernel<128>,
-                             dim3(blocks), dim3(kWaves * 64), s, q, static_cast<const _Float16*>(k16),
-                             static_cast<const _Float16*>(vt16), out, n, pos0, int(n_heads), int(n_kv_heads),
-                             int(group), staged_rows_pad, int(tiles), qscale,
-                             reinterpret_cast<const float2*>(q_rope_cs), q_rope_neox);
+                             dim3(unsigned(blocks)), dim3(kWaves * 64), s, q + off, static_cast<const _Float16*>(k16),
+                             static_cast<const _Float16*>(vt16), out + off, n_mfma, pos0 + fp32_rows, int(n_heads),
+                             int(n_kv_heads), int(group), staged_rows_pad, int(tiles), qscale,
+                             reinterpret_cast<const float2*>(q_rope_cs), q_rope_neox, k_cache, v_cache, fp32_rows,
+                             int(fp32_sub));
 }
 
 }  // extern "C"
