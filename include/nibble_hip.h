@@ -93,6 +93,24 @@ int nbh_backend_append_rope_attention(nbh_backend* be, const float* q, float* k_
                                       int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float freq_base, int neox,
                                       const float* freq_factors);
 
+/* Ragged batch of single-token decodes. No counterpart in the reference, whose Backend serves one sequence: each
+ * sequence i is Backend::attention (backend.h:68-69) with n = 1 - query row q[i] [n_heads, head_dim] at position
+ * pos0[i] over its own layer caches k_cache[i], v_cache[i] - and equals that call within rounding. q, k_cache,
+ * v_cache and out are host arrays of n_seq device pointers, pos0 a host array. One launch pair streams every
+ * sequence's cache at once (head_dim 64 and 128; other sizes run one call per sequence). */
+int nbh_backend_attention_batch(nbh_backend* be, int64_t n_seq, const float* const* q, const float* const* k_cache,
+                                const float* const* v_cache, float* const* out, const int64_t* pos0, int64_t n_heads,
+                                int64_t n_kv_heads, int64_t head_dim);
+
+/* The batch with each sequence's new K/V row (k_new[i], v_new[i] [n_kv_heads, head_dim]) appended first at row
+ * pos0[i] and q read unrotated: nbh_backend_append_rope_attention with n = 1 for every sequence (the per-layer
+ * sequence of src/model/transformer.cpp:171-202), appended rows bit-identical. */
+int nbh_backend_append_rope_attention_batch(nbh_backend* be, int64_t n_seq, const float* const* q,
+                                            float* const* k_cache, float* const* v_cache, const float* const* k_new,
+                                            const float* const* v_new, float* const* out, const int64_t* pos0,
+                                            int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float freq_base,
+                                            int neox, const float* freq_factors);
+
 /* Extension of Backend::reserve for shapes ReserveParams does not carry: sizes the prefill operand staging
  * (n_kv_heads x head_dim at the reserved n_ctx) so that the first prefill allocates nothing. */
 int nbh_backend_reserve_attention(nbh_backend* be, int64_t n_kv_heads, int64_t head_dim);

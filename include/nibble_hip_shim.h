@@ -92,6 +92,23 @@ int nbhs_append_attn_decode_f32(const float* q, float* k_cache, float* v_cache, 
                                 int64_t head_dim, float* workspace, int64_t workspace_floats, int cu_count,
                                 const float* rope_cs, int64_t rope_rows, int neox, nbhs_stream s);
 
+/* Ragged batch of single-row decodes (one launch pair for all sequences; an extension the reference's single-session
+ * Backend has no counterpart for - each sequence i is exactly Backend::attention with n = 1, backend.h:68-69):
+ * query row q[i] [n_heads, head_dim] at position pos0[i] attends to rows 0..pos0[i] of its own caches k[i], v[i]
+ * [>= pos0[i] + 1 rows, n_kv_heads, head_dim]; the result goes to out[i]. The arrays are host arrays of device
+ * pointers. With k_new / v_new (host arrays, or both NULL), row pos0[i] of each cache first receives
+ * rope(k_new[i]) and v_new[i], and q[i] is given unrotated and rotated on load (rope_cs required, covering every
+ * pos0[i]) - as nbhs_append_attn_decode_f32 per sequence. head_dim 64 or 128. Sequences go 32 to a launch;
+ * workspace_floats must be >= nbhs_attn_decode_batch_workspace(...) for the same positions. Results equal each
+ * sequence's own nbhs_attn_decode_f32 call within rounding (the chunking differs); appended rows are bit-exact. */
+int64_t nbhs_attn_decode_batch_workspace(int64_t n_seq, const int64_t* pos0, int64_t n_heads, int64_t n_kv_heads,
+                                         int64_t head_dim, int cu_count);
+int nbhs_attn_decode_batch_f32(int64_t n_seq, const float* const* q, const float* const* k, const float* const* v,
+                               float* const* out, const float* const* k_new, const float* const* v_new,
+                               const int64_t* pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                               float* workspace, int64_t workspace_floats, int cu_count, const float* rope_cs,
+                               int64_t rope_rows, int neox, nbhs_stream s);
+
 /* Operand staging for the MFMA prefill: cache rows [0, rows) of k and v [rows, n_kv_heads, head_dim] fp32 are
  * rounded to fp16 into k16 [n_kv_heads, rows_pad, head_dim] and vt16 [n_kv_heads, head_dim, rows_pad]
  * (transposed), rows_pad = rows rounded up to 64, padding zero-filled. */

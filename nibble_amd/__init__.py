@@ -37,6 +37,11 @@ _SIGNATURES = {
                                         _I, c_float, c_int, c_void_p]),
     "nbh_backend_append_rope_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                                   c_void_p, _I, _I, _I, _I, _I, c_float, c_int, c_void_p]),
+    "nbh_backend_attention_batch": (c_int, [c_void_p, _I, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, _I, _I,
+                                            _I]),
+    "nbh_backend_append_rope_attention_batch": (c_int, [c_void_p, _I, c_void_p, c_void_p, c_void_p, c_void_p,
+                                                        c_void_p, c_void_p, c_void_p, _I, _I, _I, c_float, c_int,
+                                                        c_void_p]),
     "nbh_backend_reserve_attention": (c_int, [c_void_p, _I, _I]),
     "nbh_backend_reserve_rope": (c_int, [c_void_p, _I, c_float, c_int, c_void_p]),
     "nbh_backend_sync": (c_int, [c_void_p]),
@@ -51,6 +56,17 @@ _SIGNATURES = {
 }
 
 _lib = None
+
+
+def _batch_arrays(pointer_lists, pos0):
+    """Host arrays for a batch call: one c_void_p array per list of device pointers, and the positions as int64.
+    The arrays are returned so that they outlive the call."""
+    n = len(pos0)
+    if any(len(x) != n for x in pointer_lists):
+        raise BackendError("batch: every pointer list must hold one entry per position")
+    arrs = [(c_void_p * max(n, 1))(*[int(x) for x in lst]) for lst in pointer_lists]
+    pa = (c_int64 * max(n, 1))(*[int(x) for x in pos0])
+    return n, arrs, pa
 
 
 class BackendError(RuntimeError):
@@ -155,6 +171,21 @@ class HipBackend:
             self._h, c_void_p(int(q)), c_void_p(int(k_cache)), c_void_p(int(v_cache)), c_void_p(int(k_new)),
             c_void_p(int(v_new)), c_void_p(int(out)), n, pos0, n_heads, n_kv_heads, head_dim, freq_base,
             int(bool(neox)), None if ff is None else _host_ptr(ff)))
+
+    def attention_batch(self, q, k_cache, v_cache, out, pos0, n_heads, n_kv_heads, head_dim):
+        """Ragged batch of single-token decodes: sequence i is attention(q[i], k_cache[i], v_cache[i], out[i], 1,
+        pos0[i], ...) over its own caches; the lists hold device pointers, pos0 positions."""
+        n, arrs, pa = _batch_arrays([q, k_cache, v_cache, out], pos0)
+        _check(lib().nbh_backend_attention_batch(self._h, n, *arrs, pa, n_heads, n_kv_heads, head_dim))
+
+    def append_rope_attention_batch(self, q, k_cache, v_cache, k_new, v_new, out, pos0, n_heads, n_kv_heads,
+                                    head_dim, freq_base, neox, freq_factors=None):
+        """append_rope_attention with n = 1 for every sequence of a ragged batch, in one launch pair."""
+        n, arrs, pa = _batch_arrays([q, k_cache, v_cache, k_new, v_new, out], pos0)
+        ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
+        _check(lib().nbh_backend_append_rope_attention_batch(self._h, n, *arrs, pa, n_heads, n_kv_heads, head_dim,
+                                                             freq_base, int(bool(neox)),
+                                                             None if ff is None else _host_ptr(ff)))
 
     def reserve_attention(self, n_kv_heads: int, head_dim: int):
         _check(lib().nbh_backend_reserve_attention(self._h, n_kv_heads, head_dim))

@@ -302,6 +302,62 @@ void HipBackend::append_rope_attention(const float* q, float* k_cache, float* v_
   run_attention(q, k_cache, v_cache, out, n, pos0, n_heads, n_kv_heads, head_dim, table, rows, p.neox, &app, &p);
 }
 
+void HipBackend::attention_batch(int64_t n_seq, const float* const* q, const float* const* k_cache,
+                                 const float* const* v_cache, float* const* out, const int64_t* pos0, int64_t n_heads,
+                                 int64_t n_kv_heads, int64_t head_dim) {
+  run_batch(n_seq, q, k_cache, v_cache, out, nullptr, nullptr, pos0, n_heads, n_kv_heads, head_dim, nullptr,
+            "attention_batch");
+}
+
+void HipBackend::append_rope_attention_batch(int64_t n_seq, const float* const* q, float* const* k_cache,
+                                             float* const* v_cache, const float* const* k_new,
+                                             const float* const* v_new, float* const* out, const int64_t* pos0,
+                                             int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                             const RopeParams& p) {
+  if (n_seq > 0 && (!k_new || !v_new)) throw Error("append_rope_attention_batch: k_new / v_new arrays are null");
+  run_batch(n_seq, q, k_cache, v_cache, out, k_new, v_new, pos0, n_heads, n_kv_heads, head_dim, &p,
+            "append_rope_attention_batch");
+}
+
+void HipBackend::run_batch(int64_t n_seq, const float* const* q, const float* const* k, const float* const* v,
+                           float* const* out, const float* const* k_new, const float* const* v_new,
+                           const int64_t* pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                           const RopeParams* p, const char* op) {
+  if (n_seq < 0) throw Error(std::string(op) + ": negative sequence count " + str(n_seq));
+  if (n_seq == 0) return;
+  if (!q || !k || !v || !out || !pos0) throw Error(std::string(op) + ": a pointer array is null");
+  if (p && head_dim % 2 != 0) throw Error(std::string(op) + ": head_dim must be even, got " + str(head_dim));
+  int64_t max_pos = 0;
+  for (int64_t i = 0; i < n_seq; ++i) {
+    check_attention_args(q[i], k[i], v[i], out[i], 1, pos0[i], n_heads, n_kv_heads, head_dim, op);
+    if (p) {
+      check_range(k_new[i], n_kv_heads * head_dim, op, "k_new");
+      check_range(v_new[i], n_kv_heads * head_dim, op, "v_new");
+    }
+    max_pos = std::max(max_pos, pos0[i]);
+  }
+  if (head_dim != 64 && head_dim != 128) {  // no batch kernel for these sizes: one call per sequence
+    for (int64_t i = 0; i < n_seq; ++i) {
+      if (p)
+        append_rope_attention(q[i], const_cast<float*>(k[i]), const_cast<float*>(v[i]), k_new[i], v_new[i], out[i],
+                              1, pos0[i], n_heads, n_kv_heads, head_dim, *p);
+      else
+        attention(q[i], k[i], v[i], out[i], 1, pos0[i], n_heads, n_kv_heads, head_dim);
+    }
+    return;
+  }
+  const float* table = nullptr;
+  int64_t rows = 0;
+  if (p) table = rope_table(head_dim, max_pos + 1, *p, &rows);
+  const int64_t ws = nbhs_attn_decode_batch_workspace(n_seq, pos0, n_heads, n_kv_heads, head_dim, cu_count_);
+  if (ws < 0) throw Error(std::string(op) + ": invalid batch shape");
+  ensure(decode_ws_, decode_ws_bytes_, size_t(ws) * sizeof(float));
+  check(nbhs_attn_decode_batch_f32(n_seq, q, k, v, out, k_new, v_new, pos0, n_heads, n_kv_heads, head_dim,
+                                   decode_ws_, int64_t(decode_ws_bytes_ / sizeof(float)), cu_count_, table, rows,
+                                   p && p->neox ? 1 : 0, stream_),
+        op);
+}
+
 void HipBackend::check_attention_args(const float* q, const float* k, const float* v, const float* out, int64_t n,
                                       int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
                                       const char* op) const {

@@ -64,6 +64,20 @@ class HipBackend final : public Backend {
   void append_rope_attention(const float* q, float* k_cache, float* v_cache, const float* k_new, const float* v_new,
                              float* out, int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads,
                              int64_t head_dim, const RopeParams& p);
+  // Ragged batch of single-token decodes - an extension with no counterpart in the reference, whose Backend serves
+  // one sequence: host arrays of n_seq device pointers and positions, sequence i being attention(q[i], k_cache[i],
+  // v_cache[i], out[i], 1, pos0[i], ...) over its own caches (equal within rounding: the context split differs).
+  // One launch pair streams every sequence's cache at once on the MFMA head sizes (64, 128); other head sizes run
+  // one call per sequence.
+  void attention_batch(int64_t n_seq, const float* const* q, const float* const* k_cache, const float* const* v_cache,
+                       float* const* out, const int64_t* pos0, int64_t n_heads, int64_t n_kv_heads,
+                       int64_t head_dim);
+  // The same with each sequence's new K/V row appended first and q rotated on load: append_rope_attention with
+  // n = 1 for every sequence (appended rows bit-identical).
+  void append_rope_attention_batch(int64_t n_seq, const float* const* q, float* const* k_cache,
+                                   float* const* v_cache, const float* const* k_new, const float* const* v_new,
+                                   float* const* out, const int64_t* pos0, int64_t n_heads, int64_t n_kv_heads,
+                                   int64_t head_dim, const RopeParams& p);
   void fill_normal(float* dst, int64_t count, uint64_t seed, float scale);
   void sync();
   nbhs_stream stream() const { return stream_; }
@@ -91,6 +105,9 @@ class HipBackend final : public Backend {
   void run_attention(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
                      int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const float* rope_table,
                      int64_t rope_rows, bool neox, const AppendRows* app, const RopeParams* rp);
+  void run_batch(int64_t n_seq, const float* const* q, const float* const* k, const float* const* v,
+                 float* const* out, const float* const* k_new, const float* const* v_new, const int64_t* pos0,
+                 int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const RopeParams* p, const char* op);
   void check(int code, const char* what) const;
   // Throws unless [p, p + n_floats) lies inside one buffer from alloc().
   void check_range(const void* p, int64_t n_floats, const char* op, const char* arg) const;

@@ -129,6 +129,23 @@ int nbh_backend_append_rope_attention(nbh_backend* be, const float* q, float* k_
   });
 }
 
+int nbh_backend_attention_batch(nbh_backend* be, int64_t n_seq, const float* const* q, const float* const* k_cache,
+                                const float* const* v_cache, float* const* out, const int64_t* pos0, int64_t n_heads,
+                                int64_t n_kv_heads, int64_t head_dim) {
+  return guarded([&] { B(be).attention_batch(n_seq, q, k_cache, v_cache, out, pos0, n_heads, n_kv_heads, head_dim); });
+}
+
+int nbh_backend_append_rope_attention_batch(nbh_backend* be, int64_t n_seq, const float* const* q,
+                                            float* const* k_cache, float* const* v_cache, const float* const* k_new,
+                                            const float* const* v_new, float* const* out, const int64_t* pos0,
+                                            int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float freq_base,
+                                            int neox, const float* freq_factors) {
+  return guarded([&] {
+    B(be).append_rope_attention_batch(n_seq, q, k_cache, v_cache, k_new, v_new, out, pos0, n_heads, n_kv_heads,
+                                      head_dim, RopeParams{freq_base, neox != 0, freq_factors});
+  });
+}
+
 int nbh_backend_reserve_attention(nbh_backend* be, int64_t n_kv_heads, int64_t head_dim) {
   return guarded([&] { B(be).reserve_attention(n_kv_heads, head_dim); });
 }

@@ -4,6 +4,7 @@
 // The per-workgroup body is partial_block (kernels/decode_block.h), shared with the prefill kernel.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "backend/hip/kernel_timing.h"
@@ -48,9 +49,8 @@ __device__ __forceinline__ float block_reduce(float x, float* scratch) {
 // trip for up to kPer chunks each), the global max comes from a block reduction, and the weighted sums of the
 // chunk groups are added through LDS.
 template <int HD>
-__global__ __launch_bounds__(kDecodeThreads) void attn_decode_combine(const float* __restrict__ ws_o,
-                                                                      const float* __restrict__ ws_ml,
-                                                                      float* __restrict__ out, int n_chunks) {
+__device__ __forceinline__ void combine_block(const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
+                                              float* __restrict__ out, int n_chunks, int64_t rh) {
   constexpr int V4 = HD / 4;                // float4 columns of one head row
   constexpr int CG = kDecodeThreads / V4;   // chunk groups
   constexpr int kPer = 16;                  // chunks per thread held in registers
@@ -59,7 +59,6 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_combine(const floa
   __shared__ float l_s[CG];
   const int tid = threadIdx.x;
   const int cg = tid / V4, c4 = tid % V4;
-  const int64_t rh = blockIdx.x;  // t * n_heads + head
   const float* ml = ws_ml + rh * n_chunks * 2;
   const f32x4* po = reinterpret_cast<const f32x4*>(ws_o + rh * n_chunks * HD) + c4;
   float mv[kPer], lv[kPer];
@@ -107,6 +106,63 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_combine(const floa
     }
     reinterpret_cast<f32x4*>(out + rh * HD)[tid] = r * (1.0f / l);
   }
+}
+
+// One workgroup per (row, head): rh = t * n_heads + head.
+template <int HD>
+__global__ __launch_bounds__(kDecodeThreads) void attn_decode_combine(const float* __restrict__ ws_o,
+                                                                      const float* __restrict__ ws_ml,
+                                                                      float* __restrict__ out, int n_chunks) {
+  combine_block<HD>(ws_o, ws_ml, out, n_chunks, blockIdx.x);
+}
+
+// ---- ragged batch: one query row per sequence, each over its own cache and context length ----
+// The launch's sequences travel by value in the kernel arguments (no device-side table to upload). Workgroup x of
+// the partial kernel belongs to the sequence whose chunk range [chunk0, chunk0 + n_chunks) holds x; the chunks are
+// shared out over the sequences in proportion to their lengths, so one launch streams every cache at once.
+constexpr int kMaxBatch = 32;
+struct SeqDesc {
+  const float* q;      // [n_heads, HD], the sequence's query row
+  const float* k;      // the sequence's caches [>= pos0 + 1 rows, n_kv, HD]
+  const float* v;
+  float* out;          // [n_heads, HD]
+  const float* k_new;  // appended row [n_kv, HD] (null: nothing appended)
+  const float* v_new;
+  float* ws_o;         // partials [n_heads, n_chunks, HD] and [n_heads, n_chunks, 2] (n_chunks > 1)
+  float* ws_ml;
+  int64_t pos0;        // position of the query row; it attends to rows 0..pos0
+  int64_t groups_per_chunk, extra_groups;
+  int chunk0, n_chunks;
+};
+struct Batch {
+  SeqDesc s[kMaxBatch];
+  int n_seq;
+};
+
+__device__ __forceinline__ int batch_seq_of(const Batch& b, int x) {
+  int s = 0;
+  for (int i = 1; i < b.n_seq; ++i)
+    if (x >= b.s[i].chunk0) s = i;
+  return s;
+}
+
+template <int HD, int GB>
+__global__ __launch_bounds__(kDecodeThreads) void attn_decode_batch_partial(Batch b, int n_heads, int n_kv, int group,
+                                                                            int n_sub, float qscale,
+                                                                            const float2* __restrict__ q_rope,
+                                                                            int q_rope_neox) {
+  const SeqDesc& d = b.s[batch_seq_of(b, blockIdx.x)];
+  partial_block<HD, GB>(d.q, d.k, d.v, d.out, d.ws_o, d.ws_ml, d.pos0, n_heads, n_kv, group, n_sub, d.n_chunks,
+                        d.groups_per_chunk, d.extra_groups, qscale, q_rope, q_rope_neox, d.k_new, d.v_new,
+                        const_cast<float*>(d.k), const_cast<float*>(d.v), int(blockIdx.x) - d.chunk0, blockIdx.y, 0);
+}
+
+// One workgroup per (sequence, head); sequences that took a single chunk were written by the partial kernel.
+template <int HD>
+__global__ __launch_bounds__(kDecodeThreads) void attn_decode_batch_combine(Batch b, int n_heads) {
+  const SeqDesc& d = b.s[blockIdx.x / n_heads];
+  if (d.n_chunks == 1) return;
+  combine_block<HD>(d.ws_o, d.ws_ml, d.out, d.n_chunks, blockIdx.x % n_heads);
 }
 
 // Any head_dim in [1, 256]: one wave per (row, head), one key per step, lanes over dimensions. Slow, exact
@@ -277,9 +333,138 @@ int decode(const float* q, const float* k, const float* v, float* out, int64_t n
                             app, s);
 }
 
+// Chunk layout of one batch launch (sequences pos0[0..n) with n <= kMaxBatch): the workgroup slots that fit on the
+// chip (as make_plan counts them) are shared out over the sequences in proportion to their row groups (at least one
+// chunk each), so every workgroup streams about the same number of groups. Fills the scheduling fields of b and
+// returns the workspace floats the launch needs.
+int64_t batch_layout(int64_t n, const int64_t* pos0, int64_t n_heads, int64_t n_kv, int64_t head_dim, int cu_count,
+                     Batch* b, int* gb, int* n_sub) {
+  const int64_t group = n_heads / n_kv;
+  *gb = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8;
+  *n_sub = int((group + *gb - 1) / *gb);
+  const int64_t step = (64 / (head_dim / 8)) * kUnroll * (kDecodeThreads / 64);
+  int64_t total = 0;
+  for (int64_t i = 0; i < n; ++i) total += (pos0[i] + 1 + step - 1) / step;
+  const int64_t cus = cu_count > 0 ? cu_count : 256;
+  const int64_t streams = n_kv * *n_sub;
+  const int resident = resident_per_cu(head_dim, *gb);
+  int64_t slots = cus * resident / streams;
+  if (resident > NBH_DECODE_WG_PER_CU && total < kLongGroups * slots) slots = cus * NBH_DECODE_WG_PER_CU / streams;
+  if (slots < 1) slots = 1;
+  int64_t ws = 0;
+  int chunk0 = 0;
+  b->n_seq = int(n);
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t units = (pos0[i] + 1 + step - 1) / step;
+    int64_t c = total <= slots ? units : slots * units / total;
+    c = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(c, units), kMaxChunks));
+    SeqDesc& d = b->s[i];
+    d.pos0 = pos0[i];
+    d.chunk0 = chunk0;
+    d.n_chunks = int(c);
+    d.groups_per_chunk = units / c;
+    d.extra_groups = units % c;
+    chunk0 += int(c);
+    if (c > 1) ws += n_heads * c * (head_dim + 2);
+  }
+  return ws;
+}
+
+template <int HD>
+int launch_batch(Batch& b, int gb, int n_sub, int64_t H, int64_t KV, float* ws, float qscale, const float2* q_rope,
+                 int q_rope_neox, hipStream_t s) {
+  int64_t off = 0;
+  bool merge = false;
+  int chunks = 0;
+  for (int i = 0; i < b.n_seq; ++i) {
+    SeqDesc& d = b.s[i];
+    chunks += d.n_chunks;
+    if (d.n_chunks > 1) {
+      d.ws_o = ws + off;
+      d.ws_ml = d.ws_o + H * d.n_chunks * HD;
+      off += H * d.n_chunks * (HD + 2);
+      merge = true;
+    } else {
+      d.ws_o = d.ws_ml = nullptr;
+    }
+  }
+  const int group = int(H / KV);
+  const dim3 grid(unsigned(chunks), unsigned(KV * n_sub));
+  hipError_t e;
+#define NBH_BATCH(GB)                                                                                             \
+  e = nbhs_timing::launch(NBHS_K_DECODE_PARTIAL, attn_decode_batch_partial<HD, GB>, grid, dim3(kDecodeThreads), s, \
+                          b, int(H), int(KV), group, n_sub, qscale, q_rope, q_rope_neox)
+  switch (gb) {
+    case 1: NBH_BATCH(1); break;
+    case 2: NBH_BATCH(2); break;
+    case 4: NBH_BATCH(4); break;
+    default: NBH_BATCH(8); break;
+  }
+#undef NBH_BATCH
+  if (e != hipSuccess || !merge) return e;
+  return nbhs_timing::launch(NBHS_K_DECODE_COMBINE, attn_decode_batch_combine<HD>, dim3(unsigned(b.n_seq * H)),
+                             dim3(kDecodeThreads), s, b, int(H));
+}
+
 }  // namespace
 
 extern "C" {
+
+int64_t nbhs_attn_decode_batch_workspace(int64_t n_seq, const int64_t* pos0, int64_t n_heads, int64_t n_kv_heads,
+                                         int64_t head_dim, int cu_count) {
+  if (n_seq <= 0 || !pos0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0) return -1;
+  if (!tiled_head_dim(head_dim)) return -1;
+  int64_t need = 0;
+  for (int64_t i0 = 0; i0 < n_seq; i0 += kMaxBatch) {
+    for (int64_t i = i0; i < std::min<int64_t>(n_seq, i0 + kMaxBatch); ++i)
+      if (pos0[i] < 0) return -1;
+    Batch b;
+    int gb, n_sub;
+    need = std::max(need, batch_layout(std::min<int64_t>(kMaxBatch, n_seq - i0), pos0 + i0, n_heads, n_kv_heads,
+                                       head_dim, cu_count, &b, &gb, &n_sub));
+  }
+  return need;
+}
+
+int nbhs_attn_decode_batch_f32(int64_t n_seq, const float* const* q, const float* const* k, const float* const* v,
+                               float* const* out, const float* const* k_new, const float* const* v_new,
+                               const int64_t* pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                               float* workspace, int64_t workspace_floats, int cu_count, const float* rope_cs,
+                               int64_t rope_rows, int neox, nbhs_stream stream) {
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (n_seq <= 0 || !q || !k || !v || !out || !pos0 || n_heads <= 0 || n_heads > 65535 || n_kv_heads <= 0 ||
+      n_heads % n_kv_heads != 0 || !tiled_head_dim(head_dim) || (!k_new) != (!v_new) || (k_new && !rope_cs))
+    return NBHS_EINVAL;
+  for (int64_t i = 0; i < n_seq; ++i) {
+    if (!q[i] || !k[i] || !v[i] || !out[i] || pos0[i] < 0 || (k_new && (!k_new[i] || !v_new[i])) ||
+        (rope_cs && pos0[i] + 1 > rope_rows))
+      return NBHS_EINVAL;
+  }
+  const float2* q_rope = reinterpret_cast<const float2*>(rope_cs);
+  const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
+  for (int64_t i0 = 0; i0 < n_seq; i0 += kMaxBatch) {  // launches of up to kMaxBatch sequences, in stream order
+    const int64_t n = std::min<int64_t>(kMaxBatch, n_seq - i0);
+    Batch b;
+    int gb, n_sub;
+    const int64_t need = batch_layout(n, pos0 + i0, n_heads, n_kv_heads, head_dim, cu_count, &b, &gb, &n_sub);
+    if (need > 0 && (!workspace || workspace_floats < need)) return NBHS_EINVAL;
+    if (n_kv_heads * n_sub > 65535) return NBHS_EINVAL;
+    for (int64_t i = 0; i < n; ++i) {
+      SeqDesc& d = b.s[i];
+      d.q = q[i0 + i];
+      d.k = k[i0 + i];
+      d.v = v[i0 + i];
+      d.out = out[i0 + i];
+      d.k_new = k_new ? k_new[i0 + i] : nullptr;
+      d.v_new = v_new ? v_new[i0 + i] : nullptr;
+    }
+    const int e = head_dim == 64
+                      ? launch_batch<64>(b, gb, n_sub, n_heads, n_kv_heads, workspace, qscale, q_rope, neox, s)
+                      : launch_batch<128>(b, gb, n_sub, n_heads, n_kv_heads, workspace, qscale, q_rope, neox, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
 
 int64_t nbhs_attn_decode_workspace(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
                                    int cu_count) {

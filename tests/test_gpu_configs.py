@@ -122,3 +122,44 @@ def test_config5_ragged_long_context_decode(backend, layer):
         k_all = np.concatenate([k0[:L], kr])
         v_all = np.concatenate([v0[:L], vn])
         assert_parity(got, cpu_attention(qr, k_all, v_all, L, KV), f"config5 layer {layer} seq {seq} (L={L})")
+
+
+@pytest.mark.parametrize("layer", [0, 15])
+def test_config5_ragged_batched_decode(backend, layer):
+    """Config 5 as one batch: the 16 sequences' caches resident together, each decode step of a layer one
+    append_rope_attention_batch call for all of them (two steps). Appended K rows are bit-exact and every sequence
+    is within tolerance of the reference on that sequence alone; the inputs are the per-sequence test's."""
+    s = configs.LLAMA32_1B
+    H, KV, D = s.n_heads, s.n_kv_heads, s.head_dim
+    ff = s.freq_factors()
+    lengths = configs.cfg5_lengths()
+    with Buffers(backend) as B:
+        host = []
+        dev = []
+        for seq, L in enumerate(lengths):
+            cap = L + 2
+            ck, k0 = device_normal(backend, B, (cap, KV, D), 5, layer, seq, configs.T_KCACHE)
+            cv, v0 = device_normal(backend, B, (cap, KV, D), 5, layer, seq, configs.T_VCACHE)
+            k0[configs.cfg5_scaled_rows(seq, L)] *= np.float32(configs.CFG5["scale"])
+            backend.write(ck, k0)
+            dq, q = device_normal(backend, B, (2, H, D), 5, layer, seq, configs.T_Q)
+            dk, kn = device_normal(backend, B, (2, KV, D), 5, layer, seq, configs.T_K)
+            dv, vn = device_normal(backend, B, (2, KV, D), 5, layer, seq, configs.T_V)
+            do = B.alloc(2 * H * D)
+            dev.append((ck, cv, dq, dk, dv, do))
+            host.append((k0[:L], v0[:L], q, kn, vn))
+        for st in range(2):
+            backend.append_rope_attention_batch(
+                [d[2].at(st * H * D) for d in dev], [d[0] for d in dev], [d[1] for d in dev],
+                [d[3].at(st * KV * D) for d in dev], [d[4].at(st * KV * D) for d in dev],
+                [d[5].at(st * H * D) for d in dev], [L + st for L in lengths], H, KV, D, s.rope_base, s.neox, ff)
+        got = [backend.download(d[5], (2, H, D)) for d in dev]
+        gk = [backend.download(d[0].at(L * KV * D), (2, KV, D)) for d, L in zip(dev, lengths)]
+    for seq, L in enumerate(lengths):
+        k0, v0, q, kn, vn = host[seq]
+        kr = oracle.rope(kn.copy(), L, s.rope_base, s.neox, ff)
+        qr = oracle.rope(q.copy(), L, s.rope_base, s.neox, ff)
+        assert np.array_equal(bits(gk[seq]), bits(kr)), f"seq {seq}: appended K rows"
+        k_all = np.concatenate([k0, kr])
+        v_all = np.concatenate([v0, vn])
+        assert_parity(got[seq], cpu_attention(qr, k_all, v_all, L, KV), f"config5 batch layer {layer} seq {seq} (L={L})")

@@ -9,6 +9,7 @@ import os
 import numpy as np
 import pytest
 
+import nibble_amd
 import oracle
 from nibble_amd import configs, synth
 from tests.gpu_util import Buffers, assert_parity, bits
@@ -472,3 +473,146 @@ def test_append_rope_attention_decode_never_reads_the_unwritten_row(backend, pos
     assert np.array_equal(bits(gk1[pos0]), bits(gk2[pos0]))
     assert np.array_equal(bits(gv2[pos0]), bits(vn[0]))
     assert np.all(np.isnan(gk2[pos0 + 1:])) and np.all(np.isnan(gv2[pos0 + 1:]))
+
+
+BATCH_POS = [0, 5, 31, 32, 100, 1000, 4096, 20000]
+
+
+@pytest.mark.parametrize("H,KV,D,neox", [(32, 8, 64, False), (14, 2, 64, True), (32, 4, 64, False),
+                                         (16, 8, 128, True), (8, 2, 24, False)])
+def test_attention_batch_matches_oracle_and_single_calls(backend, H, KV, D, neox):
+    """Ragged batch: each sequence's output is its own single-row attention (oracle and the single-sequence call,
+    within tolerance: the context split differs), for positions on both sides of row-group and chunk boundaries;
+    head_dim 24 takes the per-sequence fallback."""
+    rng = np.random.default_rng(H * 7 + D)
+    pos = BATCH_POS
+    qs = [rng.standard_normal((1, H, D)).astype(np.float32) for _ in pos]
+    ks = [rng.standard_normal((p + 1, KV, D)).astype(np.float32) for p in pos]
+    vs = [rng.standard_normal((p + 1, KV, D)).astype(np.float32) for p in pos]
+    with Buffers(backend) as B:
+        dq = [B.upload(x) for x in qs]
+        dk = [B.upload(x) for x in ks]
+        dv = [B.upload(x) for x in vs]
+        ob = [B.alloc(H * D) for _ in pos]
+        o1 = [B.alloc(H * D) for _ in pos]
+        backend.attention_batch(dq, dk, dv, ob, pos, H, KV, D)
+        for i, p in enumerate(pos):
+            backend.attention(dq[i], dk[i], dv[i], o1[i], 1, p, H, KV, D)
+        gb = [backend.download(x, (1, H, D)) for x in ob]
+        g1 = [backend.download(x, (1, H, D)) for x in o1]
+    for i, p in enumerate(pos):
+        ref = cpu_attention(qs[i], ks[i], vs[i], p, KV)
+        assert_parity(gb[i], ref, f"batch seq {i} pos0={p}")
+        assert_parity(gb[i], g1[i], f"batch vs single seq {i} pos0={p}")
+
+
+def test_attention_batch_over_several_launches(backend):
+    """More sequences than one launch takes (32): 40 sequences of mixed lengths, each checked against the oracle."""
+    H, KV, D = 32, 8, 64
+    rng = np.random.default_rng(40)
+    pos = [int(x) for x in rng.integers(0, 3000, 40)]
+    qs = [rng.standard_normal((1, H, D)).astype(np.float32) for _ in pos]
+    ks = [rng.standard_normal((p + 1, KV, D)).astype(np.float32) for p in pos]
+    vs = [rng.standard_normal((p + 1, KV, D)).astype(np.float32) for p in pos]
+    with Buffers(backend) as B:
+        dq, dk, dv = [B.upload(x) for x in qs], [B.upload(x) for x in ks], [B.upload(x) for x in vs]
+        ob = [B.alloc(H * D) for _ in pos]
+        backend.attention_batch(dq, dk, dv, ob, pos, H, KV, D)
+        gb = [backend.download(x, (1, H, D)) for x in ob]
+    for i, p in enumerate(pos):
+        assert_parity(gb[i], cpu_attention(qs[i], ks[i], vs[i], p, KV), f"seq {i} pos0={p}")
+
+
+@pytest.mark.parametrize("H,KV,D,neox,llama3", [(32, 8, 64, False, True), (14, 2, 64, True, False),
+                                                 (16, 4, 128, False, False)])
+def test_append_rope_attention_batch(backend, H, KV, D, neox, llama3):
+    """Fused batch: every cache gets rope(k_new[i]) and v_new[i] at row pos0[i] bit-exactly (as the per-sequence
+    fused call writes them), q is left unrotated, and each output is within tolerance of the oracle on the
+    sequence alone."""
+    base = 5e5 if llama3 else 1e4
+    ff = synth.llama3_freq_factors(D, base) if llama3 else None
+    rng = np.random.default_rng(D + H)
+    pos = BATCH_POS
+    qs = [rng.standard_normal((1, H, D)).astype(np.float32) for _ in pos]
+    kn = [rng.standard_normal((1, KV, D)).astype(np.float32) for _ in pos]
+    vn = [rng.standard_normal((1, KV, D)).astype(np.float32) for _ in pos]
+    ks = [rng.standard_normal((p + 2, KV, D)).astype(np.float32) for p in pos]
+    vs = [rng.standard_normal((p + 2, KV, D)).astype(np.float32) for p in pos]
+    with Buffers(backend) as B:
+        dq = [B.upload(x) for x in qs]
+        dkn, dvn = [B.upload(x) for x in kn], [B.upload(x) for x in vn]
+        dk, dv = [B.upload(x) for x in ks], [B.upload(x) for x in vs]
+        dk1, dv1 = [B.upload(x) for x in ks], [B.upload(x) for x in vs]
+        ob, o1 = [B.alloc(H * D) for _ in pos], [B.alloc(H * D) for _ in pos]
+        backend.append_rope_attention_batch(dq, dk, dv, dkn, dvn, ob, pos, H, KV, D, base, neox, ff)
+        for i, p in enumerate(pos):
+            backend.append_rope_attention(dq[i], dk1[i], dv1[i], dkn[i], dvn[i], o1[i], 1, p, H, KV, D, base, neox,
+                                          ff)
+        gb = [backend.download(x, (1, H, D)) for x in ob]
+        gk = [backend.download(x, ks[i].shape) for i, x in enumerate(dk)]
+        gv = [backend.download(x, vs[i].shape) for i, x in enumerate(dv)]
+        gk1 = [backend.download(x, ks[i].shape) for i, x in enumerate(dk1)]
+        gq = [backend.download(x, (1, H, D)) for x in dq]
+    for i, p in enumerate(pos):
+        assert np.array_equal(bits(gk[i]), bits(gk1[i])), f"seq {i}: K cache differs from the per-sequence call"
+        assert np.array_equal(bits(gv[i][p]), bits(vn[i][0])), f"seq {i}: appended V row"
+        assert np.array_equal(bits(gv[i][p + 1:]), bits(vs[i][p + 1:])), f"seq {i}: rows after pos0 changed"
+        assert np.array_equal(bits(gq[i]), bits(qs[i])), f"seq {i}: q modified"
+        qr = oracle.rope(qs[i].copy(), p, base, neox, ff)
+        kr = oracle.rope(kn[i].copy(), p, base, neox, ff)
+        assert np.array_equal(bits(gk[i][p]), bits(kr[0])), f"seq {i}: appended K row"
+        ref = cpu_attention(qr, np.concatenate([ks[i][:p], kr]), np.concatenate([vs[i][:p], vn[i]]), p, KV)
+        assert_parity(gb[i], ref, f"fused batch seq {i} pos0={p}")
+
+
+def test_attention_batch_causal_mask_poison(backend):
+    """Rows past each sequence's window hold NaN (and, for the fused batch, row pos0 itself before the append):
+    outputs stay finite and bitwise equal to the unpoisoned run."""
+    H, KV, D = 32, 8, 64
+    rng = np.random.default_rng(77)
+    pos = [3, 64, 777, 9000]
+    qs = [rng.standard_normal((1, H, D)).astype(np.float32) for _ in pos]
+    kn = [rng.standard_normal((1, KV, D)).astype(np.float32) for _ in pos]
+    vn = [rng.standard_normal((1, KV, D)).astype(np.float32) for _ in pos]
+    ks = [rng.standard_normal((p + 9, KV, D)).astype(np.float32) for p in pos]
+    vs = [rng.standard_normal((p + 9, KV, D)).astype(np.float32) for p in pos]
+
+    def poisoned(x, p, first):
+        y = x.copy()
+        y[first:] = np.nan
+        return y
+
+    with Buffers(backend) as B:
+        dq, dkn, dvn = [B.upload(x) for x in qs], [B.upload(x) for x in kn], [B.upload(x) for x in vn]
+        outs = {}
+        for tag, first in (("clean", None), ("plain", 1), ("fused", 0)):
+            dk = [B.upload(ks[i] if first is None else poisoned(ks[i], p, p + first)) for i, p in enumerate(pos)]
+            dv = [B.upload(vs[i] if first is None else poisoned(vs[i], p, p + first)) for i, p in enumerate(pos)]
+            ob = [B.alloc(H * D) for _ in pos]
+            if tag == "fused":
+                dk0 = [B.upload(ks[i]) for i in range(len(pos))]
+                dv0 = [B.upload(vs[i]) for i in range(len(pos))]
+                oc = [B.alloc(H * D) for _ in pos]
+                backend.append_rope_attention_batch(dq, dk0, dv0, dkn, dvn, oc, pos, H, KV, D, 1e4, False, None)
+                outs["fused_clean"] = [backend.download(x, (1, H, D)) for x in oc]
+                backend.append_rope_attention_batch(dq, dk, dv, dkn, dvn, ob, pos, H, KV, D, 1e4, False, None)
+            else:
+                backend.attention_batch(dq, dk, dv, ob, pos, H, KV, D)
+            outs[tag] = [backend.download(x, (1, H, D)) for x in ob]
+    for i in range(len(pos)):
+        for tag, ref in (("plain", "clean"), ("fused", "fused_clean")):
+            assert np.all(np.isfinite(outs[tag][i])), f"{tag} seq {i}"
+            assert np.array_equal(bits(outs[tag][i]), bits(outs[ref][i])), f"{tag} seq {i}"
+
+
+def test_attention_batch_rejects_bad_arguments(backend):
+    H, KV, D = 32, 8, 64
+    with Buffers(backend) as B:
+        q, k, v, o = B.alloc(H * D), B.alloc(10 * KV * D), B.alloc(10 * KV * D), B.alloc(H * D)
+        with pytest.raises(nibble_amd.BackendError):
+            backend.attention_batch([q, q], [k], [v], [o], [3], H, KV, D)  # list lengths differ
+        with pytest.raises(nibble_amd.BackendError):
+            backend.attention_batch([q], [k], [v], [o], [10], H, KV, D)  # cache holds rows 0..9 only
+        with pytest.raises(nibble_amd.BackendError):
+            backend.attention_batch([q], [k], [v], [o], [-1], H, KV, D)
+        backend.attention_batch([], [], [], [], [], H, KV, D)  # nothing to do
