@@ -108,6 +108,88 @@ def cpu_baseline(be, shape, ck0, cv0, dq_dec, ctx, q_pre, budget_s):
     }
 
 
+def ragged_decode(be, steps, warmup):
+    """BASELINE config 5 throughput: 16 Llama-3.2-1B-shape sequences with the ragged cache lengths of the parity
+    test (log-uniform 1024..131072, seeded), 16 layers, N(0,1) caches with 1 % of K rows scaled x8 (in blocks of 16
+    rows, one in a hundred), one token per sequence per step. Each layer of a step is one
+    append_rope_attention_batch call for all 16 sequences; the same steps are then timed again as 16 single-sequence
+    calls per layer. Returns the config-5 sub-object of the JSON line."""
+    shape = configs.LLAMA32_1B
+    H, KV, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
+    base, neox, ff = shape.rope_base, shape.neox, shape.freq_factors()
+    NL, row = 16, KV * D
+    lengths = configs.cfg5_lengths()
+    n_seq = len(lengths)
+    span = warmup + steps
+    caches = []
+    for l in range(NL):
+        per = []
+        for i, L in enumerate(lengths):
+            k, v = be.alloc((L + span) * row), be.alloc((L + span) * row)
+            be.fill_normal(k, L * row, seed=9000 + 64 * l + 2 * i)
+            be.fill_normal(v, L * row, seed=9001 + 64 * l + 2 * i)
+            for r0 in range(7 * 16, L, 1600):  # 1 % of K rows, x8
+                nr = min(16, L - r0)
+                be.fill_normal(k.at(r0 * row), nr * row, seed=7 + 131 * l + r0, scale=8.0)
+            per.append((k, v))
+        caches.append(per)
+    qs = be.alloc(span * NL * n_seq * H * D)
+    kn, vn = be.alloc(span * NL * n_seq * row), be.alloc(span * NL * n_seq * row)
+    out = be.alloc(n_seq * H * D)
+    be.fill_normal(qs, span * NL * n_seq * H * D, seed=31)
+    be.fill_normal(kn, span * NL * n_seq * row, seed=32)
+    be.fill_normal(vn, span * NL * n_seq * row, seed=33)
+    be.reserve_rope(D, base, neox, ff)
+
+    def args_of(s, l):
+        j = (s * NL + l) * n_seq
+        return ([qs.at((j + i) * H * D) for i in range(n_seq)], [c[0] for c in caches[l]], [c[1] for c in caches[l]],
+                [kn.at((j + i) * row) for i in range(n_seq)], [vn.at((j + i) * row) for i in range(n_seq)],
+                [out.at(i * H * D) for i in range(n_seq)], [L + s for L in lengths])
+
+    def step_batched(s):
+        for l in range(NL):
+            q, k, v, a, b, o, p = args_of(s, l)
+            be.append_rope_attention_batch(q, k, v, a, b, o, p, H, KV, D, base, neox, ff)
+
+    def step_single(s):
+        for l in range(NL):
+            q, k, v, a, b, o, p = args_of(s, l)
+            for i in range(n_seq):
+                be.append_rope_attention(q[i], k[i], v[i], a[i], b[i], o[i], 1, p[i], H, KV, D, base, neox, ff)
+
+    def timed(step):
+        for s in range(warmup):
+            step(s)
+        be.sync()
+        e0, e1 = be.event(), be.event()
+        e0.record()
+        for s in range(warmup, span):
+            step(s)
+        e1.record()
+        return e0.elapsed_ms(e1)
+
+    byts = sum(NL * decode_bytes(KV, D, L + s + 1) for s in range(warmup, span) for L in lengths)
+    ms_b = timed(step_batched)
+    ms_1 = timed(step_single)
+    for per in caches:
+        for k, v in per:
+            be.free(k)
+            be.free(v)
+    for x in (qs, kn, vn, out):
+        be.free(x)
+    gbs_b, gbs_1 = byts / (ms_b * 1e-3) / 1e9, byts / (ms_1 * 1e-3) / 1e9
+    log(f"config 5 (16 ragged sequences, {sum(lengths)} cache rows per layer): batched {ms_b / steps:.3f} ms/step -> "
+        f"{gbs_b:.1f} GB/s ({gbs_b / HBM_PEAK_GBS:.1%}); 16 single calls per layer {ms_1 / steps:.3f} ms/step -> "
+        f"{gbs_1:.1f} GB/s")
+    return {"metric": "ragged batched decode attn HBM GB/s (BASELINE config 5)", "value": round(gbs_b, 1),
+            "unit": "GB/s", "frac": round(gbs_b / HBM_PEAK_GBS, 4), "steps": steps, "warmup": warmup,
+            "ms_per_step": round(ms_b / steps, 4), "sequences": n_seq, "layers": NL,
+            "cache_rows_per_layer": sum(lengths), "lengths": lengths,
+            "single_calls": {"value": round(gbs_1, 1), "ms_per_step": round(ms_1 / steps, 4),
+                             "note": "the same steps as 16 single-sequence calls per layer"}}
+
+
 COPY_CAL_BYTES = 1 << 30  # calibration copy for the HBM byte counters: 1 GiB read + 1 GiB written
 PROBE_DECODE_STEPS = 8
 
@@ -221,6 +303,8 @@ def main():
                     help="untimed prefill passes first: the compute clock takes some 20-40 ms of sustained MFMA load "
                          "to settle")
     ap.add_argument("--cpu-seconds", type=float, default=16.0, help="budget of the CPU baseline samples")
+    ap.add_argument("--cfg5-steps", type=int, default=4,
+                    help="timed steps of the config-5 ragged batch (0: skip; 2 untimed steps precede them)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc passes (child processes, about 10 s each) that measure HBM "
@@ -402,6 +486,8 @@ def main():
                        "append_rope_prefill": round(app2_ms / app2_n * 1e3, 2) if app2_n else None,
                        "append_stage_kv_f16": round(stage_ms / max(stage_n, 1) * 1e3, 2)},
     }
+    if args.cfg5_steps > 0:
+        result["config5"] = ragged_decode(be, args.cfg5_steps, 2)
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(be, shape, ck[0], cv[0], qd, ctx, q_pre0_host, args.cpu_seconds)

@@ -184,7 +184,13 @@ const float* HipBackend::rope_table(int64_t head_dim, int64_t rows_needed, const
     *rows_out = it->rows;
     return it->dev;
   }
-  const int64_t rows = std::max(rows_needed, reserved_.n_ctx);
+  // Past the reserved n_ctx a table at least doubles (in whole 1024-row blocks), so positions that creep up one
+  // per decode step rebuild it a logarithmic number of times, not once per step.
+  int64_t rows = std::max(rows_needed, reserved_.n_ctx);
+  if (rows > reserved_.n_ctx) {
+    if (it != rope_tables_.end()) rows = std::max(rows, 2 * it->rows);
+    rows = (rows + 1023) / 1024 * 1024;
+  }
   int64_t entries;
   if (overflow_mul(rows, head_dim, &entries)) throw Error("rope: table size overflows");
   std::vector<float> host(static_cast<size_t>(entries));

@@ -334,9 +334,10 @@ int decode(const float* q, const float* k, const float* v, float* out, int64_t n
 }
 
 // Chunk layout of one batch launch (sequences pos0[0..n) with n <= kMaxBatch): the workgroup slots that fit on the
-// chip (as make_plan counts them) are shared out over the sequences in proportion to their row groups (at least one
-// chunk each), so every workgroup streams about the same number of groups. Fills the scheduling fields of b and
-// returns the workspace floats the launch needs.
+// chip (as make_plan counts them) are shared out over the sequences so that the largest number of row groups any
+// one chunk streams - what the launch's duration follows - is as small as the slots allow: the least T for which
+// chunks of at most T groups (sum over sequences of ceil(groups / T)) fit the slots, by bisection. Fills the
+// scheduling fields of b and returns the workspace floats the launch needs.
 int64_t batch_layout(int64_t n, const int64_t* pos0, int64_t n_heads, int64_t n_kv, int64_t head_dim, int cu_count,
                      Batch* b, int* gb, int* n_sub) {
   const int64_t group = n_heads / n_kv;
@@ -350,14 +351,30 @@ int64_t batch_layout(int64_t n, const int64_t* pos0, int64_t n_heads, int64_t n_
   const int resident = resident_per_cu(head_dim, *gb);
   int64_t slots = cus * resident / streams;
   if (resident > NBH_DECODE_WG_PER_CU && total < kLongGroups * slots) slots = cus * NBH_DECODE_WG_PER_CU / streams;
-  if (slots < 1) slots = 1;
+  if (slots < n) slots = n;  // every sequence takes at least one chunk
+  auto chunks_of = [&](int64_t units, int64_t t) {
+    return std::min<int64_t>((units + t - 1) / t, kMaxChunks);
+  };
+  auto fits = [&](int64_t t) {
+    int64_t c = 0;
+    for (int64_t i = 0; i < n; ++i) c += chunks_of((pos0[i] + 1 + step - 1) / step, t);
+    return c <= slots;
+  };
+  int64_t lo = std::max<int64_t>(1, (total + slots - 1) / slots), hi = 1;
+  for (int64_t i = 0; i < n; ++i) hi = std::max(hi, (pos0[i] + 1 + step - 1) / step);
+  while (lo < hi) {  // least T that fits (T = the longest sequence's groups always does)
+    const int64_t mid = lo + (hi - lo) / 2;
+    if (fits(mid))
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
   int64_t ws = 0;
   int chunk0 = 0;
   b->n_seq = int(n);
   for (int64_t i = 0; i < n; ++i) {
     const int64_t units = (pos0[i] + 1 + step - 1) / step;
-    int64_t c = total <= slots ? units : slots * units / total;
-    c = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(c, units), kMaxChunks));
+    const int64_t c = chunks_of(units, lo);
     SeqDesc& d = b->s[i];
     d.pos0 = pos0[i];
     d.chunk0 = chunk0;

@@ -616,3 +616,32 @@ def test_attention_batch_rejects_bad_arguments(backend):
         with pytest.raises(nibble_amd.BackendError):
             backend.attention_batch([q], [k], [v], [o], [-1], H, KV, D)
         backend.attention_batch([], [], [], [], [], H, KV, D)  # nothing to do
+
+
+def test_rope_table_grows_geometrically_past_the_reservation():
+    """Decoding one position at a time past the reserved n_ctx rebuilds the RoPE table only when it doubles (in whole
+    1024-row blocks), not at every step; the appended rows stay bit-exact across a rebuild."""
+    H, KV, D = 32, 8, 64
+    be = nibble_amd.HipBackend(0)
+    try:
+        be.reserve(64, H, 1, 8192)
+        rng = np.random.default_rng(5)
+        cap = 2100
+        with Buffers(be) as B:
+            ck, cv = B.alloc(cap * KV * D), B.alloc(cap * KV * D)
+            q = B.upload(rng.standard_normal((1, H, D)).astype(np.float32))
+            kn_h = rng.standard_normal((1, KV, D)).astype(np.float32)
+            kn, vn, out = B.upload(kn_h), B.alloc(KV * D), B.alloc(H * D)
+            sizes = {}
+            for pos in (1000, 1001, 1023, 1024, 1025, 2047):
+                be.append_rope_attention(q, ck, cv, kn, vn, out, 1, pos, H, KV, D, 1e4, False, None)
+                be.sync()
+                sizes[pos] = be.internal_bytes()
+            gk = be.download(ck, (cap, KV, D))
+        assert sizes[1000] == sizes[1001] == sizes[1023], sizes  # one table of 1024 rows
+        assert sizes[1024] > sizes[1023], sizes                   # grown once, to 2048 rows
+        assert sizes[1024] == sizes[1025] == sizes[2047], sizes
+        for pos in (1000, 1023, 1024, 2047):
+            assert np.array_equal(bits(gk[pos]), bits(oracle.rope(kn_h.copy(), pos, 1e4, False)[0])), pos
+    finally:
+        be.close()
