@@ -131,7 +131,15 @@ int nbhs_append_stage_kv_f16(float* cache_k, float* cache_v, const float* k_new,
 int nbhs_attn_prefill_mfma(const float* q, const void* k16, const void* vt16, float* out, int64_t n, int64_t pos0,
                            int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t staged_rows_pad,
                            const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, const float* k_cache,
-                           const float* v_cache, int64_t fp32_rows, nbhs_stream s);
+                           const float* v_cache, int64_t fp32_rows, float* workspace, int64_t workspace_floats,
+                           int cu_count, nbhs_stream s);
+/* Workspace (floats) nbhs_attn_prefill_mfma needs for these arguments: when the MFMA rows' tiles cannot fill the
+ * chip (short prefill chunks), each tile's key range is split over several workgroups whose partials a second,
+ * log-sum-exp launch merges; 0 when no split is taken. */
+int64_t nbhs_attn_prefill_workspace(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                    int64_t fp32_rows, int cu_count);
+/* Upper bound of nbhs_attn_prefill_workspace over every call shape, for sizing the workspace once. */
+int64_t nbhs_attn_prefill_workspace_bound(int cu_count);
 
 /* Synthetic N(0,1)*scale data for benchmarks: counter-based (SplitMix64 of seed and index), Box-Muller in fp32. */
 int nbhs_fill_normal_f32(float* dst, int64_t count, uint64_t seed, float scale, nbhs_stream s);

@@ -84,10 +84,12 @@ void HipBackend::reserve(const ReserveParams& rp) {
   if (rp.n_ctx < 0 || rp.n_heads < 0 || rp.max_rows < 0 || rp.max_width < 0)
     throw Error("reserve: negative size (n_ctx=" + str(rp.n_ctx) + " n_heads=" + str(rp.n_heads) + ")");
   reserved_ = rp;
-  // Decode partials, sized for the worst split the decode kernel plans for this many query heads.
+  // Split-context partials (decode chunks, and the key splits of short prefill chunks share the buffer), sized for
+  // the worst split either kernel plans for this many query heads.
   const int64_t floats = nbhs_attn_decode_workspace_bound(std::max<int64_t>(rp.n_heads, 1), cu_count_);
   if (floats < 0) throw Error("reserve: invalid n_heads " + str(rp.n_heads));
-  ensure(decode_ws_, decode_ws_bytes_, size_t(floats) * sizeof(float));
+  const int64_t need = std::max(floats, nbhs_attn_prefill_workspace_bound(cu_count_));
+  ensure(decode_ws_, decode_ws_bytes_, size_t(need) * sizeof(float));
 }
 
 void HipBackend::reserve_attention(int64_t n_kv_heads, int64_t head_dim) {
@@ -443,10 +445,14 @@ void HipBackend::run_attention(const float* q, const float* k, const float* v, f
     decode_rows(q, out, split, pos0);
     return;
   }
-  // rows [0, split) in fp32 and the rest on MFMA, in one launch
+  // rows [0, split) in fp32 and the rest on MFMA, in one launch (plus a merge when short chunks split their keys)
   const int64_t rows_pad = halves / (n_kv_heads * head_dim);
+  const int64_t ws = nbhs_attn_prefill_workspace(n, pos0, n_heads, n_kv_heads, head_dim, split, cu_count_);
+  if (ws < 0) throw Error("attention: invalid prefill shape");
+  ensure(decode_ws_, decode_ws_bytes_, size_t(ws) * sizeof(float));
   check(nbhs_attn_prefill_mfma(q, k16_, vt16_, out, n, pos0, n_heads, n_kv_heads, head_dim, rows_pad, rope_table,
-                               rope_rows, neox ? 1 : 0, k, v, split, stream_),
+                               rope_rows, neox ? 1 : 0, k, v, split, decode_ws_,
+                               int64_t(decode_ws_bytes_ / sizeof(float)), cu_count_, stream_),
         "attention (prefill kernel)");
 }
 

@@ -27,87 +27,6 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
                         blockIdx.z);
 }
 
-// Block-wide reduction of one float per thread (kDecodeThreads threads); every thread gets the result.
-template <bool MAX>
-__device__ __forceinline__ float block_reduce(float x, float* scratch) {
-#pragma unroll
-  for (int mask = 1; mask < 64; mask <<= 1) {
-    const float y = __shfl_xor(x, mask, 64);
-    x = MAX ? fmaxf(x, y) : x + y;
-  }
-  __syncthreads();  // scratch may still be read from a previous reduction
-  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = x;
-  __syncthreads();
-  float r = scratch[0];
-#pragma unroll
-  for (int w = 1; w < kDecodeThreads / 64; ++w) r = MAX ? fmaxf(r, scratch[w]) : r + scratch[w];
-  return r;
-}
-
-// Log-sum-exp merge of the chunk partials of one (row, head) per workgroup. Thread (chunk group cg, float4 column
-// c4) loads the max, sum and partial-output column of its chunks cg, cg + CG, ... all at once (one memory round
-// trip for up to kPer chunks each), the global max comes from a block reduction, and the weighted sums of the
-// chunk groups are added through LDS.
-template <int HD>
-__device__ __forceinline__ void combine_block(const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
-                                              float* __restrict__ out, int n_chunks, int64_t rh) {
-  constexpr int V4 = HD / 4;                // float4 columns of one head row
-  constexpr int CG = kDecodeThreads / V4;   // chunk groups
-  constexpr int kPer = 16;                  // chunks per thread held in registers
-  __shared__ float red[kDecodeThreads / 64];
-  __shared__ f32x4 acc_s[CG][V4];
-  __shared__ float l_s[CG];
-  const int tid = threadIdx.x;
-  const int cg = tid / V4, c4 = tid % V4;
-  const float* ml = ws_ml + rh * n_chunks * 2;
-  const f32x4* po = reinterpret_cast<const f32x4*>(ws_o + rh * n_chunks * HD) + c4;
-  float mv[kPer], lv[kPer];
-  f32x4 ov[kPer];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int c = cg + i * CG;
-    mv[i] = -INFINITY;
-    lv[i] = 0.f;
-    ov[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (c < n_chunks) {
-      mv[i] = ml[2 * c];
-      lv[i] = ml[2 * c + 1];
-      ov[i] = po[int64_t(c) * V4];
-    }
-    mx = fmaxf(mx, mv[i]);
-  }
-  for (int c = cg + kPer * CG; c < n_chunks; c += CG) mx = fmaxf(mx, ml[2 * c]);  // beyond the register window
-  mx = block_reduce<true>(mx, red);
-  const float ms = mx == -INFINITY ? 0.0f : mx;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.f;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const float wc = exp2_raw(mv[i] - ms);
-    acc += ov[i] * wc;
-    lsum += lv[i] * wc;
-  }
-  for (int c = cg + kPer * CG; c < n_chunks; c += CG) {
-    const float wc = exp2_raw(ml[2 * c] - ms);
-    acc += po[int64_t(c) * V4] * wc;
-    lsum += ml[2 * c + 1] * wc;
-  }
-  acc_s[cg][c4] = acc;
-  if (c4 == 0) l_s[cg] = lsum;
-  __syncthreads();
-  if (tid < V4) {
-    f32x4 r = acc_s[0][tid];
-    float l = l_s[0];
-#pragma unroll
-    for (int i = 1; i < CG; ++i) {
-      r += acc_s[i][tid];
-      l += l_s[i];
-    }
-    reinterpret_cast<f32x4*>(out + rh * HD)[tid] = r * (1.0f / l);
-  }
-}
-
 // One workgroup per (row, head): rh = t * n_heads + head.
 template <int HD>
 __global__ __launch_bounds__(kDecodeThreads) void attn_decode_combine(const float* __restrict__ ws_o,

@@ -30,6 +30,7 @@
 //    chunk per row) from the fp32 cache, in the tail the shortest MFMA tiles leave.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "backend/hip/kernel_timing.h"
@@ -185,12 +186,13 @@ void attn_prefill_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16,
     float* __restrict__ out, int64_t n, int64_t pos0, int n_heads, int n_kv, int group, int64_t rows_pad,
     int n_tiles, float qscale, const float2* __restrict__ q_rope, int q_rope_neox, const float* __restrict__ kc,
-    const float* __restrict__ vc, int64_t fp32_rows, int fp32_n_sub) {
+    const float* __restrict__ vc, int64_t fp32_rows, int fp32_n_sub, int n_split, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml) {
   // Workgroups past the MFMA tiles: query row t < fp32_rows of the call (q and out start fp32_rows rows before
   // this launch's MFMA rows) for KV head x head subgroup `by`, in fp32 over its whole causal window.
   static_assert(kWaves * 64 == nbh_decode::kDecodeThreads, "the fp32 rows' body runs on the MFMA workgroup size");
-  if (int64_t(blockIdx.x) >= int64_t(n_tiles) * n_kv) {
-    const int64_t e = int64_t(blockIdx.x) - int64_t(n_tiles) * n_kv;
+  if (int64_t(blockIdx.x) >= int64_t(n_tiles) * n_kv * n_split) {
+    const int64_t e = int64_t(blockIdx.x) - int64_t(n_tiles) * n_kv * n_split;
     const int streams = n_kv * fp32_n_sub;
     const int64_t p0 = pos0 - fp32_rows;
     constexpr int64_t kStepRows = (nbh_decode::kDecodeThreads / 64) * (64 / (HD / 8)) * nbh_decode::kUnroll;
@@ -221,9 +223,11 @@ void attn_prefill_kernel(
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ql = lane & 31, hf = lane >> 5;
+  // Workgroup b: KV head b % KV, key split (b / KV) % n_split of row tile n_tiles - 1 - b / (KV n_split).
   const int b = blockIdx.x;
   const int g = b % n_kv;
-  const int tile = n_tiles - 1 - b / n_kv;
+  const int split = (b / n_kv) % n_split;
+  const int tile = n_tiles - 1 - b / (n_kv * n_split);
   const int64_t P = n * group;
   const int64_t pb0 = int64_t(tile) * kRowsPerBlock;
   const int64_t wp0 = pb0 + wave * kRowsPerWave;
@@ -243,6 +247,9 @@ void attn_prefill_kernel(
   const int64_t p_last = min(pb0 + kRowsPerBlock, P) - 1;
   const int64_t kend = pos0 + p_last / group + 1;  // the block's keys: [0, kend)
   const int ntk = int((kend + kBN - 1) / kBN);
+  // This workgroup's key tiles: split `split` of the block's ntk tiles in n_split contiguous ranges.
+  const int per_split = (ntk + n_split - 1) / n_split;
+  const int kt0 = min(ntk, split * per_split), kt1 = min(ntk, kt0 + per_split);
   const bool wave_active = wp0 < P;
   const int64_t wave_kend = wave_active ? pos0 + (min(wp0 + kRowsPerWave, P) - 1) / group + 1 : 0;
   const int64_t wave_kfull = wave_active ? pos0 + wp0 / group + 1 : 0;  // keys every row of the wave sees
@@ -339,19 +346,19 @@ void attn_prefill_kernel(
   // are ordered by the wait on vmcnt (global_load_lds completes when its data is in LDS), and a fence here would
   // also wait for the fetches that are meant to stay in flight.
 #pragma unroll
-  for (int kt = 0; kt < kStages - 1; ++kt)
-    if (kt < ntk) fetch(kt);
-  for (int kt = 0; kt < ntk; ++kt) {
+  for (int i = 0; i < kStages - 1; ++i)
+    if (kt0 + i < kt1) fetch(kt0 + i);
+  for (int kt = kt0; kt < kt1; ++kt) {
     const int cur = kt % kStages;
     constexpr int ahead = (kStages - 2) * (K_LD + V_LD);  // this wave's loads of the tiles after kt
-    if (kStages > 2 && kt + 1 < ntk)
+    if (kStages > 2 && kt + 1 < kt1)
       __builtin_amdgcn_s_waitcnt(vmcnt_wait(ahead));
     else
       __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (kt + kStages - 1 < ntk) fetch(kt + kStages - 1);
+    if (kt + kStages - 1 < kt1) fetch(kt + kStages - 1);
     if (wave_active && int64_t(kt) * kBN < wave_kend) {
       // S^T for the tile's two 32-key halves and every query block; each K fragment read from LDS serves all
       // blocks, and the chains are interleaved so consecutive MFMAs do not wait on each other's results. The
@@ -415,7 +422,7 @@ void attn_prefill_kernel(
       // The shift is not raised per tile: the weights are computed against the current one, and only when some
       // lane's sum leaves (0, kPSumMax] - a score grew past the shift by ~12 (log2), or inf/NaN from an fp16
       // overflow - does the wave take the slow path below (always on its first tile, where no shift exists yet).
-      bool slow = kt == 0;
+      bool slow = kt == kt0;
       if (!slow) {
         bool bad = false;
 #pragma unroll
@@ -436,9 +443,9 @@ void attn_prefill_kernel(
             for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[qb][kk][r]);
           mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) - base;  // tile max relative to the current shift
           // first tile: shift to the tile max (0 if every key is masked); later: raise by the excess only
-          const float d = kt == 0 ? (mt == -INFINITY ? 0.0f : mt) : fmaxf(mt, 0.0f);
+          const float d = kt == kt0 ? (mt == -INFINITY ? 0.0f : mt) : fmaxf(mt, 0.0f);
           exps(qb, base + d);
-          if (kt != 0) {
+          if (kt != kt0) {
             const float corr = exp2_raw(-d);
             l_run[qb] *= corr;
 #pragma unroll
@@ -475,7 +482,26 @@ void attn_prefill_kernel(
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
     const float l_tot = l_run[qb] + __shfl_xor(l_run[qb], 32, 64);
-    if (active[qb]) {
+    if (active[qb] && n_split > 1) {
+      // One of several key splits: the unnormalised partial (shift m_sh in the log2 domain, sum, weighted V) in
+      // the split-context decode kernel's layout, merged by the same log-sum-exp combine. A split with no visible
+      // key leaves l = 0 and contributes nothing.
+      const int64_t slot = (t[qb] * n_heads + head[qb]) * n_split + split;
+      float* orow = ws_o + slot * HD;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 32 * dt + 8 * i + 4 * hf;
+          *reinterpret_cast<float4*>(orow + d) =
+              make_float4(oacc[qb][dt][4 * i], oacc[qb][dt][4 * i + 1], oacc[qb][dt][4 * i + 2],
+                          oacc[qb][dt][4 * i + 3]);
+        }
+      if (hf == 0) {
+        ws_ml[2 * slot] = l_tot > 0.f ? m_sh[qb] : -INFINITY;  // an empty split must not raise the merged max
+        ws_ml[2 * slot + 1] = l_tot;
+      }
+    } else if (active[qb]) {
       const float inv = 1.0f / l_tot;
       float* orow = out + (t[qb] * n_heads + head[qb]) * HD;
 #pragma unroll
@@ -491,7 +517,54 @@ void attn_prefill_kernel(
   }
 }
 
+// Merges the key splits of the MFMA rows (partials in the decode kernel's layout: slot rh * n_split + s holds the
+// shift m in the log2 domain, the sum l and the weighted V row). One thread per (row x head rh, float4 column):
+// out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s, the splits taken in order.
+template <int HD>
+__global__ __launch_bounds__(256) void prefill_split_merge(const float* __restrict__ ws_o,
+                                                           const float* __restrict__ ws_ml, float* __restrict__ out,
+                                                           int64_t rows_heads, int n_split) {
+  constexpr int V4 = HD / 4;
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows_heads * V4) return;
+  const int64_t rh = i / V4;
+  const int c4 = int(i % V4);
+  const float* ml = ws_ml + rh * n_split * 2;
+  float mx = -INFINITY;
+  for (int sp = 0; sp < n_split; ++sp) mx = fmaxf(mx, ml[2 * sp]);
+  const float ms = mx == -INFINITY ? 0.0f : mx;
+  const float4* po = reinterpret_cast<const float4*>(ws_o + rh * n_split * HD) + c4;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float l = 0.f;
+  for (int sp = 0; sp < n_split; ++sp) {
+    const float w = exp2_raw(ml[2 * sp] - ms);
+    const float4 o = po[int64_t(sp) * V4];
+    acc.x += o.x * w;
+    acc.y += o.y * w;
+    acc.z += o.z * w;
+    acc.w += o.w * w;
+    l += ml[2 * sp + 1] * w;
+  }
+  const float inv = 1.0f / l;
+  reinterpret_cast<float4*>(out + rh * HD)[c4] = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+}
+
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+// Key splits per row tile for a launch of n_mfma MFMA rows at positions pos0..: 1 when the row tiles alone fill
+// the workgroup slots of the chip (3 per CU at head_dim 64, 2 at 128), otherwise enough to fill them, at most 16
+// and keeping at least two key tiles per split. Short prefill chunks - nibble's Transformer runs a prompt in
+// chunks of max_batch = 512 rows - would otherwise leave most CUs idle.
+int prefill_splits(int64_t n_mfma, int64_t pos0, int64_t group, int64_t n_kv, int64_t head_dim, int cu_count) {
+  const int64_t tiles = (n_mfma * group + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int64_t blocks = tiles * n_kv;
+  const int64_t target = int64_t(cu_count > 0 ? cu_count : 256) * (head_dim == 64 ? 3 : 2);
+  if (blocks >= target) return 1;
+  const int64_t key_tiles = (pos0 + n_mfma + kBN - 1) / kBN;  // the longest row tile's
+  int64_t sp = (target + blocks - 1) / blocks;
+  sp = std::min<int64_t>(sp, std::min<int64_t>(16, std::max<int64_t>(1, key_tiles / 2)));
+  return int(std::max<int64_t>(1, sp));
+}
 
 }  // namespace
 
@@ -534,10 +607,29 @@ int nbhs_append_stage_kv_f16(float* cache_k, float* cache_v, const float* k_new,
                              reinterpret_cast<const float2*>(cs_table), neox);
 }
 
+int64_t nbhs_attn_prefill_workspace_bound(int cu_count) {
+  // A split is taken only when blocks = tiles * KV < target, with sp <= ceil(target / blocks) and
+  // n_mfma <= 128 tiles / G, so n_mfma * n_heads * sp < 256 target: the bound is 256 target (head_dim + 2),
+  // largest over the two head sizes (targets 3 and 2 workgroups per CU).
+  const int64_t cus = cu_count > 0 ? cu_count : 256;
+  return std::max<int64_t>(256 * 3 * cus * (64 + 2), 256 * 2 * cus * (128 + 2));
+}
+
+int64_t nbhs_attn_prefill_workspace(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                    int64_t fp32_rows, int cu_count) {
+  if (n <= 0 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || fp32_rows < 0 ||
+      fp32_rows >= n || (head_dim != 64 && head_dim != 128))
+    return -1;
+  const int64_t n_mfma = n - fp32_rows;
+  const int sp = prefill_splits(n_mfma, pos0 + fp32_rows, n_heads / n_kv_heads, n_kv_heads, head_dim, cu_count);
+  return sp == 1 ? 0 : n_mfma * n_heads * sp * (head_dim + 2);
+}
+
 int nbhs_attn_prefill_mfma(const float* q, const void* k16, const void* vt16, float* out, int64_t n, int64_t pos0,
                            int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t staged_rows_pad,
                            const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, const float* k_cache,
-                           const float* v_cache, int64_t fp32_rows, nbhs_stream stream) {
+                           const float* v_cache, int64_t fp32_rows, float* workspace, int64_t workspace_floats,
+                           int cu_count, nbhs_stream stream) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (!q || !k16 || !vt16 || !out || n <= 0 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 ||
       n_heads % n_kv_heads != 0 || (head_dim != 64 && head_dim != 128) || staged_rows_pad % kBN != 0 ||
@@ -547,17 +639,27 @@ int nbhs_attn_prefill_mfma(const float* q, const void* k16, const void* vt16, fl
   const int64_t group = n_heads / n_kv_heads;
   const int64_t n_mfma = n - fp32_rows;
   const int64_t tiles = (n_mfma * group + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int sp = prefill_splits(n_mfma, pos0 + fp32_rows, group, n_kv_heads, head_dim, cu_count);
+  const int64_t need = sp == 1 ? 0 : n_mfma * n_heads * sp * (head_dim + 2);
+  if (need > 0 && (!workspace || workspace_floats < need)) return NBHS_EINVAL;
+  float* ws_o = need > 0 ? workspace : nullptr;
+  float* ws_ml = need > 0 ? workspace + n_mfma * n_heads * sp * head_dim : nullptr;
   const int64_t fp32_sub = (group + 3) / 4;  // head subgroups of the fp32 rows' workgroups (4 query heads each)
-  const int64_t blocks = tiles * n_kv_heads + fp32_rows * n_kv_heads * fp32_sub;
+  const int64_t blocks = tiles * n_kv_heads * sp + fp32_rows * n_kv_heads * fp32_sub;
   if (blocks >= int64_t(1) << 31) return NBHS_EINVAL;
   const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
   const int64_t off = fp32_rows * n_heads * head_dim;  // the MFMA rows start fp32_rows rows in
-  return nbhs_timing::launch(NBHS_K_PREFILL_MFMA, head_dim == 64 ? attn_prefill_kernel<64> : attn_prefill_kernel<128>,
-                             dim3(unsigned(blocks)), dim3(kWaves * 64), s, q + off, static_cast<const _Float16*>(k16),
-                             static_cast<const _Float16*>(vt16), out + off, n_mfma, pos0 + fp32_rows, int(n_heads),
-                             int(n_kv_heads), int(group), staged_rows_pad, int(tiles), qscale,
-                             reinterpret_cast<const float2*>(q_rope_cs), q_rope_neox, k_cache, v_cache, fp32_rows,
-                             int(fp32_sub));
+  const hipError_t e = nbhs_timing::launch(
+      NBHS_K_PREFILL_MFMA, head_dim == 64 ? attn_prefill_kernel<64> : attn_prefill_kernel<128>, dim3(unsigned(blocks)),
+      dim3(kWaves * 64), s, q + off, static_cast<const _Float16*>(k16), static_cast<const _Float16*>(vt16), out + off,
+      n_mfma, pos0 + fp32_rows, int(n_heads), int(n_kv_heads), int(group), staged_rows_pad, int(tiles), qscale,
+      reinterpret_cast<const float2*>(q_rope_cs), q_rope_neox, k_cache, v_cache, fp32_rows, int(fp32_sub), sp, ws_o,
+      ws_ml);
+  if (e != hipSuccess || sp == 1) return e;
+  const int64_t threads = n_mfma * n_heads * (head_dim / 4);
+  return nbhs_timing::launch(NBHS_K_DECODE_COMBINE, head_dim == 64 ? prefill_split_merge<64> : prefill_split_merge<128>,
+                             dim3(unsigned((threads + 255) / 256)), dim3(256), s, ws_o, ws_ml, out + off,
+                             n_mfma * n_heads, sp);
 }
 
 }  // extern "C"
