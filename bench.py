@@ -366,6 +366,17 @@ def main():
             be.append_rope_attention(q_pre[l], ck[l], cv[l], k_pre[l], v_pre[l], out_pre, n_pre, 0, H, KV, D, base,
                                      neox, ff)
 
+    def prefill_chunked_pass(chunk):
+        # as nibble's Transformer runs a prompt: chunks of max_batch rows, each through every layer
+        # (transformer.cpp:135-136; max_batch defaults to 512, transformer.h:24)
+        row_q = H * D
+        for p0 in range(0, n_pre, chunk):
+            m = min(chunk, n_pre - p0)
+            for l in range(NL):
+                be.append_rope_attention(q_pre[l].at(p0 * row_q), ck[l], cv[l], k_pre[l].at(p0 * row),
+                                         v_pre[l].at(p0 * row), out_pre.at(p0 * row_q), m, p0, H, KV, D, base, neox,
+                                         ff)
+
     def decode_step(s):
         pos0 = ctx + s
         for l in range(NL):
@@ -403,6 +414,19 @@ def main():
 
     (mfma_ms, mfma_n), (stage_ms, stage_n), (app2_ms, app2_n) = timed_pass(
         prefill_pass, [KernelTiming.PREFILL_MFMA, KernelTiming.STAGE_KV, KernelTiming.APPEND_ROPE])
+
+    # the same prefill in nibble's max_batch = 512 chunks (same rows, same results within rounding)
+    prefill_chunked_pass(512)
+    be.sync()
+    ch_ms = []
+    for _ in range(args.prefill_reps):
+        e0.record()
+        prefill_chunked_pass(512)
+        e1.record()
+        ch_ms.append(e0.elapsed_ms(e1))
+    ch_ms_med = float(np.median(ch_ms))
+    ch_tflops = pre_flops / (ch_ms_med * 1e-3) / 1e12
+    log(f"prefill in 512-row chunks: {ch_ms_med:.3f} ms for {NL} layers -> {ch_tflops:.1f} TFLOP/s")
 
     # ---------------- decode: warm-up steps, then exactly K timed steps (re-appending the same positions)
     for s in range(args.warmup):
@@ -467,6 +491,10 @@ def main():
                      "algorithmic_bytes_per_launch": int(roof_bytes / part_n)},
         "prefill": {"metric": "prefill attn TFLOP/s @8k", "value": round(pre_tflops, 2), "unit": "TFLOP/s",
                     "ms_per_prefill_16_layers": round(pre_ms_med, 4), "reps": args.prefill_reps,
+                    "chunked_512": {"value": round(ch_tflops, 2), "unit": "TFLOP/s",
+                                    "ms_per_prefill_16_layers": round(ch_ms_med, 4),
+                                    "note": "the same 8192 rows as nibble's Transformer runs them: 16 chunks of "
+                                            "max_batch = 512 rows, each through all 16 layers"},
                     "dtype": "f16 MFMA operands, f32 accumulate and softmax (rows < 256: f32, in the same launch)",
                     "roofline": {"bound": "mfma", "achieved": round(mfma_tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                                  "unit": "TFLOP/s", "frac": round(mfma_tflops / MFMA_F16_PEAK_TFLOPS, 4),
