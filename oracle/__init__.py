@@ -52,6 +52,14 @@ def _load():
         lib.orc_attention_f64.restype = None
         lib.orc_llama3_freq_factors.argtypes = [_F, _I, c_double, c_double, c_double, c_double, c_double]
         lib.orc_llama3_freq_factors.restype = None
+        lib.orc_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        lib.orc_fp16_to_fp32.restype = c_float
+        lib.orc_fp16_to_fp32_n.argtypes = [c_void_p, _F, _I]
+        lib.orc_fp16_to_fp32_n.restype = None
+        lib.orc_matmul.argtypes = [c_int, c_void_p, _I, _I, _F, _F, _I]
+        lib.orc_matmul.restype = c_int
+        lib.orc_add_bias.argtypes = [_F, _F, _I, _I]
+        lib.orc_add_bias.restype = None
         _lib = lib
     return _lib
 
@@ -75,6 +83,9 @@ def _load_ref():
             lib.ref_backend_reserve.argtypes = [c_void_p, _I, _I, _I, _I]
             lib.ref_backend_attention.argtypes = [c_void_p, _F, _F, _F, _F, _I, _I, _I, _I, _I]
             lib.ref_backend_rope.argtypes = [c_void_p, _F, _I, _I, _I, _I, c_float, c_int, _F]
+            lib.ref_matmul_scalar.argtypes = [c_int, c_void_p, _I, _I, _F, _F, _I]
+            lib.ref_add_bias.argtypes = [_F, _F, _I, _I]
+            lib.ref_backend_matmul.argtypes = [c_void_p, c_int, c_void_p, _I, _I, _F, _F, _I]
             _ref = lib
     return _ref
 
@@ -201,6 +212,67 @@ def ref_attention_simd(q, k, v, pos0, n_kv_heads):
     return out if rc == 0 else None
 
 
+def _w_type(w) -> int:
+    if w.dtype == np.float32:
+        return 0
+    if w.dtype == np.float16:
+        return 1
+    raise TypeError("float weights are float32 (F32) or float16 (F16)")
+
+
+def matmul(w, x):
+    """ref_ops.cpp:109-135 restated: y[n, out] = x[n, in] . W^T for W [out, in] float32 or float16, each dot
+    accumulated left to right in float."""
+    w = np.ascontiguousarray(w)
+    x = _f32(x)
+    out_, in_ = w.shape
+    n = x.size // in_
+    y = np.zeros((n, out_), np.float32)
+    if _load().orc_matmul(_w_type(w), w.ctypes.data, in_, out_, _fp(x), _fp(y), n) != 0:
+        raise ValueError("orc_matmul: bad weight type")
+    return y
+
+
+def matmul_f64(w, x):
+    """Independent fp64 product of the same float32 / float16 inputs."""
+    return np.asarray(x, np.float64).reshape(-1, w.shape[1]) @ np.asarray(w, np.float64).T
+
+
+def fp16_to_fp32(h):
+    """IEEE halves (uint16 array) to float32, bit-exact (NaN payloads kept)."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.zeros(h.shape, np.float32)
+    _load().orc_fp16_to_fp32_n(h.ctypes.data, _fp(out), h.size)
+    return out
+
+
+def add_bias(x, b):
+    """ref_ops.cpp:154-160 restated: every row of x [n, d] += b [d], in place on a copy."""
+    y = _f32(x).copy()
+    b = _f32(b)
+    _load().orc_add_bias(_fp(y), _fp(b), b.size, y.size // b.size)
+    return y
+
+
+def ref_matmul_scalar(w, x):
+    """The compiled reference's cpu::matmul_rows (scalar float path)."""
+    w = np.ascontiguousarray(w)
+    x = _f32(x)
+    out_, in_ = w.shape
+    n = x.size // in_
+    y = np.zeros((n, out_), np.float32)
+    if _load_ref().ref_matmul_scalar(_w_type(w), w.ctypes.data, in_, out_, _fp(x), _fp(y), n) != 0:
+        raise RuntimeError("ref_matmul_scalar failed")
+    return y
+
+
+def ref_add_bias(x, b):
+    y = _f32(x).copy()
+    b = _f32(b)
+    _load_ref().ref_add_bias(_fp(y), _fp(b), b.size, y.size // b.size)
+    return y
+
+
 def ref_kernel_set() -> str:
     return _load_ref().ref_kernel_set().decode()
 
@@ -233,6 +305,17 @@ class RefCpuBackend:
                                         _fp(freq_factors))
         if rc != 0:
             raise RuntimeError("rope failed")
+
+    def matmul(self, w, x):
+        """CpuBackend::matmul: the production tier over the pool."""
+        w = np.ascontiguousarray(w)
+        x = _f32(x)
+        out_, in_ = w.shape
+        n = x.size // in_
+        y = np.zeros((n, out_), np.float32)
+        if self._lib.ref_backend_matmul(self._h, _w_type(w), w.ctypes.data, in_, out_, _fp(x), _fp(y), n) != 0:
+            raise RuntimeError("matmul failed")
+        return y
 
     def close(self):
         if self._h:

@@ -179,3 +179,51 @@ int orc_attention_heads_parallel(const float* q, const float* k, const float* v,
   free(tids);
   return 0;
 }
+
+/* ---- float matmul and bias (the Transformer's QKV projection into the cache, transformer.cpp:171-194) ---- */
+
+float orc_fp16_to_fp32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+  union {
+    uint32_t u;
+    float f;
+  } r;
+  if (e == 0x1Fu) {
+    r.u = sign | 0x7F800000u | (m << 13); /* inf, NaN (payload kept) */
+  } else if (e != 0) {
+    r.u = sign | ((e + 112u) << 23) | (m << 13); /* rebias 15 -> 127 */
+  } else {
+    r.f = (float)m * 0x1p-24f; /* zero and subnormals: m * 2^-24, exact */
+    r.u |= sign;
+  }
+  return r.f;
+}
+
+void orc_fp16_to_fp32_n(const uint16_t* h, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_fp16_to_fp32(h[i]);
+}
+
+int orc_matmul(int w_type, const void* w, int64_t in, int64_t out, const float* x, float* y, int64_t n) {
+  if (w_type != 0 && w_type != 1) return -1;
+  for (int64_t t = 0; t < n; ++t) {
+    const float* xt = x + t * in;
+    for (int64_t r = 0; r < out; ++r) {
+      float acc = 0.0f;
+      if (w_type == 0) {
+        const float* wr = (const float*)w + r * in;
+        for (int64_t k = 0; k < in; ++k) acc += xt[k] * wr[k];
+      } else {
+        const uint16_t* wr = (const uint16_t*)w + r * in;
+        for (int64_t k = 0; k < in; ++k) acc += xt[k] * orc_fp16_to_fp32(wr[k]);
+      }
+      y[t * out + r] = acc;
+    }
+  }
+  return 0;
+}
+
+void orc_add_bias(float* x, const float* b, int64_t d, int64_t n) {
+  for (int64_t t = 0; t < n; ++t)
+    for (int64_t i = 0; i < d; ++i) x[t * d + i] += b[i];
+}

@@ -16,6 +16,10 @@
  *                          tests/test_ops.cpp:196-216 against orc_attention_scalar.
  *   orc_exp_ps             <= 2e-7 relative vs exp() over [-88, 88] (simd_helpers_test.cpp:92-137 contract).
  *   orc_attention_f64      independent fp64 brute force (tests/naive_llama.h:118-134 pattern); known answers.
+ *   orc_matmul             bit-exact vs the compiled reference's scalar matmul_rows (oracle/_ref), F32 and F16
+ *                          weights; fp64 brute force; the reference's AVX2 tier within float rounding.
+ *   orc_fp16_to_fp32       every one of the 65536 halves (NaN payloads included) against numpy's exact conversion.
+ *   orc_add_bias           bit-exact vs the compiled reference's cpu::add_bias.
  *   orc_llama3_freq_factors  closed form of llama.cpp's Llama-3 rope scaling (third-party, not vendored):
  *                          checked against its defining properties (band limits, continuity at both edges,
  *                          monotonicity). Bit-level parity with the converter's float32 output is UNPINNED.
@@ -65,6 +69,20 @@ int orc_attention_heads_parallel(const float* q, const float* k, const float* v,
 /* Independent fp64 brute force (tests/naive_llama.h:118-134 pattern) on the same fp32 inputs; out is double. */
 void orc_attention_f64(const float* q, const float* k, const float* v, double* out, int64_t n, int64_t pos0,
                        int64_t n_heads, int64_t n_kv_heads, int64_t head_dim);
+
+/* IEEE binary16 -> binary32, exact (every half is a float), as fp16.h:18-41 converts F16 weights. */
+float orc_fp16_to_fp32(uint16_t h);
+/* The same over n halves into memory (a float return value can quiet a signalling NaN on its way out). */
+void orc_fp16_to_fp32_n(const uint16_t* h, float* out, int64_t n);
+
+/* ref_ops.cpp:109-135 (cpu::matmul_rows, float weights): y[t*out + r] = sum_k x[t*in + k] * w[r*in + k] for
+ * t < n, r < out, each dot accumulated left to right in float with no FMA (this file is built with
+ * -ffp-contract=off, as ref_ops.cpp is, CMakeLists.txt:72-73). w_type 0 = F32 (floats), 1 = F16 (halves, converted
+ * exactly). Returns -1 for another w_type. */
+int orc_matmul(int w_type, const void* w, int64_t in, int64_t out, const float* x, float* y, int64_t n);
+
+/* ref_ops.cpp:154-160 (cpu::add_bias): x[t*d + i] += b[i] for t < n. */
+void orc_add_bias(float* x, const float* b, int64_t d, int64_t n);
 
 /* Llama-3 rope frequency factors (llama.cpp convert_hf_to_gguf.py, rope_type "llama3"; not in the reference
  * tree, the reference only reads rope_freqs.weight, weights.cpp:56, and divides by it, ref_ops.cpp:175):

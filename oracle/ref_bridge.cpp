@@ -60,6 +60,38 @@ const char* ref_kernel_set() {
   }
 }
 
+namespace {
+nibble::Tensor weight(int type, const void* w, int64_t in, int64_t out) {
+  nibble::Tensor t;
+  t.type = type == 1 ? nibble::DType::F16 : nibble::DType::F32;
+  t.n_dims = 2;
+  t.ne = {in, out, 1, 1};
+  t.data = w;
+  return t;
+}
+}  // namespace
+
+// nibble::cpu::matmul_rows (ref_ops.cpp:109-135), all output rows, float weights (type 0 F32, 1 F16).
+int ref_matmul_scalar(int type, const void* w, int64_t in, int64_t out, const float* x, float* y, int64_t n) {
+  try {
+    nibble::cpu::matmul_rows(weight(type, w, in, out), x, y, n, 0, out, nullptr);
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// nibble::cpu::add_bias (ref_ops.cpp:154-160); the bias is an F32 vector of d floats.
+int ref_add_bias(float* x, const float* b, int64_t d, int64_t n) {
+  nibble::Tensor t;
+  t.type = nibble::DType::F32;
+  t.n_dims = 1;
+  t.ne = {d, 1, 1, 1};
+  t.data = b;
+  nibble::cpu::add_bias(x, t, n);
+  return 0;
+}
+
 // A ThreadPool of `threads` threads and a CpuBackend on it (nibble.cpp:75-85 builds the same pair).
 void* ref_backend_create(int threads) {
   try {
@@ -97,6 +129,18 @@ int ref_backend_rope(void* h, float* x, int64_t n, int64_t n_heads, int64_t head
                      int neox, const float* freq_factors) {
   try {
     static_cast<RefBackend*>(h)->be.rope(x, n, n_heads, head_dim, pos0, {base, neox != 0, freq_factors});
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// CpuBackend::matmul (cpu_backend.cpp:134-138 -> matmul_multi :146-248): the production tier (AVX2 gemm_f /
+// matmul_rows_f on this host) over the pool.
+int ref_backend_matmul(void* h, int type, const void* w, int64_t in, int64_t out, const float* x, float* y,
+                       int64_t n) {
+  try {
+    static_cast<RefBackend*>(h)->be.matmul(weight(type, w, in, out), x, y, n);
     return 0;
   } catch (const std::exception&) {
     return -1;

@@ -282,3 +282,81 @@ def test_pins_reject_planted_attention_mistakes():
     assert not matches_gold(key, oracle.attention_scalar(q, v, k, pos0, KV))
     # and the tolerance checks would catch them too (differences far above 1e-3)
     assert np.max(np.abs(oracle.attention_scalar(q, v, k, pos0, KV) - oracle.attention_scalar(q, k, v, pos0, KV))) > 1e-2
+
+
+# ---- float matmul and bias (the QKV projection into the cache, transformer.cpp:171-194) ----
+
+MATMUL_SHAPES = [(1, 1, 1), (1, 64, 96), (3, 129, 17), (5, 2048, 64), (16, 896, 128), (40, 256, 300)]
+
+
+@pytest.mark.skipif(not oracle.have_ref(), reason="oracle/_ref not built")
+@pytest.mark.parametrize("dt", [np.float32, np.float16])
+@pytest.mark.parametrize("n,k,m", MATMUL_SHAPES)
+def test_matmul_restatement_bit_exact_vs_reference(dt, n, k, m):
+    """orc_matmul reproduces the reference's scalar float matmul (ref_ops.cpp:109-135) bit for bit."""
+    rng = np.random.default_rng(n * 1000 + k + m)
+    w = (rng.standard_normal((m, k)) * 0.05).astype(dt)
+    x = rng.standard_normal((n, k)).astype(np.float32)
+    assert bits_equal(oracle.matmul(w, x), oracle.ref_matmul_scalar(w, x))
+
+
+@pytest.mark.skipif(not oracle.have_ref(), reason="oracle/_ref not built")
+@pytest.mark.parametrize("dt", [np.float32, np.float16])
+def test_matmul_against_fp64_and_the_reference_tier(dt):
+    """The float dot's only error is float rounding: within 1e-5 of an fp64 product of the same inputs (relative to
+    the row's sum of |terms|), and the reference's production tier (AVX2 gemm / matmul_rows_f, another order)
+    agrees to the same bound."""
+    rng = np.random.default_rng(7)
+    w = (rng.standard_normal((200, 2048)) * 0.03).astype(dt)
+    x = rng.standard_normal((9, 2048)).astype(np.float32)
+    y = oracle.matmul(w, x)
+    scale = np.abs(x).astype(np.float64) @ np.abs(np.asarray(w, np.float64)).T
+    assert np.all(np.abs(y - oracle.matmul_f64(w, x)) <= 1e-5 * scale)
+    cb = oracle.RefCpuBackend(4)
+    try:
+        assert np.all(np.abs(cb.matmul(w, x) - y) <= 1e-5 * scale)
+    finally:
+        cb.close()
+
+
+def test_matmul_planted_mistakes_fail():
+    """A transposed weight or a reversed accumulation order does not reproduce the restatement."""
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((64, 64)) * 0.1).astype(np.float32)
+    x = rng.standard_normal((4, 64)).astype(np.float32)
+    y = oracle.matmul(w, x)
+    assert not np.allclose(oracle.matmul(np.ascontiguousarray(w.T), x), y, atol=1e-3)
+    rev = np.zeros_like(y)
+    for t in range(4):
+        for r in range(64):
+            acc = np.float32(0)
+            for kk in range(63, -1, -1):
+                acc = np.float32(acc + np.float32(x[t, kk] * w[r, kk]))
+            rev[t, r] = acc
+    assert not bits_equal(rev, y)
+    fwd = np.zeros_like(y)
+    for t in range(4):
+        for r in range(64):
+            acc = np.float32(0)
+            for kk in range(64):
+                acc = np.float32(acc + np.float32(x[t, kk] * w[r, kk]))
+            fwd[t, r] = acc
+    assert bits_equal(fwd, y)  # the same loop in the forward order is the restatement
+
+
+def test_fp16_conversion_every_half():
+    """orc_fp16_to_fp32 (fp16.h:18-41 restated) on all 65536 halves, NaN payloads included, against numpy's exact
+    float16 -> float32 conversion."""
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    assert bits_equal(oracle.fp16_to_fp32(h), want)
+
+
+@pytest.mark.skipif(not oracle.have_ref(), reason="oracle/_ref not built")
+def test_add_bias_bit_exact_vs_reference():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((7, 96)).astype(np.float32)
+    b = rng.standard_normal(96).astype(np.float32)
+    y = oracle.add_bias(x, b)
+    assert bits_equal(y, oracle.ref_add_bias(x, b))
+    assert bits_equal(y, x + b[None, :])
