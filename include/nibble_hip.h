@@ -33,6 +33,17 @@ extern "C" {
 typedef struct nbh_backend nbh_backend;
 typedef struct nbh_event nbh_event;
 
+/* A weight view, field for field nibble::Tensor (src/tensor.h:21-66): type is the ggml type id (0 = F32, 1 = F16),
+ * ne[1] * ne[2] * ne[3] rows of ne[0] elements, row-major at data. data is host memory (copied to HBM on first use
+ * and kept until nbh_backend_release_weights; its bytes must not change meanwhile) or lies inside a buffer from
+ * nbh_backend_alloc (used in place). */
+typedef struct nbh_tensor {
+  uint32_t type;
+  int32_t n_dims;
+  int64_t ne[4];
+  const void* data;
+} nbh_tensor;
+
 /* Message of the calling thread's last failed call ("" if none). */
 const char* nbh_last_error(void);
 
@@ -44,7 +55,7 @@ int nbh_backend_create(int device, nbh_backend** out);
 void nbh_backend_destroy(nbh_backend* be);
 
 /* Backend::supports (backend.h:41): whether weight type `dtype` (ggml id) can run matmul/embed. Always 0 for
- * now: the HIP backend covers the attention path, not weight ops. */
+ * now: embed is not on the GPU yet, so a whole model cannot bind (matmul itself takes F32 and F16). */
 int nbh_backend_supports(const nbh_backend* be, uint32_t dtype, int* out);
 
 /* Backend::reserve (backend.h:45; ReserveParams backend.h:24-26). */
@@ -111,6 +122,23 @@ int nbh_backend_append_rope_attention_batch(nbh_backend* be, int64_t n_seq, cons
                                             int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float freq_base,
                                             int neox, const float* freq_factors);
 
+/* Backend::matmul (backend.h:56): y[n, w.rows] = x[n, w.ne[0]] . W^T for F32/F16 weights (ref_ops.cpp:109-135),
+ * fp32 products and sums in another order than the reference's (equal within float rounding). x, y device. */
+int nbh_backend_matmul(nbh_backend* be, const nbh_tensor* w, const float* x, float* y, int64_t n);
+
+/* Backend::matmul_multi (backend.h:57-60): ys[i] = matmul(ws[i], x, n) for n_w weights sharing the input x; the
+ * QKV projection of src/model/transformer.cpp:177-180 passes ys = {q, k cache rows, v cache rows}. ws and ys are
+ * host arrays. */
+int nbh_backend_matmul_multi(nbh_backend* be, int64_t n_w, const nbh_tensor* const* ws, const float* x,
+                             float* const* ys, int64_t n);
+
+/* Backend::add_bias (backend.h:63, ref_ops.cpp:154-160): each of the n rows of x [n, bias.ne[0]] += bias (F32);
+ * bit-exact. */
+int nbh_backend_add_bias(nbh_backend* be, float* x, const nbh_tensor* bias, int64_t n);
+
+/* Drops every device copy of a host weight; no reference counterpart (CpuBackend reads weights in place). */
+int nbh_backend_release_weights(nbh_backend* be);
+
 /* Extension of Backend::reserve for shapes ReserveParams does not carry: sizes the prefill operand staging
  * (n_kv_heads x head_dim at the reserved n_ctx) so that the first prefill allocates nothing. */
 int nbh_backend_reserve_attention(nbh_backend* be, int64_t n_kv_heads, int64_t head_dim);
@@ -126,6 +154,7 @@ int nbh_backend_sync(nbh_backend* be);
 int nbh_backend_live_allocations(const nbh_backend* be, int64_t* out);
 int nbh_backend_internal_bytes(const nbh_backend* be, int64_t* out);
 int nbh_backend_cu_count(const nbh_backend* be, int* out);
+int nbh_backend_weight_bytes(const nbh_backend* be, int64_t* out); /* HBM held by copies of host weights */
 
 /* Synthetic N(0,1)*scale data generated on the device (benchmarks). No reference counterpart. */
 int nbh_backend_fill_normal(nbh_backend* be, float* dst, int64_t count, uint64_t seed, float scale);

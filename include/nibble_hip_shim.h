@@ -21,9 +21,11 @@ extern "C" {
 #endif
 
 #define NBHS_EINVAL 1 /* hipErrorInvalidValue: a size or shape the launcher does not accept */
+#define NBHS_EBLAS 100000 /* a rocBLAS call failed (outside hipError_t's range) */
 
 typedef struct nbhs_stream_* nbhs_stream; /* a hipStream_t */
 typedef struct nbhs_event_* nbhs_event;   /* a hipEvent_t */
+typedef struct nbhs_blas_* nbhs_blas;     /* a rocblas_handle */
 
 /* ---- device, streams, events, memory ---- */
 
@@ -144,6 +146,27 @@ int64_t nbhs_attn_prefill_workspace_bound(int cu_count);
 /* Synthetic N(0,1)*scale data for benchmarks: counter-based (SplitMix64 of seed and index), Box-Muller in fp32. */
 int nbhs_fill_normal_f32(float* dst, int64_t count, uint64_t seed, float scale, nbhs_stream s);
 
+/* ---- float-weight projections (Backend::matmul / matmul_multi / add_bias, backend.h:56-62) ---- */
+
+#define NBHS_GEMV_MAX_WEIGHTS 8
+#define NBHS_GEMV_MAX_ROWS 16
+/* Up to 8 weights sharing one input in one launch, for n <= 16 rows (decode, short appends): for each i,
+ * y[i][t * rows[i] + r] = sum_k x[t * in + k] * w[i][r * in + k] (ref_ops.cpp:109-135 semantics; fp32 accumulation in
+ * another order than the reference's, so equal within float rounding). w[i] is F32 (f16[i] = 0) or F16 (f16[i] = 1)
+ * [rows[i], in] in device memory. */
+int nbhs_gemv_multi(int n_w, const int* f16, const void* const* w, float* const* y, const int64_t* rows, int64_t in,
+                    const float* x, int64_t n, nbhs_stream s);
+/* Exact widening of count IEEE halves to floats. */
+int nbhs_f16_to_f32(const void* src, float* dst, int64_t count, nbhs_stream s);
+/* ref_ops.cpp:154-160 (cpu::add_bias): x[t * d + i] += bias[i] for t < n; bit-exact. */
+int nbhs_add_bias_f32(float* x, const float* bias, int64_t d, int64_t n, nbhs_stream s);
+/* A rocBLAS handle bound to stream s (its device workspace is allocated here, once). */
+int nbhs_blas_create(nbhs_blas* out, nbhs_stream s);
+int nbhs_blas_destroy(nbhs_blas h);
+/* y[n, out] = x[n, in] . w[out, in]^T in fp32 (rocBLAS sgemm, full fp32 math), on the handle's stream: the same
+ * product as nbhs_gemv_multi, for any n. */
+int nbhs_sgemm_xwt(nbhs_blas h, const float* x, const float* w, float* y, int64_t n, int64_t in, int64_t out);
+
 /* ---- per-kernel timing (measurement only) ----
  * While enabled for a kernel, its launcher launches it with a HIP event pair (hipExtLaunchKernel) stamped from the
  * dispatch itself, so the average device duration of that kernel can be read back live (bench.py's roofline
@@ -157,7 +180,10 @@ enum nbhs_kernel_id {
   NBHS_K_GENERIC = 4,
   NBHS_K_STAGE_KV = 5,
   NBHS_K_PREFILL_MFMA = 6,
-  NBHS_K_COUNT = 7
+  NBHS_K_GEMV = 7,
+  NBHS_K_CONVERT = 8,
+  NBHS_K_ADD_BIAS = 9,
+  NBHS_K_COUNT = 10
 };
 int nbhs_kernel_timing_enable(int on); /* on != 0: time every kernel; 0: none (clears what was recorded) */
 int nbhs_kernel_timing_select(uint32_t kernel_mask); /* time the kernels whose bit (1 << id) is set; clears */

@@ -1,4 +1,4 @@
-"""nibble_amd: nibble's attention path (RoPE, KV-cache append, causal GQA attention) on one MI355X.
+"""nibble_amd: nibble's attention path (QKV projection, RoPE, KV-cache append, causal GQA attention) on one MI355X.
 
 The product is libnibble_hip.so: hand-written HIP kernels for gfx950 behind a C++20 HipBackend that implements
 nibble's Backend operator interface (reference src/backend/backend.h:36-71), exported through the C ABI in
@@ -18,6 +18,14 @@ LIB_PATH = os.path.join(_DIR, "libnibble_hip.so")
 
 _F = POINTER(c_float)
 _I = c_int64
+
+# ggml type ids of the weight types the GPU matmul takes (src/tensor.h:21-31 in the reference).
+F32, F16 = 0, 1
+
+
+class NbhTensor(ctypes.Structure):
+    """nbh_tensor: a weight view, field for field nibble::Tensor."""
+    _fields_ = [("type", c_uint32), ("n_dims", ctypes.c_int32), ("ne", c_int64 * 4), ("data", c_void_p)]
 
 # Every function the C ABI exports, with its ctypes signature (restype, argtypes).
 _SIGNATURES = {
@@ -42,6 +50,11 @@ _SIGNATURES = {
     "nbh_backend_append_rope_attention_batch": (c_int, [c_void_p, _I, c_void_p, c_void_p, c_void_p, c_void_p,
                                                         c_void_p, c_void_p, c_void_p, _I, _I, _I, c_float, c_int,
                                                         c_void_p]),
+    "nbh_backend_matmul": (c_int, [c_void_p, POINTER(NbhTensor), c_void_p, c_void_p, _I]),
+    "nbh_backend_matmul_multi": (c_int, [c_void_p, _I, c_void_p, c_void_p, c_void_p, _I]),
+    "nbh_backend_add_bias": (c_int, [c_void_p, c_void_p, POINTER(NbhTensor), _I]),
+    "nbh_backend_release_weights": (c_int, [c_void_p]),
+    "nbh_backend_weight_bytes": (c_int, [c_void_p, POINTER(c_int64)]),
     "nbh_backend_reserve_attention": (c_int, [c_void_p, _I, _I]),
     "nbh_backend_reserve_rope": (c_int, [c_void_p, _I, c_float, c_int, c_void_p]),
     "nbh_backend_sync": (c_int, [c_void_p]),
@@ -106,6 +119,26 @@ class DevicePtr(int):
         return DevicePtr(int(self) + 4 * int(floats))
 
 
+def weight(w, shape=None, dtype=None) -> NbhTensor:
+    """An nbh_tensor for a weight: a 2-D (or 1-D) float32/float16 host array, or a DevicePtr into a buffer of
+    this backend with its (rows, ne0) shape and type (F32 or F16)."""
+    if isinstance(w, np.ndarray):
+        if w.dtype == np.float32:
+            t = F32
+        elif w.dtype == np.float16:
+            t = F16
+        else:
+            raise BackendError(f"weight dtype {w.dtype}: the GPU matmul takes float32 and float16")
+        assert w.flags.c_contiguous
+        shape, data = w.shape, w.ctypes.data
+    else:
+        if shape is None or dtype is None:
+            raise BackendError("a device weight needs its shape and type")
+        t, data = dtype, int(w)
+    ne = [int(shape[-1]), int(shape[0]) if len(shape) > 1 else 1, 1, 1]
+    return NbhTensor(t, len(shape), (c_int64 * 4)(*ne), c_void_p(data))
+
+
 class HipBackend:
     """Python face of nibble::hip::HipBackend (the reference's Backend interface on one gfx950 GPU)."""
 
@@ -113,6 +146,9 @@ class HipBackend:
         h = c_void_p()
         _check(lib().nbh_backend_create(device, byref(h)))
         self._h = h
+        # Host weight arrays whose device copies the backend keeps (by address): held here so that no other array
+        # takes their address while the copy is live.
+        self._kept = {}
 
     # -- Backend members (backend.h:36-71) --
     def supports(self, dtype: int) -> bool:
@@ -187,6 +223,37 @@ class HipBackend:
                                                              freq_base, int(bool(neox)),
                                                              None if ff is None else _host_ptr(ff)))
 
+    def _tensor(self, w, shape=None, dtype=None) -> NbhTensor:
+        if isinstance(w, np.ndarray):
+            self._kept[w.ctypes.data] = w
+        return weight(w, shape, dtype)
+
+    def matmul(self, w, x, y, n: int, shape=None, dtype=None):
+        """y[n, rows] = x[n, ne0] . W^T; w a host array (float32/float16) or a DevicePtr with shape and dtype."""
+        t = self._tensor(w, shape, dtype)
+        _check(lib().nbh_backend_matmul(self._h, byref(t), c_void_p(int(x)), c_void_p(int(y)), n))
+
+    def matmul_multi(self, ws, x, ys, n: int):
+        """ys[i] = matmul(ws[i], x, n) for host weight arrays (or NbhTensor views) sharing the input x."""
+        ts = [w if isinstance(w, NbhTensor) else self._tensor(w) for w in ws]
+        tp = (c_void_p * len(ts))(*[ctypes.addressof(t) for t in ts])
+        yp = (c_void_p * len(ys))(*[int(y) for y in ys])
+        _check(lib().nbh_backend_matmul_multi(self._h, len(ts), tp, c_void_p(int(x)), yp, n))
+
+    def add_bias(self, x, bias, n: int):
+        """Each of the n rows of x += bias (a float32 host array or an NbhTensor)."""
+        t = bias if isinstance(bias, NbhTensor) else self._tensor(np.ascontiguousarray(bias, dtype=np.float32))
+        _check(lib().nbh_backend_add_bias(self._h, c_void_p(int(x)), byref(t), n))
+
+    def release_weights(self):
+        _check(lib().nbh_backend_release_weights(self._h))
+        self._kept.clear()
+
+    def weight_bytes(self) -> int:
+        out = c_int64()
+        _check(lib().nbh_backend_weight_bytes(self._h, byref(out)))
+        return out.value
+
     def reserve_attention(self, n_kv_heads: int, head_dim: int):
         _check(lib().nbh_backend_reserve_attention(self._h, n_kv_heads, head_dim))
 
@@ -252,7 +319,7 @@ class KernelTiming:
     """Live per-kernel device durations from the shim's launch bracketing (nbhs_kernel_timing_*,
     include/nibble_hip_shim.h). Used by the benchmark for roofline figures."""
 
-    ROPE, APPEND_ROPE, DECODE_PARTIAL, DECODE_COMBINE, GENERIC, STAGE_KV, PREFILL_MFMA = range(7)
+    ROPE, APPEND_ROPE, DECODE_PARTIAL, DECODE_COMBINE, GENERIC, STAGE_KV, PREFILL_MFMA, GEMV, CONVERT, ADD_BIAS = range(10)
 
     @staticmethod
     def enable(on: bool = True, only: int | None = None):

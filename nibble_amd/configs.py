@@ -22,14 +22,16 @@ class Shape:
     rope_base: float
     neox: bool
     llama3: bool = False  # Llama-3 frequency scaling: factor 32, low 1, high 4, original context 8192
+    n_embd: int = 0  # model width: the QKV projection's input width
+    qkv_bias: bool = False  # q/k/v projections carry biases (qwen2)
 
     def freq_factors(self):
         return synth.llama3_freq_factors(self.head_dim, self.rope_base) if self.llama3 else None
 
 
-QWEN25_05B = Shape("qwen2.5-0.5b", 14, 2, 64, 24, 1e6, True)
-TINYLLAMA_11B = Shape("tinyllama-1.1b", 32, 4, 64, 22, 1e4, False)
-LLAMA32_1B = Shape("llama-3.2-1b", 32, 8, 64, 16, 5e5, False, llama3=True)
+QWEN25_05B = Shape("qwen2.5-0.5b", 14, 2, 64, 24, 1e6, True, n_embd=896, qkv_bias=True)
+TINYLLAMA_11B = Shape("tinyllama-1.1b", 32, 4, 64, 22, 1e4, False, n_embd=2048)
+LLAMA32_1B = Shape("llama-3.2-1b", 32, 8, 64, 16, 5e5, False, llama3=True, n_embd=2048)
 
 # Stream-key tensor ids for synth.stream_key(config, layer, sequence, tensor, ...).
 T_Q, T_K, T_V, T_KCACHE, T_VCACHE, T_SCALE = 1, 2, 3, 4, 5, 6

@@ -16,6 +16,9 @@ constexpr int64_t kDecodeMaxRows = 16;
 // Prefill rows at positions below this see fewer keys than it takes for fp16 rounding of single V rows to
 // average out; they take the fp32 kernel (a few hundred rows, negligible work next to the MFMA pass).
 constexpr int64_t kFp32PrefixRows = 256;
+// matmul calls with at most this many rows take the weight-streaming gemv kernel; longer ones are GEMMs.
+constexpr int64_t kGemvMaxRows = NBHS_GEMV_MAX_ROWS;
+constexpr size_t kGemvMaxWeights = NBHS_GEMV_MAX_WEIGHTS;
 
 std::string str(int64_t v) { return std::to_string(v); }
 
@@ -36,6 +39,12 @@ HipBackend::~HipBackend() {
   nbhs_free(k16_);
   nbhs_free(vt16_);
   nbhs_free(copy_tmp_);
+  nbhs_free(widen_tmp_);
+  for (auto& [key, d] : weights_) {
+    nbhs_free(const_cast<void*>(d.dev));
+    nbhs_free(d.f32);
+  }
+  if (blas_) nbhs_blas_destroy(blas_);
   if (stream_) nbhs_stream_destroy(stream_);
 }
 
@@ -75,7 +84,7 @@ void HipBackend::ensure(float*& buf, size_t& cap_bytes, size_t need_bytes) {
 }
 
 size_t HipBackend::internal_bytes() const {
-  size_t s = decode_ws_bytes_ + k16_bytes_ + vt16_bytes_ + copy_tmp_bytes_;
+  size_t s = decode_ws_bytes_ + k16_bytes_ + vt16_bytes_ + copy_tmp_bytes_ + widen_tmp_bytes_;
   for (auto& t : rope_tables_) s += size_t(t.rows) * size_t(t.head_dim) * sizeof(float);
   return s;
 }
@@ -168,6 +177,170 @@ void HipBackend::fill_normal(float* dst, int64_t count, uint64_t seed, float sca
   if (count == 0) return;
   check_range(dst, count, "fill_normal", "dst");
   check(nbhs_fill_normal_f32(dst, count, seed, scale, stream_), "fill_normal");
+}
+
+// ---- weights and the QKV projection (transformer.cpp:171-194) ----
+
+bool HipBackend::in_buffer(const void* p, int64_t bytes) const {
+  const auto a = reinterpret_cast<uintptr_t>(p);
+  auto it = allocs_.upper_bound(a);
+  if (it == allocs_.begin()) return false;
+  --it;
+  return a >= it->first && a - it->first + uint64_t(bytes) <= it->second;
+}
+
+HipBackend::DeviceWeight HipBackend::device_weight(const Tensor& w, const char* op) {
+  if (!w.data) throw Error(std::string(op) + ": weight data is null");
+  if (w.type != DType::F32 && w.type != DType::F16)
+    throw Error(std::string(op) + ": weight type " + str(int64_t(w.type)) +
+                " is not supported by the GPU backend (F32 and F16 only)");
+  const int64_t in = w.ne[0], rows = w.rows();
+  const int64_t elem = w.type == DType::F32 ? 4 : 2;
+  int64_t count, bytes;
+  if (in <= 0 || rows <= 0 || overflow_mul(in, rows, &count) || overflow_mul(count, elem, &bytes))
+    throw Error(std::string(op) + ": invalid weight shape " + str(in) + " x " + str(rows));
+  if (reinterpret_cast<uintptr_t>(w.data) % size_t(elem) != 0)
+    throw Error(std::string(op) + ": weight data is not aligned to its element size");
+  DeviceWeight d;
+  d.type = w.type;
+  d.in = in;
+  d.rows = rows;
+  if (in_buffer(w.data, bytes)) {  // already in HBM: use in place
+    d.dev = w.data;
+    return d;
+  }
+  auto it = weights_.find(w.data);
+  if (it != weights_.end()) {
+    if (it->second.type == w.type && it->second.in == in && it->second.rows == rows) return it->second;
+    // The same host address now describes another tensor: replace the copy.
+    check(nbhs_stream_sync(stream_), "sync before weight replacement");
+    nbhs_free(const_cast<void*>(it->second.dev));
+    nbhs_free(it->second.f32);
+    weights_.erase(it);
+  }
+  void* p = nullptr;
+  check(nbhs_malloc(&p, size_t(bytes)), "weight allocation");
+  const int cr = nbhs_memcpy_h2d(p, w.data, size_t(bytes), stream_);
+  if (cr != 0) {
+    nbhs_free(p);
+    check(cr, "weight upload");
+  }
+  d.dev = p;
+  d.key = w.data;
+  weights_.emplace(w.data, d);
+  return d;
+}
+
+const float* HipBackend::weight_f32(const DeviceWeight& d) {
+  if (d.type == DType::F32) return static_cast<const float*>(d.dev);
+  const int64_t count = d.in * d.rows;
+  if (!d.key) {  // in place: widen into a scratch buffer for this call
+    ensure(widen_tmp_, widen_tmp_bytes_, size_t(count) * sizeof(float));
+    check(nbhs_f16_to_f32(d.dev, widen_tmp_, count, stream_), "weight widening");
+    return widen_tmp_;
+  }
+  DeviceWeight& kept = weights_.at(d.key);
+  if (!kept.f32) {
+    void* p = nullptr;
+    check(nbhs_malloc(&p, size_t(count) * sizeof(float)), "weight widening allocation");
+    const int cr = nbhs_f16_to_f32(kept.dev, static_cast<float*>(p), count, stream_);
+    if (cr != 0) {
+      nbhs_free(p);
+      check(cr, "weight widening");
+    }
+    kept.f32 = static_cast<float*>(p);
+  }
+  return kept.f32;
+}
+
+void HipBackend::release_weights() {
+  if (weights_.empty()) return;
+  check(nbhs_stream_sync(stream_), "sync before weight release");
+  for (auto& [key, d] : weights_) {
+    nbhs_free(const_cast<void*>(d.dev));
+    nbhs_free(d.f32);
+  }
+  weights_.clear();
+}
+
+size_t HipBackend::weight_bytes() const {
+  size_t s = 0;
+  for (auto& [key, d] : weights_) {
+    const size_t count = size_t(d.in) * size_t(d.rows);
+    s += count * (d.type == DType::F32 ? 4 : 2) + (d.f32 ? count * 4 : 0);
+  }
+  return s;
+}
+
+void HipBackend::matmul(const Tensor& w, const float* x, float* y, int64_t n) {
+  const Tensor* ws[] = {&w};
+  float* ys[] = {y};
+  matmul_multi(ws, x, ys, n);
+}
+
+void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x, std::span<float* const> ys,
+                              int64_t n) {
+  if (ws.empty() || ws.size() != ys.size())
+    throw Error("matmul: " + str(int64_t(ws.size())) + " weights for " + str(int64_t(ys.size())) + " outputs");
+  if (n <= 0) throw Error("matmul: n must be positive, got " + str(n));
+  for (const Tensor* t : ws)
+    if (!t) throw Error("matmul: null weight");
+  const int64_t in = ws[0]->ne[0];
+  for (const Tensor* t : ws)
+    if (t->ne[0] != in) {  // different input widths: one call per weight (backend.h:58-60)
+      for (size_t i = 0; i < ws.size(); ++i) matmul(*ws[i], x, ys[i], n);
+      return;
+    }
+  int64_t x_count;
+  if (overflow_mul(n, in, &x_count)) throw Error("matmul: n x width overflows");
+  check_range(x, x_count, "matmul", "x");
+  std::vector<DeviceWeight> dw;
+  dw.reserve(ws.size());
+  const auto xa = reinterpret_cast<uintptr_t>(x);
+  for (size_t i = 0; i < ws.size(); ++i) {
+    dw.push_back(device_weight(*ws[i], "matmul"));
+    int64_t y_count;
+    if (overflow_mul(n, dw.back().rows, &y_count)) throw Error("matmul: n x rows overflows");
+    check_range(ys[i], y_count, "matmul", "y");
+    const auto ya = reinterpret_cast<uintptr_t>(ys[i]);
+    if (ya < xa + uint64_t(x_count) * 4 && xa < ya + uint64_t(y_count) * 4)
+      throw Error("matmul: output " + str(int64_t(i)) + " overlaps the input");
+  }
+  if (n <= kGemvMaxRows) {
+    // One launch per (up to) eight weights: every weight row is read once for all n rows.
+    for (size_t b = 0; b < dw.size(); b += kGemvMaxWeights) {
+      const size_t cnt = std::min(dw.size() - b, kGemvMaxWeights);
+      int f16[kGemvMaxWeights];
+      const void* wp[kGemvMaxWeights];
+      float* yp[kGemvMaxWeights];
+      int64_t rows[kGemvMaxWeights];
+      for (size_t j = 0; j < cnt; ++j) {
+        f16[j] = dw[b + j].type == DType::F16;
+        wp[j] = dw[b + j].dev;
+        yp[j] = ys[b + j];
+        rows[j] = dw[b + j].rows;
+      }
+      check(nbhs_gemv_multi(int(cnt), f16, wp, yp, rows, in, x, n, stream_), "matmul (gemv)");
+    }
+    return;
+  }
+  if (!blas_) check(nbhs_blas_create(&blas_, stream_), "rocBLAS handle");
+  for (size_t i = 0; i < dw.size(); ++i)
+    check(nbhs_sgemm_xwt(blas_, x, weight_f32(dw[i]), ys[i], n, in, dw[i].rows), "matmul (sgemm)");
+}
+
+void HipBackend::add_bias(float* x, const Tensor& bias, int64_t n) {
+  if (n <= 0) throw Error("add_bias: n must be positive, got " + str(n));
+  if (bias.type != DType::F32) throw Error("add_bias: bias type " + str(int64_t(bias.type)) + " (need F32)");
+  const int64_t d = bias.ne[0];
+  int64_t count;
+  if (d <= 0 || overflow_mul(n, d, &count)) throw Error("add_bias: invalid bias width " + str(d));
+  check_range(x, count, "add_bias", "x");
+  Tensor row = bias;  // the bias is its first ne[0] floats
+  row.n_dims = 1;
+  row.ne = {d, 1, 1, 1};
+  const DeviceWeight b = device_weight(row, "add_bias");
+  check(nbhs_add_bias_f32(x, static_cast<const float*>(b.dev), d, n, stream_), "add_bias");
 }
 
 // The table holds, for every position `pos` and pair i, float(cos(theta)) and float(sin(theta)) with

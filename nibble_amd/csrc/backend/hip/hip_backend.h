@@ -2,8 +2,14 @@
 // HipBackend: nibble's Backend (backend.h) on one MI355X (gfx950), the attention path in hand-written HIP.
 // It replaces CpuBackend (reference src/backend/cpu/cpu_backend.h:18-91) for the ops the attention path uses:
 // reserve/alloc/free/read/copy, rope and attention, plus HIP-only extensions (host upload, the fused KV append
-// with RoPE, synthetic fill, events). The weight ops (embed, matmul, rmsnorm, add, add_bias, silu_mul) are not on
-// the GPU yet and throw nibble::Error; supports() is false for every weight type, so a model load fails early.
+// with RoPE, synthetic fill, events), and the QKV projection that feeds it: matmul / matmul_multi with F32 and F16
+// weights and add_bias. The other weight ops (embed, rmsnorm, add, silu_mul) are not on the GPU yet and throw
+// nibble::Error; supports() is false for every weight type, so a model load fails early.
+//
+// Weights: a Tensor's data is host memory (nibble maps the GGUF file), or memory from alloc(). Host weights are
+// copied to HBM on first use and kept, keyed by their data pointer, until release_weights() or destruction; the
+// caller must not change a weight's host bytes while its copy is kept (nibble's weights are read-only). Weights
+// inside a buffer from alloc() are used in place.
 //
 // Memory: every buffer handed out is HBM, zeroed, tracked; every op checks that the device ranges it is given lie
 // inside one tracked buffer before it launches anything, and throws Error otherwise (a bad range never reaches a
@@ -36,10 +42,15 @@ class HipBackend final : public Backend {
   void free(float* p) override;
   void read(float* host_dst, const float* src, int64_t n) override;  // waits for queued work
   void embed(const Tensor&, std::span<const int32_t>, float*) override { not_on_gpu("embed"); }
-  void matmul(const Tensor&, const float*, float*, int64_t) override { not_on_gpu("matmul"); }
+  // y[n, w.rows()] = x[n, w.ne[0]] . W^T for F32 and F16 weights (ref_ops.cpp:109-135): fp32 products and sums, in
+  // another order than the reference's left-to-right one (equal within float rounding).
+  void matmul(const Tensor& w, const float* x, float* y, int64_t n) override;
+  // ys[i] = matmul(*ws[i], x, n); weights of one input width share one launch on the decode route (n <= 16).
+  void matmul_multi(std::span<const Tensor* const> ws, const float* x, std::span<float* const> ys,
+                    int64_t n) override;
   void rmsnorm(const float*, const Tensor&, float*, int64_t, float) override { not_on_gpu("rmsnorm"); }
   void add(float*, const float*, int64_t) override { not_on_gpu("add"); }
-  void add_bias(float*, const Tensor&, int64_t) override { not_on_gpu("add_bias"); }
+  void add_bias(float* x, const Tensor& bias, int64_t n) override;  // bias F32 [d]; bit-exact
   void rope(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0, const RopeParams& p) override;
   void copy(float* dst, const float* src, int64_t count) override;  // memmove semantics
   void attention(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
@@ -78,6 +89,9 @@ class HipBackend final : public Backend {
                                    float* const* v_cache, const float* const* k_new, const float* const* v_new,
                                    float* const* out, const int64_t* pos0, int64_t n_heads, int64_t n_kv_heads,
                                    int64_t head_dim, const RopeParams& p);
+  // Drops every device copy of a host weight (after a caller changes or frees host weight memory).
+  void release_weights();
+  size_t weight_bytes() const;  // HBM held by weight copies
   void fill_normal(float* dst, int64_t count, uint64_t seed, float scale);
   void sync();
   nbhs_stream stream() const { return stream_; }
@@ -95,6 +109,14 @@ class HipBackend final : public Backend {
     float* dev = nullptr;  // [rows, head_dim/2] (cos, sin) float pairs
   };
 
+  // A weight's device form: the F32/F16 bytes, plus (F16 only) an fp32 widening for the GEMM route.
+  struct DeviceWeight {
+    DType type = DType::F32;
+    int64_t in = 0, rows = 0;
+    const void* dev = nullptr;
+    const void* key = nullptr;  // host data pointer of a kept copy; null for a weight used in place
+    float* f32 = nullptr;       // kept copies only: widening of an F16 weight for the GEMM route
+  };
   struct AppendRows {
     const float* k_new;
     const float* v_new;
@@ -113,6 +135,11 @@ class HipBackend final : public Backend {
   void check_range(const void* p, int64_t n_floats, const char* op, const char* arg) const;
   const float* rope_table(int64_t head_dim, int64_t rows_needed, const RopeParams& p, int64_t* rows_out);
   void ensure(float*& buf, size_t& cap_bytes, size_t need_bytes);
+  // The device form of w (copied to HBM on first use unless it lies in a buffer from alloc()).
+  DeviceWeight device_weight(const Tensor& w, const char* op);
+  // fp32 weights for the GEMM route: a kept F16 copy is widened once; an in-place F16 weight per call.
+  const float* weight_f32(const DeviceWeight& d);
+  bool in_buffer(const void* p, int64_t bytes) const;  // [p, p + bytes) inside one buffer from alloc()
 
   int device_ = 0;
   int cu_count_ = 0;
@@ -127,6 +154,10 @@ class HipBackend final : public Backend {
   size_t k16_bytes_ = 0, vt16_bytes_ = 0;
   float* copy_tmp_ = nullptr;  // bounce buffer for overlapping copies
   size_t copy_tmp_bytes_ = 0;
+  std::map<const void*, DeviceWeight> weights_;  // host weight data -> its device form
+  float* widen_tmp_ = nullptr;                  // fp32 widening of an in-place F16 weight for one GEMM
+  size_t widen_tmp_bytes_ = 0;
+  nbhs_blas blas_ = nullptr;
 };
 
 }  // namespace nibble::hip

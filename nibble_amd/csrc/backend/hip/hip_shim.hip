@@ -187,7 +187,10 @@ int nbhs_device_init(int device, int* cu_count) {
   return hipSuccess;
 }
 
-const char* nbhs_error_string(int code) { return hipGetErrorString(static_cast<hipError_t>(code)); }
+const char* nbhs_error_string(int code) {
+  if (code == NBHS_EBLAS) return "rocBLAS call failed";
+  return hipGetErrorString(static_cast<hipError_t>(code));
+}
 
 int nbhs_stream_create(nbhs_stream* out) {
   hipStream_t s = nullptr;

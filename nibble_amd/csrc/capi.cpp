@@ -3,6 +3,7 @@
 #include <exception>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "backend/hip/hip_backend.h"
 #include "nibble_hip.h"
@@ -42,6 +43,16 @@ int guarded(F&& f) {
     g_last_error = "unknown exception";
     return NBH_E_INTERNAL;
   }
+}
+
+nibble::Tensor tensor_of(const nbh_tensor* t) {
+  if (!t) throw nibble::Error("null tensor");
+  nibble::Tensor r;
+  r.type = static_cast<nibble::DType>(t->type);
+  r.n_dims = t->n_dims;
+  for (int i = 0; i < 4; ++i) r.ne[size_t(i)] = t->ne[i];
+  r.data = t->data;
+  return r;
 }
 
 HipBackend& B(nbh_backend* be) {
@@ -103,6 +114,31 @@ int nbh_backend_copy(nbh_backend* be, float* dst, const float* src, int64_t coun
 int nbh_backend_rope(nbh_backend* be, float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0,
                      float freq_base, int neox, const float* freq_factors) {
   return guarded([&] { B(be).rope(x, n, n_heads, head_dim, pos0, RopeParams{freq_base, neox != 0, freq_factors}); });
+}
+
+int nbh_backend_matmul(nbh_backend* be, const nbh_tensor* w, const float* x, float* y, int64_t n) {
+  return guarded([&] { B(be).matmul(tensor_of(w), x, y, n); });
+}
+
+int nbh_backend_matmul_multi(nbh_backend* be, int64_t n_w, const nbh_tensor* const* ws, const float* x,
+                             float* const* ys, int64_t n) {
+  return guarded([&] {
+    if (n_w <= 0 || !ws || !ys) throw nibble::Error("matmul_multi: need n_w > 0 weights and outputs");
+    std::vector<nibble::Tensor> t;
+    t.reserve(size_t(n_w));
+    for (int64_t i = 0; i < n_w; ++i) t.push_back(tensor_of(ws[i]));
+    std::vector<const nibble::Tensor*> tp;
+    for (auto& x_ : t) tp.push_back(&x_);
+    B(be).matmul_multi(std::span<const nibble::Tensor* const>(tp), x, std::span<float* const>(ys, size_t(n_w)), n);
+  });
+}
+
+int nbh_backend_add_bias(nbh_backend* be, float* x, const nbh_tensor* bias, int64_t n) {
+  return guarded([&] { B(be).add_bias(x, tensor_of(bias), n); });
+}
+
+int nbh_backend_release_weights(nbh_backend* be) {
+  return guarded([&] { B(be).release_weights(); });
 }
 
 int nbh_backend_attention(nbh_backend* be, const float* q, const float* k, const float* v, float* out, int64_t n,
@@ -168,6 +204,10 @@ int nbh_backend_internal_bytes(const nbh_backend* be, int64_t* out) {
 
 int nbh_backend_cu_count(const nbh_backend* be, int* out) {
   return guarded([&] { *out = B(be).cu_count(); });
+}
+
+int nbh_backend_weight_bytes(const nbh_backend* be, int64_t* out) {
+  return guarded([&] { *out = int64_t(B(be).weight_bytes()); });
 }
 
 int nbh_backend_fill_normal(nbh_backend* be, float* dst, int64_t count, uint64_t seed, float scale) {

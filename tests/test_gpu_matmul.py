@@ -1,0 +1,199 @@
+"""GPU parity of the QKV projection (Backend::matmul / matmul_multi / add_bias) against the CPU oracle.
+
+The reference's float matmul (ref_ops.cpp:109-135) accumulates each dot product left to right in float; the GPU
+sums the same float products in another order (lane partials and a wave tree on the gemv route, rocBLAS's blocking
+on the GEMM route). Both stay within the classical bound for float summation of the same terms, so the test bound
+is, per output element,
+    |gpu - exact| <= in * 2^-24 * sum_k |x_k w_k|      (exact = fp64 product of the same float inputs)
+    |gpu - ref|   <= 2 * in * 2^-24 * sum_k |x_k w_k|  (ref = the restated reference, bit-exact to it on the CPU)
+A dropped, repeated or misplaced term moves an element by about one term, |x_k w_k| ~ sum/in, several times the
+bound at these widths. add_bias is one float add per element and is compared bitwise, as are results that must be
+the same computation (matmul_multi against separate calls, device-resident against host weights).
+"""
+import numpy as np
+import pytest
+
+import nibble_amd
+import oracle
+from nibble_amd import configs
+from tests.gpu_util import Buffers, bits
+
+pytestmark = pytest.mark.gpu
+U = 2.0 ** -24
+
+
+def rand(rng, shape, dtype=np.float32, scale=1.0):
+    return (rng.standard_normal(shape) * scale).astype(dtype)
+
+
+def assert_matmul_close(got, w, x, what=""):
+    """got [n, out] against the exact product and the restated reference, within the summation bound."""
+    in_ = w.shape[1]
+    x2 = np.asarray(x, np.float32).reshape(-1, in_)
+    exact = oracle.matmul_f64(w, x2)
+    ref = oracle.matmul(w, x2)
+    absdot = np.abs(x2.astype(np.float64)) @ np.abs(np.asarray(w, np.float64)).T
+    bound = in_ * U * absdot + 1e-37
+    e_exact = np.abs(got.astype(np.float64) - exact)
+    e_ref = np.abs(got.astype(np.float64) - ref)
+    worst = float(np.max(e_exact / bound))
+    print(f"matmul {what}: max |gpu-exact|/bound = {worst:.3f}, max |gpu-ref| = {float(e_ref.max()):.3e}", flush=True)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    assert np.all(e_exact <= bound), f"{what}: {int(np.sum(e_exact > bound))} elements beyond the summation bound"
+    assert np.all(e_ref <= 2 * bound), f"{what}: {int(np.sum(e_ref > 2 * bound))} elements beyond 2x the bound vs ref"
+
+
+def gpu_matmul(be, w, x, n):
+    out_ = w.shape[0]
+    with Buffers(be) as B:
+        dx, dy = B.upload(x), B.alloc(n * out_)
+        be.matmul(w, dx, dy, n)
+        return be.download(dy, (n, out_))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16], ids=["f32", "f16"])
+@pytest.mark.parametrize("in_out", [(256, 96), (200, 40), (100, 33)], ids=["256x96", "200x40", "100x33-unaligned"])
+@pytest.mark.parametrize("n", [1, 2, 7, 16, 17, 64])
+def test_matmul_matches_reference(backend, dtype, in_out, n):
+    """Both routes (gemv for n <= 16, GEMM above) and both weight types, aligned (in % 8 == 0) and not."""
+    in_, out_ = in_out
+    rng = np.random.default_rng(1000 * n + in_ + out_)
+    w = rand(rng, (out_, in_), dtype, 0.5)
+    x = rand(rng, (n, in_))
+    got = gpu_matmul(backend, w, x, n)
+    assert_matmul_close(got, w, x, f"{np.dtype(dtype).name} {in_}x{out_} n={n}")
+    backend.release_weights()
+
+
+@pytest.mark.parametrize("shape", [configs.LLAMA32_1B, configs.QWEN25_05B, configs.TINYLLAMA_11B],
+                         ids=lambda s: s.name)
+@pytest.mark.parametrize("n", [1, 5, 16, 300])
+def test_qkv_projection_into_cache_rows(backend, shape, n):
+    """transformer.cpp:171-194: q, and K/V projected straight into cache rows pos0..pos0+n-1 (+ biases for qwen2),
+    F16 weights at the model's real widths. Cache rows outside the window keep their bits."""
+    E, Q, kvw = shape.n_embd, shape.n_heads * shape.head_dim, shape.n_kv_heads * shape.head_dim
+    pos0, n_ctx = 37, 400
+    rng = np.random.default_rng(n + E)
+    wq, wk, wv = (rand(rng, (r, E), np.float16, 0.05) for r in (Q, kvw, kvw))
+    bq, bk, bv = (rand(rng, (r,), np.float32, 0.1) for r in (Q, kvw, kvw))
+    x = rand(rng, (n, E))
+    kc0, vc0 = rand(rng, (n_ctx, kvw)), rand(rng, (n_ctx, kvw))
+    with Buffers(backend) as B:
+        dx, dq, dk, dv = B.upload(x), B.alloc(n * Q), B.upload(kc0), B.upload(vc0)
+        kc, vc = dk.at(pos0 * kvw), dv.at(pos0 * kvw)
+        backend.matmul_multi([wq, wk, wv], dx, [dq, kc, vc], n)
+        q_mm = backend.download(dq, (n, Q))
+        k_all, v_all = backend.download(dk, (n_ctx, kvw)), backend.download(dv, (n_ctx, kvw))
+        if shape.qkv_bias:
+            backend.add_bias(dq, bq, n)
+            backend.add_bias(kc, bk, n)
+            backend.add_bias(vc, bv, n)
+            q_b = backend.download(dq, (n, Q))
+            k_b, v_b = backend.download(dk, (n_ctx, kvw)), backend.download(dv, (n_ctx, kvw))
+        # matmul_multi equals separate matmul calls (backend.h:57), bit for bit
+        dq2, dk2, dv2 = B.alloc(n * Q), B.alloc(n * kvw), B.alloc(n * kvw)
+        for w, y in ((wq, dq2), (wk, dk2), (wv, dv2)):
+            backend.matmul(w, dx, y, n)
+        sep = [backend.download(dq2, (n, Q)), backend.download(dk2, (n, kvw)), backend.download(dv2, (n, kvw))]
+    win = slice(pos0, pos0 + n)
+    for got, w, name in ((q_mm, wq, "q"), (k_all[win], wk, "k"), (v_all[win], wv, "v")):
+        assert_matmul_close(got, w, x, f"{shape.name} n={n} {name}")
+    for a, b, name in ((q_mm, sep[0], "q"), (k_all[win], sep[1], "k"), (v_all[win], sep[2], "v")):
+        assert np.array_equal(bits(a), bits(b)), f"matmul_multi {name} differs from a separate matmul"
+    outside = np.ones(n_ctx, bool)
+    outside[win] = False
+    assert np.array_equal(bits(k_all[outside]), bits(kc0[outside])), "K cache rows outside the window changed"
+    assert np.array_equal(bits(v_all[outside]), bits(vc0[outside])), "V cache rows outside the window changed"
+    if shape.qkv_bias:
+        assert np.array_equal(bits(q_b), bits(oracle.add_bias(q_mm, bq))), "add_bias q not bit-exact"
+        assert np.array_equal(bits(k_b[win]), bits(oracle.add_bias(k_all[win], bk))), "add_bias k not bit-exact"
+        assert np.array_equal(bits(v_b[win]), bits(oracle.add_bias(v_all[win], bv))), "add_bias v not bit-exact"
+        assert np.array_equal(bits(k_b[outside]), bits(kc0[outside])), "add_bias touched rows outside the window"
+    backend.release_weights()
+
+
+@pytest.mark.parametrize("n", [3, 40])
+def test_device_resident_weights_match_host_weights(backend, n):
+    """Weights inside a buffer from alloc() are used in place (an F16 one widened per call on the GEMM route):
+    the same kernels on the same bytes as host weights, so the same bits."""
+    rng = np.random.default_rng(77 + n)
+    in_, out_ = 256, 72
+    w32 = rand(rng, (out_, in_), np.float32, 0.3)
+    w16 = rand(rng, (out_, in_), np.float16, 0.3)
+    x = rand(rng, (n, in_))
+    with Buffers(backend) as B:
+        dx = B.upload(x)
+        dw32 = B.upload(w32)
+        dw16 = B.upload(w16.view(np.float32))  # the halves' bytes, carried as floats
+        y = [B.alloc(n * out_) for _ in range(4)]
+        backend.matmul(w32, dx, y[0], n)
+        backend.matmul(dw32, dx, y[1], n, shape=w32.shape, dtype=nibble_amd.F32)
+        backend.matmul(w16, dx, y[2], n)
+        backend.matmul(dw16, dx, y[3], n, shape=w16.shape, dtype=nibble_amd.F16)
+        got = [backend.download(p, (n, out_)) for p in y]
+    assert np.array_equal(bits(got[0]), bits(got[1])), "F32: device-resident weight differs from host weight"
+    assert np.array_equal(bits(got[2]), bits(got[3])), "F16: device-resident weight differs from host weight"
+    assert_matmul_close(got[3], w16, x, f"device f16 n={n}")
+    backend.release_weights()
+
+
+def test_matmul_multi_mixed_widths_and_many_weights(backend):
+    """Weights of different input widths fall back to one call each (backend.h:58-60); more than eight weights of
+    one width take several launches."""
+    rng = np.random.default_rng(5)
+    n = 4
+    x = rand(rng, (n, 192))
+    ws = [rand(rng, (16 + i, 192), np.float16 if i % 2 else np.float32, 0.4) for i in range(11)]
+    narrow = rand(rng, (24, 96), np.float32, 0.4)
+    with Buffers(backend) as B:
+        dx = B.upload(x)
+        ys = [B.alloc(n * w.shape[0]) for w in ws]
+        backend.matmul_multi(ws, dx, ys, n)
+        got = [backend.download(y, (n, w.shape[0])) for y, w in zip(ys, ws)]
+        dn, dw0 = B.alloc(n * 24), B.alloc(n * ws[0].shape[0])
+        backend.matmul_multi([ws[0], narrow], dx, [dw0, dn], n)
+        got_n = backend.download(dn, (n, 24))
+        got_0 = backend.download(dw0, (n, ws[0].shape[0]))
+    for i, (g, w) in enumerate(zip(got, ws)):
+        assert_matmul_close(g, w, x, f"weight {i}")
+    assert np.array_equal(bits(got_0), bits(got[0]))
+    # the narrow weight reads x as [n, 96]: the first n*96 floats of the buffer
+    assert_matmul_close(got_n, narrow, x.reshape(-1)[: n * 96], "narrow")
+    backend.release_weights()
+
+
+def test_weight_copies_are_kept_and_released(backend):
+    rng = np.random.default_rng(9)
+    backend.release_weights()
+    assert backend.weight_bytes() == 0
+    w = rand(rng, (64, 128), np.float16)
+    x = rand(rng, (20, 128))
+    with Buffers(backend) as B:
+        dx, dy = B.upload(x), B.alloc(20 * 64)
+        backend.matmul(w, dx, dy, 1)
+        assert backend.weight_bytes() == w.nbytes  # one F16 copy
+        backend.matmul(w, dx, dy, 1)
+        assert backend.weight_bytes() == w.nbytes  # reused, not copied again
+        backend.matmul(w, dx, dy, 20)
+        assert backend.weight_bytes() == w.nbytes + 4 * w.size  # plus its fp32 widening for the GEMM route
+    backend.release_weights()
+    assert backend.weight_bytes() == 0
+
+
+def test_matmul_rejects_bad_arguments(backend):
+    rng = np.random.default_rng(3)
+    w = rand(rng, (32, 64))
+    with Buffers(backend) as B:
+        dx, dy = B.alloc(4 * 64), B.alloc(4 * 32)
+        with pytest.raises(nibble_amd.BackendError, match="not supported"):
+            q8 = nibble_amd.weight(dx, shape=(2, 64), dtype=8)  # Q8_0
+            backend.matmul_multi([q8], dx, [dy], 1)
+        with pytest.raises(nibble_amd.BackendError, match="overlaps the input"):
+            backend.matmul(w, dx, dx.at(64), 2)
+        with pytest.raises(nibble_amd.BackendError, match="not inside one buffer"):
+            backend.matmul(w, dx, dy, 5)  # y holds 4 rows
+        with pytest.raises(nibble_amd.BackendError, match="positive"):
+            backend.matmul(w, dx, dy, 0)
+        with pytest.raises(nibble_amd.BackendError, match="need F32"):
+            backend.add_bias(dy, nibble_amd.weight(np.zeros(32, np.float16)), 1)
+    backend.release_weights()
