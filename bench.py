@@ -190,6 +190,79 @@ def ragged_decode(be, steps, warmup):
                              "note": "the same steps as 16 single-sequence calls per layer"}}
 
 
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 (MFMA)
+
+
+def qkv_projection(be, steps, warmup, chunk=512, chunk_reps=3):
+    """The QKV projection feeding the attention path (transformer.cpp:171-194) at the Llama-3.2-1B shape: F16
+    weights wq [2048, 2048], wk and wv [512, 2048] per layer, 16 layers, one matmul_multi per layer writing q and the
+    new K/V cache rows. Decode: one token per step (the gemv route: weight bytes streamed once per layer);
+    prefill: chunks of `chunk` rows (the GEMM route: rocBLAS sgemm on the fp32 widening of each weight). Weights
+    start in host memory and are copied to HBM on the first (untimed) call, as a model's are."""
+    shape = configs.LLAMA32_1B
+    E, Q, kvw, NL = shape.n_embd, shape.n_heads * shape.head_dim, shape.n_kv_heads * shape.head_dim, 16
+    rng = np.random.default_rng(17)
+    ws = [[(rng.standard_normal((r, E), dtype=np.float32) * 0.02).astype(np.float16) for r in (Q, kvw, kvw)]
+          for _ in range(NL)]
+    rows = warmup + steps
+    x = be.alloc(max(rows, chunk) * E)
+    be.fill_normal(x, max(rows, chunk) * E, seed=41)
+    q = be.alloc(max(rows, chunk) * Q)
+    kc = [be.alloc(max(rows, chunk) * kvw) for _ in range(NL)]
+    vc = [be.alloc(max(rows, chunk) * kvw) for _ in range(NL)]
+
+    def step(s, n):
+        for l in range(NL):
+            be.matmul_multi(ws[l], x.at(s * E), [q, kc[l].at(s * kvw), vc[l].at(s * kvw)], n)
+
+    def timed(fn, reps):
+        e0, e1 = be.event(), be.event()
+        e0.record()
+        for r in range(reps):
+            fn(r)
+        e1.record()
+        return e0.elapsed_ms(e1)
+
+    for s in range(warmup):
+        step(s, 1)  # first call uploads the weights
+    be.sync()
+    dec_ms = timed(lambda r: step(warmup + r, 1), steps)
+    KernelTiming.enable(True, only=KernelTiming.GEMV)
+    timed(lambda r: step(warmup + r, 1), steps)
+    be.sync()
+    gemv_ms, gemv_n = KernelTiming.read(KernelTiming.GEMV)
+    KernelTiming.enable(False)
+    w_bytes = E * (Q + 2 * kvw) * 2
+    alg_bytes = w_bytes + E * 4 + (Q + 2 * kvw) * 4  # weights, the x row, the q/k/v rows
+    dec_gbs = NL * steps * alg_bytes / (dec_ms * 1e-3) / 1e9
+    gemv_us = gemv_ms / gemv_n * 1e3
+    gemv_gbs = alg_bytes / (gemv_us * 1e-6) / 1e9
+    for r in range(2):
+        step(0, chunk)  # first GEMM call widens the F16 weights once; rocBLAS loads its kernels
+    be.sync()
+    pre_ms = timed(lambda r: step(0, chunk), chunk_reps)
+    flops = 2 * chunk * E * (Q + 2 * kvw)
+    pre_tflops = NL * chunk_reps * flops / (pre_ms * 1e-3) / 1e12
+    for p in [x, q] + kc + vc:
+        be.free(p)
+    be.release_weights()
+    log(f"qkv projection: decode {dec_ms / steps * 1e3:.1f} us/step over {NL} layers -> {dec_gbs:.0f} GB/s; gemv "
+        f"kernel {gemv_us:.2f} us -> {gemv_gbs:.0f} GB/s ({gemv_gbs / HBM_PEAK_GBS:.1%}); prefill chunk {chunk}: "
+        f"{pre_ms / chunk_reps / NL * 1e3:.1f} us/layer -> {pre_tflops:.1f} TFLOP/s "
+        f"({pre_tflops / FP32_PEAK_TFLOPS:.1%} of fp32)")
+    return {"metric": "QKV projection (matmul_multi, F16 weights, llama-3.2-1b shape, 16 layers)",
+            "decode": {"value": round(dec_gbs, 1), "unit": "GB/s", "us_per_step": round(dec_ms / steps * 1e3, 2),
+                       "steps": steps, "roofline": {"bound": "hbm", "kernel": "gemv_kernel",
+                                                    "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS,
+                                                    "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+                                                    "avg_launch_us": round(gemv_us, 3), "launches": gemv_n,
+                                                    "algorithmic_bytes_per_launch": alg_bytes}},
+            "prefill_chunk": {"rows": chunk, "value": round(pre_tflops, 2), "unit": "TFLOP/s",
+                              "us_per_layer": round(pre_ms / chunk_reps / NL * 1e3, 2),
+                              "frac_of_fp32_peak": round(pre_tflops / FP32_PEAK_TFLOPS, 4),
+                              "note": "rocBLAS sgemm x3 per layer on fp32-widened weights (fp32 math)"}}
+
+
 COPY_CAL_BYTES = 1 << 30  # calibration copy for the HBM byte counters: 1 GiB read + 1 GiB written
 PROBE_DECODE_STEPS = 8
 
@@ -305,6 +378,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=16.0, help="budget of the CPU baseline samples")
     ap.add_argument("--cfg5-steps", type=int, default=4,
                     help="timed steps of the config-5 ragged batch (0: skip; 2 untimed steps precede them)")
+    ap.add_argument("--qkv-steps", type=int, default=32,
+                    help="timed decode steps of the QKV projection figure (0: skip it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc passes (child processes, about 10 s each) that measure HBM "
@@ -516,6 +591,8 @@ def main():
     }
     if args.cfg5_steps > 0:
         result["config5"] = ragged_decode(be, args.cfg5_steps, 2)
+    if args.qkv_steps > 0:
+        result["qkv_projection"] = qkv_projection(be, args.qkv_steps, 4)
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(be, shape, ck[0], cv[0], qd, ctx, q_pre0_host, args.cpu_seconds)

@@ -20,12 +20,13 @@ namespace {
 
 constexpr int kGemvMaxRows = NBHS_GEMV_MAX_ROWS;  // activation rows one gemv launch serves
 constexpr int kGemvMaxWeights = NBHS_GEMV_MAX_WEIGHTS;
+constexpr int kRowsPerWave = 4;  // weight rows one wave streams together (x chunks are read once for all four)
 
 struct GemvWeight {
   const void* w;  // [rows, in], F32 or F16
   float* y;       // [n, rows]
   int64_t rows;
-  int64_t row0;   // first stacked row of this weight
+  int64_t wave0;  // first wave (block) of this weight
   int f16;
 };
 struct GemvBatch {
@@ -33,88 +34,145 @@ struct GemvBatch {
   int n_w;
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
-// 8 weights from element k of a row, as floats.
+// Eight consecutive weights of a row as loaded: 16 bytes of halves or 32 bytes of floats.
 template <bool F16>
-__device__ __forceinline__ void load8(const void* row, int64_t k, float (&w)[8]) {
-  if constexpr (F16) {
-    typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-    const half8 h = *reinterpret_cast<const half8*>(static_cast<const _Float16*>(row) + k);
+struct Chunk;
+template <>
+struct Chunk<true> {
+  half8 h;
+  __device__ __forceinline__ void load(const void* row, int64_t k) {
+    h = *reinterpret_cast<const half8*>(static_cast<const _Float16*>(row) + k);
+  }
+  __device__ __forceinline__ float operator[](int e) const { return float(h[e]); }
+};
+template <>
+struct Chunk<false> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const void* row, int64_t k) {
+    a = *reinterpret_cast<const float4*>(static_cast<const float*>(row) + k);
+    b = *reinterpret_cast<const float4*>(static_cast<const float*>(row) + k + 4);
+  }
+  __device__ __forceinline__ float operator[](int e) const {
+    return e < 4 ? (e == 0 ? a.x : e == 1 ? a.y : e == 2 ? a.z : a.w) : (e == 4 ? b.x : e == 5 ? b.y : e == 6 ? b.z : b.w);
+  }
+};
+
+// Sum of each of CNT values over the 64 lanes of the wave, halving the values held per lane at each butterfly step
+// (a lane keeps the half its partner does not), so CNT - 1 + log2(64 / CNT) exchanges instead of 6 * CNT. Lane L
+// ends with the full sum of value L >> (6 - log2 CNT) in v[0].
+template <int CNT, int MASK, int M>
+__device__ __forceinline__ void wave_reduce_scatter(float (&v)[M], int lane) {
+  if constexpr (MASK >= 1) {
+    if constexpr (CNT > 1) {
+      constexpr int h = CNT / 2;
+      const bool up = (lane & MASK) != 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) w[e] = float(h[e]);
-  } else {
-    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(row) + k);
-    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(row) + k + 4);
-    w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w, w[4] = b.x, w[5] = b.y, w[6] = b.z, w[7] = b.w;
+      for (int j = 0; j < h; ++j) {
+        const float send = up ? v[j] : v[j + h];
+        const float keep = up ? v[j + h] : v[j];
+        v[j] = keep + __shfl_xor(send, MASK, 64);
+      }
+      wave_reduce_scatter<h, MASK / 2>(v, lane);
+    } else {
+      v[0] += __shfl_xor(v[0], MASK, 64);
+      wave_reduce_scatter<1, MASK / 2>(v, lane);
+    }
   }
 }
 
-template <bool F16>
-__device__ __forceinline__ float load1(const void* row, int64_t k) {
-  if constexpr (F16)
-    return float(static_cast<const _Float16*>(row)[k]);
-  else
-    return static_cast<const float*>(row)[k];
-}
+constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
 
-// One wave per stacked output row; lanes take 8-element chunks of the row (16-byte loads when `vec`: in % 8 == 0
-// and every weight and x 16-byte aligned, checked on the host).
-template <bool F16>
-__device__ __forceinline__ void gemv_row(const void* wrow, const float* __restrict__ x, int64_t in, int n, bool vec,
-                                         float (&acc)[kGemvMaxRows]) {
-  const int lane = threadIdx.x & 63;
-  if (vec) {
-    for (int64_t k = int64_t(lane) * 8; k < in; k += 64 * 8) {
-      float w[8];
-      load8<F16>(wrow, k, w);
+// One wave: rows r0..r0+3 of one weight against NT (>= n) activation rows. Every chunk the wave needs of its four
+// rows is loaded before any arithmetic (64 bytes per lane per row and pass), so a wave keeps 16 KB in flight.
+// `vec`: 16-byte loads (in % 8 == 0, weight and x 16-byte aligned, checked on the host); otherwise one element per
+// lane per step.
+template <bool F16, int NT>
+__device__ __forceinline__ void gemv_rows(const GemvWeight& d, const float* __restrict__ x, int64_t in, int n,
+                                          bool vec, int64_t r0) {
+  constexpr int R = kRowsPerWave;
+  const int lane = threadIdx.x;
+  const int nr = int(d.rows - r0 < R ? d.rows - r0 : R);
+  const void* row[R];
 #pragma unroll
-      for (int t = 0; t < kGemvMaxRows; ++t) {
-        if (t < n) {
-          const float4 a = *reinterpret_cast<const float4*>(x + t * in + k);
-          const float4 b = *reinterpret_cast<const float4*>(x + t * in + k + 4);
-          acc[t] += a.x * w[0] + a.y * w[1] + a.z * w[2] + a.w * w[3] + b.x * w[4] + b.y * w[5] + b.z * w[6] +
-                    b.w * w[7];
+  for (int r = 0; r < R; ++r) {  // rows past the weight's end re-read its last row; their sums are dropped
+    const int64_t rr = r0 + (r < nr ? r : nr - 1);
+    row[r] = F16 ? static_cast<const void*>(static_cast<const _Float16*>(d.w) + rr * in)
+                 : static_cast<const void*>(static_cast<const float*>(d.w) + rr * in);
+  }
+  float acc[R * NT];
+#pragma unroll
+  for (int j = 0; j < R * NT; ++j) acc[j] = 0.f;
+  if (vec) {
+    constexpr int U = F16 ? 4 : 2;  // chunks per lane per pass: 64 bytes of each row
+    for (int64_t k0 = int64_t(lane) * 8; k0 < in; k0 += 64 * 8 * U) {
+      Chunk<F16> w[R][U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t k = k0 + u * 512;
+        if (k < in) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) w[r][u].load(row[r], k);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t k = k0 + u * 512;
+        if (k < in) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            if (t < n) {
+              const float4 xa = *reinterpret_cast<const float4*>(x + t * in + k);
+              const float4 xb = *reinterpret_cast<const float4*>(x + t * in + k + 4);
+#pragma unroll
+              for (int r = 0; r < R; ++r)
+                acc[r * NT + t] += xa.x * w[r][u][0] + xa.y * w[r][u][1] + xa.z * w[r][u][2] + xa.w * w[r][u][3] +
+                                   xb.x * w[r][u][4] + xb.y * w[r][u][5] + xb.z * w[r][u][6] + xb.w * w[r][u][7];
+            }
+          }
         }
       }
     }
   } else {
     for (int64_t k = lane; k < in; k += 64) {
-      const float w = load1<F16>(wrow, k);
+      float w[R];
 #pragma unroll
-      for (int t = 0; t < kGemvMaxRows; ++t)
-        if (t < n) acc[t] += x[t * in + k] * w;
+      for (int r = 0; r < R; ++r)
+        w[r] = F16 ? float(static_cast<const _Float16*>(row[r])[k]) : static_cast<const float*>(row[r])[k];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if (t < n) {
+          const float xv = x[t * in + k];
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[r * NT + t] += xv * w[r];
+        }
+      }
     }
+  }
+  constexpr int M = R * NT;
+  static_assert(M <= 64 && (M & (M - 1)) == 0, "R * NT must be a power of two up to 64");
+  wave_reduce_scatter<M, 32>(acc, lane);
+  constexpr int shift = 6 - ilog2(M);
+  if ((lane & ((1 << shift) - 1)) == 0) {
+    const int idx = lane >> shift, r = idx / NT, t = idx % NT;
+    if (r < nr && t < n) d.y[int64_t(t) * d.rows + r0 + r] = acc[0];
   }
 }
 
-__global__ __launch_bounds__(256) void gemv_kernel(GemvBatch b, const float* __restrict__ x, int64_t in, int n,
-                                                   bool vec) {
-  const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);  // stacked output row of this wave
+// One 64-thread block (one wave) per four stacked weight rows.
+template <int NT>
+__global__ __launch_bounds__(64) void gemv_kernel(GemvBatch b, const float* __restrict__ x, int64_t in, int n,
+                                                  bool vec) {
   int i = 0;
   for (int j = 1; j < b.n_w; ++j)
-    if (r >= b.w[j].row0) i = j;
+    if (int64_t(blockIdx.x) >= b.w[j].wave0) i = j;
   const GemvWeight& d = b.w[i];
-  const int64_t rr = r - d.row0;
-  if (rr >= d.rows) return;  // past the last weight's rows: the whole wave leaves
-  float acc[kGemvMaxRows];
-#pragma unroll
-  for (int t = 0; t < kGemvMaxRows; ++t) acc[t] = 0.f;
+  const int64_t r0 = (int64_t(blockIdx.x) - d.wave0) * kRowsPerWave;
   if (d.f16)
-    gemv_row<true>(static_cast<const _Float16*>(d.w) + rr * in, x, in, n, vec, acc);
+    gemv_rows<true, NT>(d, x, in, n, vec, r0);
   else
-    gemv_row<false>(static_cast<const float*>(d.w) + rr * in, x, in, n, vec, acc);
-#pragma unroll
-  for (int t = 0; t < kGemvMaxRows; ++t) {
-    if (t < n) {
-      const float s = wave_sum(acc[t]);
-      if ((threadIdx.x & 63) == 0) d.y[t * d.rows + rr] = s;
-    }
-  }
+    gemv_rows<false, NT>(d, x, in, n, vec, r0);
 }
 
 __global__ __launch_bounds__(256) void f16_to_f32_kernel(const _Float16* __restrict__ src, float* __restrict__ dst,
@@ -144,19 +202,21 @@ int nbhs_gemv_multi(int n_w, const int* f16, const void* const* w, float* const*
       n > kGemvMaxRows)
     return NBHS_EINVAL;
   GemvBatch b{};
-  int64_t total = 0;
+  int64_t waves = 0;
   bool vec = in % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
   for (int i = 0; i < n_w; ++i) {
     if (!w[i] || !y[i] || rows[i] <= 0) return NBHS_EINVAL;
     vec = vec && reinterpret_cast<uintptr_t>(w[i]) % 16 == 0;
-    b.w[i] = GemvWeight{w[i], y[i], rows[i], total, f16[i] ? 1 : 0};
-    total += rows[i];
+    b.w[i] = GemvWeight{w[i], y[i], rows[i], waves, f16[i] ? 1 : 0};
+    waves += (rows[i] + kRowsPerWave - 1) / kRowsPerWave;
   }
   b.n_w = n_w;
-  const int64_t blocks = (total + 3) / 4;
-  if (blocks >= (int64_t(1) << 31)) return NBHS_EINVAL;
-  return nbhs_timing::launch(NBHS_K_GEMV, gemv_kernel, dim3(unsigned(blocks)), dim3(256),
-                             reinterpret_cast<hipStream_t>(stream), b, x, in, int(n), vec);
+  if (waves >= (int64_t(1) << 31)) return NBHS_EINVAL;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid{unsigned(waves), 1, 1}, block{64, 1, 1};
+  if (n == 1) return nbhs_timing::launch(NBHS_K_GEMV, gemv_kernel<1>, grid, block, s, b, x, in, int(n), vec);
+  if (n <= 4) return nbhs_timing::launch(NBHS_K_GEMV, gemv_kernel<4>, grid, block, s, b, x, in, int(n), vec);
+  return nbhs_timing::launch(NBHS_K_GEMV, gemv_kernel<16>, grid, block, s, b, x, in, int(n), vec);
 }
 
 int nbhs_f16_to_f32(const void* src, float* dst, int64_t count, nbhs_stream stream) {
