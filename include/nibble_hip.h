@@ -54,8 +54,8 @@ int nbh_backend_create(int device, nbh_backend** out);
 /* Frees every buffer still allocated. Replaces CpuBackend::~CpuBackend (cpu_backend.cpp:70-72). */
 void nbh_backend_destroy(nbh_backend* be);
 
-/* Backend::supports (backend.h:41): whether weight type `dtype` (ggml id) can run matmul/embed. Always 0 for
- * now: embed is not on the GPU yet, so a whole model cannot bind (matmul itself takes F32 and F16). */
+/* Backend::supports (backend.h:41): whether weight type `dtype` (ggml id) can run matmul/embed: 1 for F32 (0) and
+ * F16 (1), 0 for the quantized types. */
 int nbh_backend_supports(const nbh_backend* be, uint32_t dtype, int* out);
 
 /* Backend::reserve (backend.h:45; ReserveParams backend.h:24-26). */
@@ -135,6 +135,25 @@ int nbh_backend_matmul_multi(nbh_backend* be, int64_t n_w, const nbh_tensor* con
 /* Backend::add_bias (backend.h:63, ref_ops.cpp:154-160): each of the n rows of x [n, bias.ne[0]] += bias (F32);
  * bit-exact. */
 int nbh_backend_add_bias(nbh_backend* be, float* x, const nbh_tensor* bias, int64_t n);
+
+/* Backend::embed (backend.h:55, ref_ops.cpp:80-99): out[t, :] = row ids[t] of table (F32 copied, F16 widened
+ * exactly), t < n_ids. ids is HOST memory; an id outside [0, rows) fails with NBH_E_INPUT before any work. */
+int nbh_backend_embed(nbh_backend* be, const nbh_tensor* table, const int32_t* ids, int64_t n_ids, float* out);
+
+/* Backend::rmsnorm (backend.h:61, ref_ops.cpp:137-148): y[t] = x[t] * w / sqrt(mean(x[t]^2) + eps) for n rows of
+ * weight.ne[0] floats (weight F32), the sum and scale in double as the reference computes them. */
+int nbh_backend_rmsnorm(nbh_backend* be, const float* x, const nbh_tensor* weight, float* y, int64_t n, float eps);
+
+/* Backend::add (backend.h:62, ref_ops.cpp:151-153): x[i] += y[i]; bit-exact. */
+int nbh_backend_add(nbh_backend* be, float* x, const float* y, int64_t count);
+
+/* Backend::silu_mul (backend.h:70, ref_ops.cpp:217-222): gate[i] = g / (1 + exp(-g)) * up[i]. */
+int nbh_backend_silu_mul(nbh_backend* be, float* gate, const float* up, int64_t count);
+
+/* Attention precision switch (no reference counterpart: the reference computes attention in float). on = 0
+ * (default): calls of more than 16 rows with head_dim 64/128 run rows at positions >= 256 on the fp16-operand MFMA
+ * kernel. on != 0: every row takes the fp32 split-context kernel, as decode does, at a much lower prefill rate. */
+int nbh_backend_set_attention_fp32(nbh_backend* be, int on);
 
 /* Drops every device copy of a host weight; no reference counterpart (CpuBackend reads weights in place). */
 int nbh_backend_release_weights(nbh_backend* be);

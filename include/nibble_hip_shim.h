@@ -167,6 +167,18 @@ int nbhs_blas_destroy(nbhs_blas h);
  * product as nbhs_gemv_multi, for any n. */
 int nbhs_sgemm_xwt(nbhs_blas h, const float* x, const float* w, float* y, int64_t n, int64_t in, int64_t out);
 
+/* ---- the other per-token ops (Backend::embed / rmsnorm / add / silu_mul, backend.h:55-70) ---- */
+
+/* out[t, :] = row ids[t] of table [rows, d] (F32, or F16 widened exactly); ids in device memory, already checked
+ * against the row count by the caller (ref_ops.cpp:80-99). */
+int nbhs_embed(int f16, const void* table, const int32_t* ids, int64_t n, int64_t d, float* out, nbhs_stream s);
+/* ref_ops.cpp:137-148: y[t] = float(x[t] * scale * w) with scale = 1 / sqrt(sum(x^2) / d + eps) in double. */
+int nbhs_rmsnorm_f32(const float* x, const float* w, float* y, int64_t n, int64_t d, float eps, nbhs_stream s);
+/* x[i] += y[i] (ref_ops.cpp:151-153). */
+int nbhs_add_f32(float* x, const float* y, int64_t count, nbhs_stream s);
+/* gate[i] = g / (1 + exp(-g)) * up[i] (ref_ops.cpp:217-222). */
+int nbhs_silu_mul_f32(float* gate, const float* up, int64_t count, nbhs_stream s);
+
 /* ---- per-kernel timing (measurement only) ----
  * While enabled for a kernel, its launcher launches it with a HIP event pair (hipExtLaunchKernel) stamped from the
  * dispatch itself, so the average device duration of that kernel can be read back live (bench.py's roofline
@@ -183,7 +195,9 @@ enum nbhs_kernel_id {
   NBHS_K_GEMV = 7,
   NBHS_K_CONVERT = 8,
   NBHS_K_ADD_BIAS = 9,
-  NBHS_K_COUNT = 10
+  NBHS_K_RMSNORM = 10,
+  NBHS_K_ELEMENTWISE = 11, /* embed, add, silu_mul */
+  NBHS_K_COUNT = 12
 };
 int nbhs_kernel_timing_enable(int on); /* on != 0: time every kernel; 0: none (clears what was recorded) */
 int nbhs_kernel_timing_select(uint32_t kernel_mask); /* time the kernels whose bit (1 << id) is set; clears */

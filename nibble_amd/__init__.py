@@ -54,6 +54,11 @@ _SIGNATURES = {
     "nbh_backend_matmul_multi": (c_int, [c_void_p, _I, c_void_p, c_void_p, c_void_p, _I]),
     "nbh_backend_add_bias": (c_int, [c_void_p, c_void_p, POINTER(NbhTensor), _I]),
     "nbh_backend_release_weights": (c_int, [c_void_p]),
+    "nbh_backend_set_attention_fp32": (c_int, [c_void_p, c_int]),
+    "nbh_backend_embed": (c_int, [c_void_p, POINTER(NbhTensor), c_void_p, _I, c_void_p]),
+    "nbh_backend_rmsnorm": (c_int, [c_void_p, c_void_p, POINTER(NbhTensor), c_void_p, _I, c_float]),
+    "nbh_backend_add": (c_int, [c_void_p, c_void_p, c_void_p, _I]),
+    "nbh_backend_silu_mul": (c_int, [c_void_p, c_void_p, c_void_p, _I]),
     "nbh_backend_weight_bytes": (c_int, [c_void_p, POINTER(c_int64)]),
     "nbh_backend_reserve_attention": (c_int, [c_void_p, _I, _I]),
     "nbh_backend_reserve_rope": (c_int, [c_void_p, _I, c_float, c_int, c_void_p]),
@@ -245,6 +250,26 @@ class HipBackend:
         t = bias if isinstance(bias, NbhTensor) else self._tensor(np.ascontiguousarray(bias, dtype=np.float32))
         _check(lib().nbh_backend_add_bias(self._h, c_void_p(int(x)), byref(t), n))
 
+    def embed(self, table, ids, out):
+        """out[t, :] = row ids[t] of table (a float32/float16 host array or an NbhTensor); ids host int32."""
+        t = table if isinstance(table, NbhTensor) else self._tensor(table)
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        _check(lib().nbh_backend_embed(self._h, byref(t), _host_ptr(ids), ids.size, c_void_p(int(out))))
+
+    def rmsnorm(self, x, weight, y, n: int, eps: float):
+        t = weight if isinstance(weight, NbhTensor) else self._tensor(np.ascontiguousarray(weight, dtype=np.float32))
+        _check(lib().nbh_backend_rmsnorm(self._h, c_void_p(int(x)), byref(t), c_void_p(int(y)), n, eps))
+
+    def add(self, x, y, count: int):
+        _check(lib().nbh_backend_add(self._h, c_void_p(int(x)), c_void_p(int(y)), count))
+
+    def silu_mul(self, gate, up, count: int):
+        _check(lib().nbh_backend_silu_mul(self._h, c_void_p(int(gate)), c_void_p(int(up)), count))
+
+    def set_attention_fp32(self, on: bool):
+        """Every attention row on the fp32 kernels (on) or the default fp16-operand MFMA prefill (off)."""
+        _check(lib().nbh_backend_set_attention_fp32(self._h, int(bool(on))))
+
     def release_weights(self):
         _check(lib().nbh_backend_release_weights(self._h))
         self._kept.clear()
@@ -319,7 +344,8 @@ class KernelTiming:
     """Live per-kernel device durations from the shim's launch bracketing (nbhs_kernel_timing_*,
     include/nibble_hip_shim.h). Used by the benchmark for roofline figures."""
 
-    ROPE, APPEND_ROPE, DECODE_PARTIAL, DECODE_COMBINE, GENERIC, STAGE_KV, PREFILL_MFMA, GEMV, CONVERT, ADD_BIAS = range(10)
+    (ROPE, APPEND_ROPE, DECODE_PARTIAL, DECODE_COMBINE, GENERIC, STAGE_KV, PREFILL_MFMA, GEMV, CONVERT, ADD_BIAS, RMSNORM,
+     ELEMENTWISE) = range(12)
 
     @staticmethod
     def enable(on: bool = True, only: int | None = None):

@@ -40,16 +40,13 @@ HipBackend::~HipBackend() {
   nbhs_free(vt16_);
   nbhs_free(copy_tmp_);
   nbhs_free(widen_tmp_);
+  nbhs_free(ids_buf_);
   for (auto& [key, d] : weights_) {
     nbhs_free(const_cast<void*>(d.dev));
     nbhs_free(d.f32);
   }
   if (blas_) nbhs_blas_destroy(blas_);
   if (stream_) nbhs_stream_destroy(stream_);
-}
-
-void HipBackend::not_on_gpu(const char* op) {
-  throw Error(std::string("HipBackend: ") + op + " is not implemented on the GPU backend (attention path only)");
 }
 
 void HipBackend::check(int code, const char* what) const {
@@ -84,7 +81,7 @@ void HipBackend::ensure(float*& buf, size_t& cap_bytes, size_t need_bytes) {
 }
 
 size_t HipBackend::internal_bytes() const {
-  size_t s = decode_ws_bytes_ + k16_bytes_ + vt16_bytes_ + copy_tmp_bytes_ + widen_tmp_bytes_;
+  size_t s = decode_ws_bytes_ + k16_bytes_ + vt16_bytes_ + copy_tmp_bytes_ + widen_tmp_bytes_ + ids_buf_bytes_;
   for (auto& t : rope_tables_) s += size_t(t.rows) * size_t(t.head_dim) * sizeof(float);
   return s;
 }
@@ -327,6 +324,51 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
   if (!blas_) check(nbhs_blas_create(&blas_, stream_), "rocBLAS handle");
   for (size_t i = 0; i < dw.size(); ++i)
     check(nbhs_sgemm_xwt(blas_, x, weight_f32(dw[i]), ys[i], n, in, dw[i].rows), "matmul (sgemm)");
+}
+
+void HipBackend::embed(const Tensor& table, std::span<const int32_t> ids, float* out) {
+  if (ids.empty()) throw Error("embed: no token ids");
+  const int64_t n = int64_t(ids.size()), d = table.ne[0], rows = table.rows();
+  for (const int32_t id : ids)
+    if (id < 0 || id >= rows)
+      throw Error("embed: token id " + std::to_string(id) + " out of range (n_vocab " + std::to_string(rows) + ")");
+  int64_t count;
+  if (d <= 0 || overflow_mul(n, d, &count)) throw Error("embed: invalid table width " + str(d));
+  check_range(out, count, "embed", "out");
+  const DeviceWeight w = device_weight(table, "embed");
+  ensure(ids_buf_, ids_buf_bytes_, size_t(n) * sizeof(int32_t));
+  check(nbhs_memcpy_h2d(ids_buf_, ids.data(), size_t(n) * sizeof(int32_t), stream_), "embed ids upload");
+  check(nbhs_embed(w.type == DType::F16, w.dev, reinterpret_cast<const int32_t*>(ids_buf_), n, d, out, stream_),
+        "embed");
+}
+
+void HipBackend::rmsnorm(const float* x, const Tensor& weight, float* y, int64_t n, float eps) {
+  if (n <= 0) throw Error("rmsnorm: n must be positive, got " + str(n));
+  if (weight.type != DType::F32) throw Error("rmsnorm: weight type " + str(int64_t(weight.type)) + " (need F32)");
+  const int64_t d = weight.ne[0];
+  int64_t count;
+  if (d <= 0 || overflow_mul(n, d, &count)) throw Error("rmsnorm: invalid weight width " + str(d));
+  check_range(x, count, "rmsnorm", "x");
+  check_range(y, count, "rmsnorm", "y");
+  Tensor row = weight;
+  row.n_dims = 1;
+  row.ne = {d, 1, 1, 1};
+  const DeviceWeight w = device_weight(row, "rmsnorm");
+  check(nbhs_rmsnorm_f32(x, static_cast<const float*>(w.dev), y, n, d, eps, stream_), "rmsnorm");
+}
+
+void HipBackend::add(float* x, const float* y, int64_t count) {
+  if (count <= 0) throw Error("add: count must be positive, got " + str(count));
+  check_range(x, count, "add", "x");
+  check_range(y, count, "add", "y");
+  check(nbhs_add_f32(x, y, count, stream_), "add");
+}
+
+void HipBackend::silu_mul(float* gate, const float* up, int64_t count) {
+  if (count <= 0) throw Error("silu_mul: count must be positive, got " + str(count));
+  check_range(gate, count, "silu_mul", "gate");
+  check_range(up, count, "silu_mul", "up");
+  check(nbhs_silu_mul_f32(gate, up, count, stream_), "silu_mul");
 }
 
 void HipBackend::add_bias(float* x, const Tensor& bias, int64_t n) {
@@ -596,7 +638,7 @@ void HipBackend::run_attention(const float* q, const float* k, const float* v, f
     decode_rows(q, out, n, pos0);
     return;
   }
-  const int64_t split = std::clamp<int64_t>(kFp32PrefixRows - pos0, 0, n);
+  const int64_t split = attention_fp32_ ? n : std::clamp<int64_t>(kFp32PrefixRows - pos0, 0, n);
   const int64_t rows = pos0 + n;
   const int64_t halves = nbhs_prefill_staging_halves(rows, n_kv_heads, head_dim);
   if (split < n) {

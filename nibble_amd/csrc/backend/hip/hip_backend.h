@@ -2,9 +2,9 @@
 // HipBackend: nibble's Backend (backend.h) on one MI355X (gfx950), the attention path in hand-written HIP.
 // It replaces CpuBackend (reference src/backend/cpu/cpu_backend.h:18-91) for the ops the attention path uses:
 // reserve/alloc/free/read/copy, rope and attention, plus HIP-only extensions (host upload, the fused KV append
-// with RoPE, synthetic fill, events), and the QKV projection that feeds it: matmul / matmul_multi with F32 and F16
-// weights and add_bias. The other weight ops (embed, rmsnorm, add, silu_mul) are not on the GPU yet and throw
-// nibble::Error; supports() is false for every weight type, so a model load fails early.
+// with RoPE, synthetic fill, events), the QKV projection that feeds it (matmul / matmul_multi and add_bias), and the
+// remaining per-token ops (embed, rmsnorm, add, silu_mul), so a whole forward stays on the GPU. Weights may be F32 or
+// F16 (supports() is true for those two); quantized types are not on the GPU and are rejected up front.
 //
 // Weights: a Tensor's data is host memory (nibble maps the GGUF file), or memory from alloc(). Host weights are
 // copied to HBM on first use and kept, keyed by their data pointer, until release_weights() or destruction; the
@@ -34,28 +34,31 @@ class HipBackend final : public Backend {
   HipBackend(const HipBackend&) = delete;
   HipBackend& operator=(const HipBackend&) = delete;
 
-  bool supports(DType) const override { return false; }
+  bool supports(DType t) const override { return t == DType::F32 || t == DType::F16; }
   // Sizes the decode workspace for n_heads query heads at up to n_ctx positions. Shapes it cannot know from
   // ReserveParams (KV heads, head_dim) are sized by reserve_attention() or on first use.
   void reserve(const ReserveParams&) override;
   float* alloc(int64_t n_floats) override;  // HBM, 64-byte granular, zeroed
   void free(float* p) override;
   void read(float* host_dst, const float* src, int64_t n) override;  // waits for queued work
-  void embed(const Tensor&, std::span<const int32_t>, float*) override { not_on_gpu("embed"); }
+  // out[t, :] = row ids[t] of the table (F32 copied, F16 widened; ref_ops.cpp:80-99); ids are host memory and are
+  // checked against the row count before anything is queued (Error, as the reference throws).
+  void embed(const Tensor& table, std::span<const int32_t> ids, float* out) override;
   // y[n, w.rows()] = x[n, w.ne[0]] . W^T for F32 and F16 weights (ref_ops.cpp:109-135): fp32 products and sums, in
   // another order than the reference's left-to-right one (equal within float rounding).
   void matmul(const Tensor& w, const float* x, float* y, int64_t n) override;
   // ys[i] = matmul(*ws[i], x, n); weights of one input width share one launch on the decode route (n <= 16).
   void matmul_multi(std::span<const Tensor* const> ws, const float* x, std::span<float* const> ys,
                     int64_t n) override;
-  void rmsnorm(const float*, const Tensor&, float*, int64_t, float) override { not_on_gpu("rmsnorm"); }
-  void add(float*, const float*, int64_t) override { not_on_gpu("add"); }
+  // ref_ops.cpp:137-148 with the sum of squares and the scale in double (weight F32 [d]).
+  void rmsnorm(const float* x, const Tensor& weight, float* y, int64_t n, float eps) override;
+  void add(float* x, const float* y, int64_t count) override;  // bit-exact
   void add_bias(float* x, const Tensor& bias, int64_t n) override;  // bias F32 [d]; bit-exact
   void rope(float* x, int64_t n, int64_t n_heads, int64_t head_dim, int64_t pos0, const RopeParams& p) override;
   void copy(float* dst, const float* src, int64_t count) override;  // memmove semantics
   void attention(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
                  int64_t n_heads, int64_t n_kv_heads, int64_t head_dim) override;
-  void silu_mul(float*, const float*, int64_t) override { not_on_gpu("silu_mul"); }
+  void silu_mul(float* gate, const float* up, int64_t count) override;  // within a few ulp (device expf)
 
   // ---- HIP-only extensions ----
   // Host -> device upload of n floats (the reference needs none: its buffers are host memory).
@@ -89,6 +92,12 @@ class HipBackend final : public Backend {
                                    float* const* v_cache, const float* const* k_new, const float* const* v_new,
                                    float* const* out, const int64_t* pos0, int64_t n_heads, int64_t n_kv_heads,
                                    int64_t head_dim, const RopeParams& p);
+  // Attention precision. By default calls of more than 16 rows with head_dim 64/128 run their rows at positions
+  // >= 256 on the fp16-operand MFMA kernel (fp32 accumulation and softmax). With fp32 set, every row takes the fp32
+  // split-context kernel, as decode does: the reference's float arithmetic throughout, at a much lower prefill
+  // rate. For models whose attention scores are large enough that fp16 rounding of Q and K moves the softmax.
+  void set_attention_fp32(bool on) { attention_fp32_ = on; }
+  bool attention_fp32() const { return attention_fp32_; }
   // Drops every device copy of a host weight (after a caller changes or frees host weight memory).
   void release_weights();
   size_t weight_bytes() const;  // HBM held by weight copies
@@ -121,7 +130,6 @@ class HipBackend final : public Backend {
     const float* k_new;
     const float* v_new;
   };
-  [[noreturn]] static void not_on_gpu(const char* op);
   void check_attention_args(const float* q, const float* k, const float* v, const float* out, int64_t n,
                             int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const char* op) const;
   void run_attention(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
@@ -158,6 +166,9 @@ class HipBackend final : public Backend {
   float* widen_tmp_ = nullptr;                  // fp32 widening of an in-place F16 weight for one GEMM
   size_t widen_tmp_bytes_ = 0;
   nbhs_blas blas_ = nullptr;
+  bool attention_fp32_ = false;
+  float* ids_buf_ = nullptr;  // token ids of the last embed, on the device
+  size_t ids_buf_bytes_ = 0;
 };
 
 }  // namespace nibble::hip

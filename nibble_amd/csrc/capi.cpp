@@ -137,6 +137,29 @@ int nbh_backend_add_bias(nbh_backend* be, float* x, const nbh_tensor* bias, int6
   return guarded([&] { B(be).add_bias(x, tensor_of(bias), n); });
 }
 
+int nbh_backend_embed(nbh_backend* be, const nbh_tensor* table, const int32_t* ids, int64_t n_ids, float* out) {
+  return guarded([&] {
+    if (n_ids <= 0 || !ids) throw nibble::Error("embed: need n_ids > 0 host token ids");
+    B(be).embed(tensor_of(table), std::span<const int32_t>(ids, size_t(n_ids)), out);
+  });
+}
+
+int nbh_backend_rmsnorm(nbh_backend* be, const float* x, const nbh_tensor* weight, float* y, int64_t n, float eps) {
+  return guarded([&] { B(be).rmsnorm(x, tensor_of(weight), y, n, eps); });
+}
+
+int nbh_backend_add(nbh_backend* be, float* x, const float* y, int64_t count) {
+  return guarded([&] { B(be).add(x, y, count); });
+}
+
+int nbh_backend_silu_mul(nbh_backend* be, float* gate, const float* up, int64_t count) {
+  return guarded([&] { B(be).silu_mul(gate, up, count); });
+}
+
+int nbh_backend_set_attention_fp32(nbh_backend* be, int on) {
+  return guarded([&] { B(be).set_attention_fp32(on != 0); });
+}
+
 int nbh_backend_release_weights(nbh_backend* be) {
   return guarded([&] { B(be).release_weights(); });
 }

@@ -60,6 +60,13 @@ def _load():
         lib.orc_matmul.restype = c_int
         lib.orc_add_bias.argtypes = [_F, _F, _I, _I]
         lib.orc_add_bias.restype = None
+        lib.orc_embed.argtypes = [c_int, c_void_p, _I, _I, c_void_p, _I, _F]
+        lib.orc_rmsnorm.argtypes = [_F, _F, _F, _I, _I, c_float]
+        lib.orc_rmsnorm.restype = None
+        lib.orc_add.argtypes = [_F, _F, _I]
+        lib.orc_add.restype = None
+        lib.orc_silu_mul.argtypes = [_F, _F, _I]
+        lib.orc_silu_mul.restype = None
         _lib = lib
     return _lib
 
@@ -85,6 +92,12 @@ def _load_ref():
             lib.ref_backend_rope.argtypes = [c_void_p, _F, _I, _I, _I, _I, c_float, c_int, _F]
             lib.ref_matmul_scalar.argtypes = [c_int, c_void_p, _I, _I, _F, _F, _I]
             lib.ref_add_bias.argtypes = [_F, _F, _I, _I]
+            lib.ref_embed.argtypes = [c_int, c_void_p, _I, _I, c_void_p, _I, _F]
+            lib.ref_rmsnorm.argtypes = [_F, _F, _F, _I, _I, c_float]
+            lib.ref_rmsnorm_simd.argtypes = [_F, _F, _F, _I, _I, c_float]
+            lib.ref_add.argtypes = [_F, _F, _I]
+            lib.ref_silu_mul.argtypes = [_F, _F, _I]
+            lib.ref_silu_mul_simd.argtypes = [_F, _F, _I]
             lib.ref_backend_matmul.argtypes = [c_void_p, c_int, c_void_p, _I, _I, _F, _F, _I]
             _ref = lib
     return _ref
@@ -271,6 +284,74 @@ def ref_add_bias(x, b):
     b = _f32(b)
     _load_ref().ref_add_bias(_fp(y), _fp(b), b.size, y.size // b.size)
     return y
+
+
+def embed(table, ids):
+    """ref_ops.cpp:80-99 restated: rows ids of a float32 / float16 table [rows, d] as float32 [n, d]."""
+    table = np.ascontiguousarray(table)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    rows, d = table.shape
+    out = np.zeros((ids.size, d), np.float32)
+    if _load().orc_embed(_w_type(table), table.ctypes.data, rows, d, ids.ctypes.data, ids.size, _fp(out)) != 0:
+        raise ValueError("embed: token id out of range")
+    return out
+
+
+def rmsnorm(x, w, eps):
+    """ref_ops.cpp:137-148 restated: rows of x [n, d] normalised with the double sum and scale, times w [d]."""
+    x = _f32(x)
+    w = _f32(w)
+    y = np.zeros_like(x)
+    _load().orc_rmsnorm(_fp(x), _fp(w), _fp(y), x.size // w.size, w.size, eps)
+    return y
+
+
+def add(x, y):
+    """ref_ops.cpp:151-153 restated: x + y elementwise in float, on a copy of x."""
+    out = _f32(x).copy()
+    _load().orc_add(_fp(out), _fp(_f32(y)), out.size)
+    return out
+
+
+def silu_mul(gate, up):
+    """ref_ops.cpp:217-222 restated: g / (1 + expf(-g)) * up, on a copy of gate."""
+    out = _f32(gate).copy()
+    _load().orc_silu_mul(_fp(out), _fp(_f32(up)), out.size)
+    return out
+
+
+def ref_embed(table, ids):
+    table = np.ascontiguousarray(table)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    rows, d = table.shape
+    out = np.zeros((ids.size, d), np.float32)
+    if _load_ref().ref_embed(_w_type(table), table.ctypes.data, rows, d, ids.ctypes.data, ids.size, _fp(out)) != 0:
+        raise ValueError("ref_embed: token id out of range")
+    return out
+
+
+def ref_rmsnorm(x, w, eps, simd=False):
+    x = _f32(x)
+    w = _f32(w)
+    y = np.zeros_like(x)
+    fn = _load_ref().ref_rmsnorm_simd if simd else _load_ref().ref_rmsnorm
+    if fn(_fp(x), _fp(w), _fp(y), x.size // w.size, w.size, eps) != 0:
+        raise RuntimeError("the reference has no SIMD tier on this host")
+    return y
+
+
+def ref_add(x, y):
+    out = _f32(x).copy()
+    _load_ref().ref_add(_fp(out), _fp(_f32(y)), out.size)
+    return out
+
+
+def ref_silu_mul(gate, up, simd=False):
+    out = _f32(gate).copy()
+    fn = _load_ref().ref_silu_mul_simd if simd else _load_ref().ref_silu_mul
+    if fn(_fp(out), _fp(_f32(up)), out.size) != 0:
+        raise RuntimeError("the reference has no SIMD tier on this host")
+    return out
 
 
 def ref_kernel_set() -> str:

@@ -227,3 +227,43 @@ void orc_add_bias(float* x, const float* b, int64_t d, int64_t n) {
   for (int64_t t = 0; t < n; ++t)
     for (int64_t i = 0; i < d; ++i) x[t * d + i] += b[i];
 }
+
+/* ---- the other per-token ops of the forward (transformer.cpp:166-230) ---- */
+
+int orc_embed(int type, const void* table, int64_t rows, int64_t d, const int32_t* ids, int64_t n, float* out) {
+  if (type != 0 && type != 1) return -1;
+  for (int64_t t = 0; t < n; ++t) {
+    const int64_t id = ids[t];
+    if (id < 0 || id >= rows) return -1;
+    float* o = out + t * d;
+    if (type == 0) {
+      const float* r = (const float*)table + id * d;
+      for (int64_t k = 0; k < d; ++k) o[k] = r[k];
+    } else {
+      const uint16_t* r = (const uint16_t*)table + id * d;
+      for (int64_t k = 0; k < d; ++k) o[k] = orc_fp16_to_fp32(r[k]);
+    }
+  }
+  return 0;
+}
+
+void orc_rmsnorm(const float* x, const float* w, float* y, int64_t n, int64_t d, float eps) {
+  for (int64_t t = 0; t < n; ++t) {
+    const float* xt = x + t * d;
+    double ss = 0.0;
+    for (int64_t i = 0; i < d; ++i) ss += (double)xt[i] * (double)xt[i];
+    const double scale = 1.0 / sqrt(ss / (double)d + (double)eps);
+    for (int64_t i = 0; i < d; ++i) y[t * d + i] = (float)((double)xt[i] * scale * (double)w[i]);
+  }
+}
+
+void orc_add(float* x, const float* y, int64_t count) {
+  for (int64_t i = 0; i < count; ++i) x[i] += y[i];
+}
+
+void orc_silu_mul(float* gate, const float* up, int64_t count) {
+  for (int64_t i = 0; i < count; ++i) {
+    const float g = gate[i];
+    gate[i] = g / (1.0f + expf(-g)) * up[i];
+  }
+}

@@ -20,6 +20,12 @@
  *                          weights; fp64 brute force; the reference's AVX2 tier within float rounding.
  *   orc_fp16_to_fp32       every one of the 65536 halves (NaN payloads included) against numpy's exact conversion.
  *   orc_add_bias           bit-exact vs the compiled reference's cpu::add_bias.
+ *   orc_embed              bit-exact vs the compiled reference's cpu::embed (F32 and F16 tables, bad ids rejected).
+ *   orc_rmsnorm            bit-exact vs the compiled reference's scalar cpu::rmsnorm; its AVX2 tier within 1 ulp;
+ *                          closed form for constant rows; fp64 brute force.
+ *   orc_add                bit-exact vs the compiled reference's cpu::add and numpy.
+ *   orc_silu_mul           bit-exact vs the compiled reference's scalar cpu::silu_mul (same libm expf); fp64 closed
+ *                          form within 2 ulp; silu(0) = 0 and the large-|g| limits.
  *   orc_llama3_freq_factors  closed form of llama.cpp's Llama-3 rope scaling (third-party, not vendored):
  *                          checked against its defining properties (band limits, continuity at both edges,
  *                          monotonicity). Bit-level parity with the converter's float32 output is UNPINNED.
@@ -83,6 +89,20 @@ int orc_matmul(int w_type, const void* w, int64_t in, int64_t out, const float* 
 
 /* ref_ops.cpp:154-160 (cpu::add_bias): x[t*d + i] += b[i] for t < n. */
 void orc_add_bias(float* x, const float* b, int64_t d, int64_t n);
+
+/* ref_ops.cpp:80-99 (cpu::embed, float tables): out[t*d ..] = row ids[t] of table [rows, d], type 0 = F32,
+ * 1 = F16 (widened exactly). Returns -1 (writing nothing further) at the first id outside [0, rows). */
+int orc_embed(int type, const void* table, int64_t rows, int64_t d, const int32_t* ids, int64_t n, float* out);
+
+/* ref_ops.cpp:137-148 (cpu::rmsnorm): per row, ss = sum of double(x)^2 left to right, scale = 1 / sqrt(ss / d + eps)
+ * in double, y = float(x * scale * w) with the two double products in that order. */
+void orc_rmsnorm(const float* x, const float* w, float* y, int64_t n, int64_t d, float eps);
+
+/* ref_ops.cpp:151-153 (cpu::add): x[i] += y[i]. */
+void orc_add(float* x, const float* y, int64_t count);
+
+/* ref_ops.cpp:217-222 (cpu::silu_mul): gate[i] = g / (1 + expf(-g)) * up[i] in float. */
+void orc_silu_mul(float* gate, const float* up, int64_t count);
 
 /* Llama-3 rope frequency factors (llama.cpp convert_hf_to_gguf.py, rope_type "llama3"; not in the reference
  * tree, the reference only reads rope_freqs.weight, weights.cpp:56, and divides by it, ref_ops.cpp:175):

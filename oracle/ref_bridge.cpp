@@ -5,6 +5,7 @@
 #include <cstdint>
 #include <exception>
 #include <new>
+#include <span>
 
 #include "backend/cpu/cpu_backend.h"
 #include "backend/cpu/ref_ops.h"
@@ -89,6 +90,57 @@ int ref_add_bias(float* x, const float* b, int64_t d, int64_t n) {
   t.ne = {d, 1, 1, 1};
   t.data = b;
   nibble::cpu::add_bias(x, t, n);
+  return 0;
+}
+
+namespace {
+nibble::Tensor vec_f32(const float* v, int64_t d) {
+  nibble::Tensor t;
+  t.type = nibble::DType::F32;
+  t.n_dims = 1;
+  t.ne = {d, 1, 1, 1};
+  t.data = v;
+  return t;
+}
+}  // namespace
+
+// nibble::cpu::embed (ref_ops.cpp:80-99) for F32 (type 0) and F16 (type 1) tables [rows, d]; -1 on a bad id.
+int ref_embed(int type, const void* table, int64_t rows, int64_t d, const int32_t* ids, int64_t n, float* out) {
+  try {
+    nibble::cpu::embed(weight(type, table, d, rows), std::span<const int32_t>(ids, size_t(n)), out);
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
+// nibble::cpu::rmsnorm (ref_ops.cpp:137-148), the scalar path.
+int ref_rmsnorm(const float* x, const float* w, float* y, int64_t n, int64_t d, float eps) {
+  nibble::cpu::rmsnorm(x, vec_f32(w, d), y, n, eps);
+  return 0;
+}
+
+// nibble::cpu::add (ref_ops.cpp:151-153) and cpu::silu_mul (:217-222), the scalar paths.
+int ref_add(float* x, const float* y, int64_t count) {
+  nibble::cpu::add(x, y, count);
+  return 0;
+}
+int ref_silu_mul(float* gate, const float* up, int64_t count) {
+  nibble::cpu::silu_mul(gate, up, count);
+  return 0;
+}
+
+// The selected SIMD tier's rmsnorm / silu_mul (simd/ops.cpp:64-100): -1 when no tier is available.
+int ref_rmsnorm_simd(const float* x, const float* w, float* y, int64_t n, int64_t d, float eps) {
+  const nibble::simd::Kernels* ks = nibble::simd::select();
+  if (!ks) return -1;
+  ks->rmsnorm(x, vec_f32(w, d), y, n, eps);
+  return 0;
+}
+int ref_silu_mul_simd(float* gate, const float* up, int64_t count) {
+  const nibble::simd::Kernels* ks = nibble::simd::select();
+  if (!ks) return -1;
+  ks->silu_mul(gate, up, count);
   return 0;
 }
 

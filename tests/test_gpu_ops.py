@@ -1,0 +1,94 @@
+"""GPU parity of the per-token ops a forward needs besides attention and the projections: embed, rmsnorm, add,
+silu_mul (Backend members, backend.h:55-70), through the C ABI, against the oracle (each op pinned to the compiled
+reference in tests/test_oracle.py).
+
+Bars: embed and add bit-exact. rmsnorm within 1 ulp: the double sum of squares is taken in another order than the
+reference's (as the reference's own AVX2 tier does), which can move a float result only when the exact value lies
+within ~1e-16 of a rounding boundary. silu_mul within 4 ulp (device expf against the host's), or 1e-37 absolute
+where exp(-g) overflows and both give a signed zero or denormal.
+"""
+import numpy as np
+import pytest
+
+import nibble_amd
+import oracle
+from tests.gpu_util import Buffers, bits
+from tests.test_oracle import ulp_diff
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16], ids=["f32", "f16"])
+@pytest.mark.parametrize("d", [16, 896, 2048, 2049])
+def test_embed_bit_exact(backend, dt, d):
+    rng = np.random.default_rng(d)
+    table = rng.standard_normal((300, d)).astype(dt)
+    ids = rng.integers(0, 300, 37).astype(np.int32)
+    ids[:3] = [0, 299, 0]
+    with Buffers(backend) as B:
+        out = B.alloc(ids.size * d)
+        backend.embed(table, ids, out)
+        got = backend.download(out, (ids.size, d))
+    assert np.array_equal(bits(got), bits(oracle.embed(table, ids)))
+    backend.release_weights()
+
+
+def test_embed_rejects_bad_ids_before_any_work(backend):
+    table = np.zeros((10, 8), np.float32)
+    with Buffers(backend) as B:
+        out = B.upload(np.full((2, 8), 7.0, np.float32))
+        for bad in ([10], [-1], [3, 11]):
+            with pytest.raises(nibble_amd.BackendError, match="out of range"):
+                backend.embed(table, np.array(bad, np.int32), out)
+        assert np.all(backend.download(out, (2, 8)) == 7.0)
+    backend.release_weights()
+
+
+@pytest.mark.parametrize("n,d", [(1, 896), (5, 2048), (512, 2048), (3, 16), (7, 1000)])
+def test_rmsnorm_matches_reference(backend, n, d):
+    rng = np.random.default_rng(n * d)
+    x = (rng.standard_normal((n, d)) * rng.uniform(0.01, 50, (n, 1))).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    with Buffers(backend) as B:
+        dx, dy = B.upload(x), B.alloc(n * d)
+        backend.rmsnorm(dx, w, dy, n, 1e-5)
+        got = backend.download(dy, (n, d))
+        backend.rmsnorm(dx, w, dx, n, 1e-5)  # in place (x == y) gives the same bits
+        inplace = backend.download(dx, (n, d))
+    ref = oracle.rmsnorm(x, w, 1e-5)
+    u = ulp_diff(got, ref)
+    print(f"rmsnorm n={n} d={d}: {int(np.sum(u > 0))} elements differ, max {int(u.max())} ulp", flush=True)
+    assert int(u.max()) <= 1
+    assert np.array_equal(bits(got), bits(inplace))
+    backend.release_weights()
+
+
+@pytest.mark.parametrize("count", [1, 1000, 8192 * 5 + 3])
+def test_add_and_silu_mul(backend, count):
+    rng = np.random.default_rng(count)
+    g = (rng.standard_normal(count) * 8).astype(np.float32)
+    u = rng.standard_normal(count).astype(np.float32)
+    if count > 6:
+        g[:6] = [0.0, -0.0, 88.0, -88.0, 95.0, -100.0]
+    with Buffers(backend) as B:
+        dg, du = B.upload(g), B.upload(u)
+        backend.add(dg, du, count)
+        added = backend.download(dg, (count,))
+        backend.write(dg, g)
+        backend.silu_mul(dg, du, count)
+        silu = backend.download(dg, (count,))
+    assert np.array_equal(bits(added), bits(oracle.add(g, u)))
+    ref = oracle.silu_mul(g, u)
+    ok = (ulp_diff(silu, ref) <= 4) | ((np.abs(ref) < 1e-37) & (np.abs(silu) < 1e-37))
+    assert np.all(ok), f"{int(np.sum(~ok))} silu_mul elements beyond 4 ulp"
+
+
+def test_ops_reject_ranges_outside_buffers(backend):
+    with Buffers(backend) as B:
+        a, b = B.alloc(64), B.alloc(32)  # allocations are 64-byte granular: b holds exactly 32 floats
+        with pytest.raises(nibble_amd.BackendError, match="not inside one buffer"):
+            backend.add(a, b, 64)
+        with pytest.raises(nibble_amd.BackendError, match="not inside one buffer"):
+            backend.silu_mul(b, a, 64)
+        with pytest.raises(nibble_amd.BackendError, match="need F32"):
+            backend.rmsnorm(a, nibble_amd.weight(np.ones(64, np.float16)), a, 1, 1e-5)
