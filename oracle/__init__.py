@@ -67,6 +67,19 @@ def _load():
         lib.orc_add.restype = None
         lib.orc_silu_mul.argtypes = [_F, _F, _I]
         lib.orc_silu_mul.restype = None
+        lib.orc_block_bytes.argtypes = [c_int]
+        lib.orc_block_bytes.restype = _I
+        lib.orc_block_elems.argtypes = [c_int]
+        lib.orc_block_elems.restype = _I
+        lib.orc_fp32_to_fp16.argtypes = [c_float]
+        lib.orc_fp32_to_fp16.restype = ctypes.c_uint16
+        for q in ("orc_quantize_q8_0", "orc_quantize_q8_1", "orc_quantize_q8_k"):
+            getattr(lib, q).argtypes = [_F, c_void_p, _I]
+        lib.orc_dequantize.argtypes = [c_int, c_void_p, _F, _I]
+        lib.orc_dot.argtypes = [c_int, c_void_p, c_void_p, _I]
+        lib.orc_dot.restype = c_float
+        lib.orc_act_kind.argtypes = [c_int]
+        lib.orc_matmul_q.argtypes = [c_int, c_void_p, _I, _I, _F, _F, _I]
         _lib = lib
     return _lib
 
@@ -98,6 +111,10 @@ def _load_ref():
             lib.ref_add.argtypes = [_F, _F, _I]
             lib.ref_silu_mul.argtypes = [_F, _F, _I]
             lib.ref_silu_mul_simd.argtypes = [_F, _F, _I]
+            lib.ref_quantize.argtypes = [c_int, _F, c_void_p, _I]
+            lib.ref_dequantize.argtypes = [c_int, c_void_p, _F, _I]
+            lib.ref_dot.argtypes = [c_int, c_void_p, c_void_p, _I]
+            lib.ref_dot.restype = c_float
             lib.ref_backend_matmul.argtypes = [c_void_p, c_int, c_void_p, _I, _I, _F, _F, _I]
             _ref = lib
     return _ref
@@ -398,6 +415,15 @@ class RefCpuBackend:
             raise RuntimeError("matmul failed")
         return y
 
+    def matmul_q(self, t, w, in_, out_, x):
+        """CpuBackend::matmul for a quantized weight (raw row bytes): the production tier over the pool."""
+        w = np.ascontiguousarray(w, np.uint8)
+        x = _f32(x).reshape(-1, in_)
+        y = np.zeros((x.shape[0], out_), np.float32)
+        if self._lib.ref_backend_matmul(self._h, t, w.ctypes.data, in_, out_, _fp(x), _fp(y), x.shape[0]) != 0:
+            raise RuntimeError("matmul failed")
+        return y
+
     def close(self):
         if self._h:
             self._lib.ref_backend_destroy(self._h)
@@ -408,3 +434,87 @@ class RefCpuBackend:
             self.close()
         except Exception:
             pass
+
+
+# ---------------------------------------------------------------- quantized formats (quant.c; src/quant.cpp)
+
+# ggml type ids (src/tensor.h) and the activation kind each weight type pairs with (quant.h:7-12)
+F32, F16, Q4_0, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 6, 7, 8, 12, 13, 14
+QUANT_TYPES = (Q4_0, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K)
+ACT_BYTES = {0: 34, 1: 36, 2: 292}  # Q8_0, Q8_1, Q8_K block bytes
+
+
+def block_bytes(t):
+    return int(_load().orc_block_bytes(t))
+
+
+def block_elems(t):
+    return int(_load().orc_block_elems(t))
+
+
+def act_kind(t):
+    return int(_load().orc_act_kind(t))
+
+
+def fp32_to_fp16(f):
+    return int(_load().orc_fp32_to_fp16(float(f)))
+
+
+def quantize(kind, x):
+    """quant.cpp:245-303: float row(s) x to Q8_0 (kind 0), Q8_1 (1) or Q8_K (2) block bytes (uint8 array)."""
+    x = _f32(x).reshape(-1)
+    per = 32 if kind < 2 else 256
+    out = np.zeros(x.size // per * ACT_BYTES[kind], np.uint8)
+    fn = (_load().orc_quantize_q8_0, _load().orc_quantize_q8_1, _load().orc_quantize_q8_k)[kind]
+    if fn(_fp(x), out.ctypes.data, x.size) != 0:
+        raise ValueError("quantize: length is not a multiple of the block size")
+    return out
+
+
+def dequantize(t, raw, n):
+    """quant.cpp:157-242: n elements of type t from raw bytes."""
+    raw = np.ascontiguousarray(raw, np.uint8)
+    out = np.zeros(n, np.float32)
+    if _load().orc_dequantize(t, raw.ctypes.data, _fp(out), n) != 0:
+        raise ValueError("dequantize: bad type or length")
+    return out
+
+
+def dot(t, w, a, nb):
+    """quant.cpp:305-419: block dot of weight blocks w (type t) with activation blocks a, nb blocks."""
+    w = np.ascontiguousarray(w, np.uint8)
+    a = np.ascontiguousarray(a, np.uint8)
+    return np.float32(_load().orc_dot(t, w.ctypes.data, a.ctypes.data, nb))
+
+
+def matmul_q(t, w, in_, out_, x):
+    """ref_ops.cpp:109-135 for quantized weights: y[n, out] from raw weight rows (out rows of in_ elements)."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x = _f32(x).reshape(-1, in_)
+    y = np.zeros((x.shape[0], out_), np.float32)
+    if _load().orc_matmul_q(t, w.ctypes.data, in_, out_, _fp(x), _fp(y), x.shape[0]) != 0:
+        raise ValueError("matmul_q: bad type or width")
+    return y
+
+
+def ref_quantize(kind, x):
+    x = _f32(x).reshape(-1)
+    per = 32 if kind < 2 else 256
+    out = np.zeros(x.size // per * ACT_BYTES[kind], np.uint8)
+    if _load_ref().ref_quantize(kind, _fp(x), out.ctypes.data, x.size) != 0:
+        raise ValueError("ref_quantize failed")
+    return out
+
+
+def ref_dequantize(t, raw, n):
+    raw = np.ascontiguousarray(raw, np.uint8)
+    out = np.zeros(n, np.float32)
+    if _load_ref().ref_dequantize(t, raw.ctypes.data, _fp(out), n) != 0:
+        raise ValueError("ref_dequantize failed")
+    return out
+
+
+def ref_dot(t, w, a, nb):
+    w = np.ascontiguousarray(w, np.uint8)
+    a = np.ascontiguousarray(a, np.uint8)
+    return np.float32(_load_ref().ref_dot(t, w.ctypes.data, a.ctypes.data, nb))

@@ -26,6 +26,9 @@
  *   orc_add                bit-exact vs the compiled reference's cpu::add and numpy.
  *   orc_silu_mul           bit-exact vs the compiled reference's scalar cpu::silu_mul (same libm expf); fp64 closed
  *                          form within 2 ulp; silu(0) = 0 and the large-|g| limits.
+ *   orc_quantize_q8_0/_q8_1/_q8_k, orc_dequantize, orc_dot, orc_matmul_q (quant.c): the golden vectors of the
+ *                          reference's tests/data/quant_golden.inc (llama.cpp's own outputs) and bit-exact vs the
+ *                          compiled reference's quant.cpp and CpuBackend::matmul on random blocks of every type.
  *   orc_llama3_freq_factors  closed form of llama.cpp's Llama-3 rope scaling (third-party, not vendored):
  *                          checked against its defining properties (band limits, continuity at both edges,
  *                          monotonicity). Bit-level parity with the converter's float32 output is UNPINNED.
@@ -103,6 +106,18 @@ void orc_add(float* x, const float* y, int64_t count);
 
 /* ref_ops.cpp:217-222 (cpu::silu_mul): gate[i] = g / (1 + expf(-g)) * up[i] in float. */
 void orc_silu_mul(float* gate, const float* up, int64_t count);
+
+/* ---- quantized formats (quant.c, restating src/quant.cpp and src/fp16.h); type = ggml id ---- */
+int64_t orc_block_bytes(int type); /* bytes per block, -1 for an unknown type */
+int64_t orc_block_elems(int type); /* elements per block (1 for F32 / F16) */
+uint16_t orc_fp32_to_fp16(float f);
+int orc_quantize_q8_0(const float* x, void* y, int64_t n);
+int orc_quantize_q8_1(const float* x, void* y, int64_t n);
+int orc_quantize_q8_k(const float* x, void* y, int64_t n);
+int orc_dequantize(int type, const void* src, float* dst, int64_t n);
+float orc_dot(int type, const void* w, const void* a, int64_t n_blocks);
+int orc_act_kind(int type); /* 0 = Q8_0, 1 = Q8_1, 2 = Q8_K activations, -1 = float weights */
+int orc_matmul_q(int type, const void* w, int64_t in, int64_t out, const float* x, float* y, int64_t n);
 
 /* Llama-3 rope frequency factors (llama.cpp convert_hf_to_gguf.py, rope_type "llama3"; not in the reference
  * tree, the reference only reads rope_freqs.weight, weights.cpp:56, and divides by it, ref_ops.cpp:175):

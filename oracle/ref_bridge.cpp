@@ -4,12 +4,14 @@
 // bench.py can time the reference's CPU attention as its baseline. Nothing of the reference is copied here.
 #include <cstdint>
 #include <exception>
+#include <limits>
 #include <new>
 #include <span>
 
 #include "backend/cpu/cpu_backend.h"
 #include "backend/cpu/ref_ops.h"
 #include "backend/cpu/simd/dispatch.h"
+#include "quant.h"
 #include "thread_pool.h"
 
 namespace {
@@ -64,7 +66,7 @@ const char* ref_kernel_set() {
 namespace {
 nibble::Tensor weight(int type, const void* w, int64_t in, int64_t out) {
   nibble::Tensor t;
-  t.type = type == 1 ? nibble::DType::F16 : nibble::DType::F32;
+  t.type = static_cast<nibble::DType>(type);  // ggml type id: 0 F32, 1 F16, 2 Q4_0, ... 14 Q6_K
   t.n_dims = 2;
   t.ne = {in, out, 1, 1};
   t.data = w;
@@ -142,6 +144,40 @@ int ref_silu_mul_simd(float* gate, const float* up, int64_t count) {
   if (!ks) return -1;
   ks->silu_mul(gate, up, count);
   return 0;
+}
+
+// src/quant.cpp: the activation quantizers (quant.h:120-133), dequantize_row (:117) and the block dots
+// (:137-160), as the reference compiles them.
+int ref_quantize(int kind, const float* x, void* y, int64_t n) {
+  try {
+    if (kind == 0) nibble::quantize_row_q8_0(x, static_cast<nibble::BlockQ8_0*>(y), n);
+    else if (kind == 1) nibble::quantize_row_q8_1(x, static_cast<nibble::BlockQ8_1*>(y), n);
+    else nibble::quantize_row_q8_K(x, static_cast<nibble::BlockQ8_K*>(y), n);
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+int ref_dequantize(int type, const void* src, float* dst, int64_t n) {
+  try {
+    nibble::dequantize_row(static_cast<nibble::DType>(type), src, dst, n);
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+float ref_dot(int type, const void* w, const void* a, int64_t nb) {
+  using namespace nibble;
+  switch (static_cast<DType>(type)) {
+    case DType::Q4_0: return dot_q4_0_q8_0(static_cast<const BlockQ4_0*>(w), static_cast<const BlockQ8_0*>(a), nb);
+    case DType::Q8_0: return dot_q8_0_q8_0(static_cast<const BlockQ8_0*>(w), static_cast<const BlockQ8_0*>(a), nb);
+    case DType::Q5_0: return dot_q5_0_q8_0(static_cast<const BlockQ5_0*>(w), static_cast<const BlockQ8_0*>(a), nb);
+    case DType::Q5_1: return dot_q5_1_q8_1(static_cast<const BlockQ5_1*>(w), static_cast<const BlockQ8_1*>(a), nb);
+    case DType::Q4_K: return dot_q4_K_q8_K(static_cast<const BlockQ4_K*>(w), static_cast<const BlockQ8_K*>(a), nb);
+    case DType::Q5_K: return dot_q5_K_q8_K(static_cast<const BlockQ5_K*>(w), static_cast<const BlockQ8_K*>(a), nb);
+    case DType::Q6_K: return dot_q6_K_q8_K(static_cast<const BlockQ6_K*>(w), static_cast<const BlockQ8_K*>(a), nb);
+    default: return std::numeric_limits<float>::quiet_NaN();
+  }
 }
 
 // A ThreadPool of `threads` threads and a CpuBackend on it (nibble.cpp:75-85 builds the same pair).
