@@ -179,6 +179,21 @@ int nbhs_add_f32(float* x, const float* y, int64_t count, nbhs_stream s);
 /* gate[i] = g / (1 + exp(-g)) * up[i] (ref_ops.cpp:217-222). */
 int nbhs_silu_mul_f32(float* gate, const float* up, int64_t count, nbhs_stream s);
 
+/* ---- quantized weights (Backend::matmul / embed for Q4_0 .. Q6_K; src/quant.h, ref_ops.cpp:109-135) ----
+ * type is the ggml id. A weight lives on the device in the plane layout of kernels/quant_layout.h (the host repacks
+ * the file's blocks on upload); activations are quantized into planes of the same header's ActLayout. */
+int64_t nbhs_quant_weight_bytes(int type, int64_t rows, int64_t in); /* -1 when not a quant type / bad width */
+int64_t nbhs_quant_act_bytes(int type, int64_t n, int64_t in);
+/* The n x in activation rows x quantized to type's companion format (quant.cpp:37-49, 245-303), bit-exact. */
+int nbhs_quantize_acts(int type, const float* x, int64_t n, int64_t in, void* acts, nbhs_stream s);
+/* y[t * rows + r] for t < n (n <= 16): the block dot of weight row r with activation row t0 + t of the n_acts rows
+ * quantized into acts (quant.cpp:305-419, same bits). */
+int nbhs_qgemv(int type, const void* w, int64_t rows, int64_t in, const void* acts, int64_t n_acts, int64_t t0,
+               int64_t n, float* y, nbhs_stream s);
+/* out[t, :] = dequantized row ids[t] (device ids) of the weight, quant.cpp:157-242 bit for bit. */
+int nbhs_dequant_rows(int type, const void* w, int64_t rows, int64_t in, const int32_t* ids, int64_t n, float* out,
+                      nbhs_stream s);
+
 /* ---- per-kernel timing (measurement only) ----
  * While enabled for a kernel, its launcher launches it with a HIP event pair (hipExtLaunchKernel) stamped from the
  * dispatch itself, so the average device duration of that kernel can be read back live (bench.py's roofline
@@ -196,8 +211,10 @@ enum nbhs_kernel_id {
   NBHS_K_CONVERT = 8,
   NBHS_K_ADD_BIAS = 9,
   NBHS_K_RMSNORM = 10,
-  NBHS_K_ELEMENTWISE = 11, /* embed, add, silu_mul */
-  NBHS_K_COUNT = 12
+  NBHS_K_ELEMENTWISE = 11, /* embed, add, silu_mul, dequantized embed */
+  NBHS_K_QUANTIZE = 12,    /* activation quantization for quantized weights */
+  NBHS_K_QGEMV = 13,
+  NBHS_K_COUNT = 14
 };
 int nbhs_kernel_timing_enable(int on); /* on != 0: time every kernel; 0: none (clears what was recorded) */
 int nbhs_kernel_timing_select(uint32_t kernel_mask); /* time the kernels whose bit (1 << id) is set; clears */

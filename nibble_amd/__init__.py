@@ -19,8 +19,9 @@ LIB_PATH = os.path.join(_DIR, "libnibble_hip.so")
 _F = POINTER(c_float)
 _I = c_int64
 
-# ggml type ids of the weight types the GPU matmul takes (src/tensor.h:21-31 in the reference).
-F32, F16 = 0, 1
+# ggml type ids of the weight types the GPU backend takes (src/tensor.h:21-31 in the reference).
+F32, F16, Q4_0, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 6, 7, 8, 12, 13, 14
+QUANT_TYPES = (Q4_0, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K)
 
 
 class NbhTensor(ctypes.Structure):
@@ -125,8 +126,17 @@ class DevicePtr(int):
 
 
 def weight(w, shape=None, dtype=None) -> NbhTensor:
-    """An nbh_tensor for a weight: a 2-D (or 1-D) float32/float16 host array, or a DevicePtr into a buffer of
-    this backend with its (rows, ne0) shape and type (F32 or F16)."""
+    """An nbh_tensor for a weight: a 2-D (or 1-D) float32/float16 host array; raw block bytes (a uint8 host array)
+    with the (rows, ne0) shape and a quantized type id; or a DevicePtr into a buffer of this backend with its shape
+    and type (F32 or F16)."""
+    if isinstance(w, NbhTensor):
+        return w
+    if hasattr(w, "nbh_tensor"):
+        return w.nbh_tensor()
+    if isinstance(w, np.ndarray) and dtype is not None:
+        assert w.flags.c_contiguous and shape is not None
+        ne = [int(shape[-1]), int(shape[0]) if len(shape) > 1 else 1, 1, 1]
+        return NbhTensor(dtype, len(shape), (c_int64 * 4)(*ne), c_void_p(w.ctypes.data))
     if isinstance(w, np.ndarray):
         if w.dtype == np.float32:
             t = F32
@@ -231,6 +241,8 @@ class HipBackend:
     def _tensor(self, w, shape=None, dtype=None) -> NbhTensor:
         if isinstance(w, np.ndarray):
             self._kept[w.ctypes.data] = w
+        elif hasattr(w, "nbh_tensor"):  # an object holding raw blocks (keeps its array alive through us)
+            self._kept[id(w)] = w
         return weight(w, shape, dtype)
 
     def matmul(self, w, x, y, n: int, shape=None, dtype=None):
@@ -345,7 +357,7 @@ class KernelTiming:
     include/nibble_hip_shim.h). Used by the benchmark for roofline figures."""
 
     (ROPE, APPEND_ROPE, DECODE_PARTIAL, DECODE_COMBINE, GENERIC, STAGE_KV, PREFILL_MFMA, GEMV, CONVERT, ADD_BIAS, RMSNORM,
-     ELEMENTWISE) = range(12)
+     ELEMENTWISE, QUANTIZE, QGEMV) = range(14)
 
     @staticmethod
     def enable(on: bool = True, only: int | None = None):

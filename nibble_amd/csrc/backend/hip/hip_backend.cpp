@@ -3,6 +3,8 @@
 // Host-side C++20 only; every device action goes through nibble_hip_shim.h.
 #include "backend/hip/hip_backend.h"
 
+#include "kernels/quant_layout.h"
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -21,6 +23,37 @@ constexpr int64_t kGemvMaxRows = NBHS_GEMV_MAX_ROWS;
 constexpr size_t kGemvMaxWeights = NBHS_GEMV_MAX_WEIGHTS;
 
 std::string str(int64_t v) { return std::to_string(v); }
+
+// Splits a quantized weight's file blocks (src/quant.h:34-110: rows x nb blocks of block_bytes) into the plane
+// layout of kernels/quant_layout.h. Bytes are copied unchanged, only moved to aligned places.
+std::vector<uint8_t> repack_quant(int t, const uint8_t* src, int64_t rows, int64_t nb) {
+  using namespace nbh_quant;
+  const WeightLayout l = weight_layout(t, rows, nb);
+  std::vector<uint8_t> out(size_t(l.bytes), 0);
+  const int64_t bb = block_bytes(t), qb = q_bytes(t), hb = h_bytes(t), sb = s_bytes(t);
+  // field offsets inside a file block: d, m (or dmin), scales, qh, quants
+  int od = 0, om = -1, os = -1, oh = -1, oq = 2;
+  switch (t) {
+    case kQ4_0: break;
+    case kQ8_0: break;
+    case kQ5_0: oh = 2, oq = 6; break;
+    case kQ5_1: om = 2, oh = 4, oq = 8; break;
+    case kQ4_K: om = 2, os = 4, oq = 16; break;
+    case kQ5_K: om = 2, os = 4, oh = 16, oq = 48; break;
+    case kQ6_K: od = 208, os = 192, oh = 128, oq = 0; break;
+    default: break;
+  }
+  const int64_t s_len = t == kQ6_K ? 16 : 12;
+  for (int64_t i = 0; i < rows * nb; ++i) {
+    const uint8_t* b = src + i * bb;
+    std::memcpy(&out[size_t(l.q_off + i * qb)], b + oq, size_t(qb));
+    std::memcpy(&out[size_t(l.d_off + i * 2)], b + od, 2);
+    if (om >= 0) std::memcpy(&out[size_t(l.m_off + i * 2)], b + om, 2);
+    if (oh >= 0) std::memcpy(&out[size_t(l.h_off + i * hb)], b + oh, size_t(hb));
+    if (os >= 0) std::memcpy(&out[size_t(l.s_off + i * sb)], b + os, size_t(s_len));
+  }
+  return out;
+}
 
 bool overflow_mul(int64_t a, int64_t b, int64_t* out) { return __builtin_mul_overflow(a, b, out); }
 
@@ -41,6 +74,7 @@ HipBackend::~HipBackend() {
   nbhs_free(copy_tmp_);
   nbhs_free(widen_tmp_);
   nbhs_free(ids_buf_);
+  nbhs_free(acts_buf_);
   for (auto& [key, d] : weights_) {
     nbhs_free(const_cast<void*>(d.dev));
     nbhs_free(d.f32);
@@ -81,7 +115,8 @@ void HipBackend::ensure(float*& buf, size_t& cap_bytes, size_t need_bytes) {
 }
 
 size_t HipBackend::internal_bytes() const {
-  size_t s = decode_ws_bytes_ + k16_bytes_ + vt16_bytes_ + copy_tmp_bytes_ + widen_tmp_bytes_ + ids_buf_bytes_;
+  size_t s = decode_ws_bytes_ + k16_bytes_ + vt16_bytes_ + copy_tmp_bytes_ + widen_tmp_bytes_ + ids_buf_bytes_ +
+             acts_buf_bytes_;
   for (auto& t : rope_tables_) s += size_t(t.rows) * size_t(t.head_dim) * sizeof(float);
   return s;
 }
@@ -188,21 +223,32 @@ bool HipBackend::in_buffer(const void* p, int64_t bytes) const {
 
 HipBackend::DeviceWeight HipBackend::device_weight(const Tensor& w, const char* op) {
   if (!w.data) throw Error(std::string(op) + ": weight data is null");
-  if (w.type != DType::F32 && w.type != DType::F16)
-    throw Error(std::string(op) + ": weight type " + str(int64_t(w.type)) +
-                " is not supported by the GPU backend (F32 and F16 only)");
+  const bool quant = nbh_quant::is_quant(int(w.type));
+  if (w.type != DType::F32 && w.type != DType::F16 && !quant)
+    throw Error(std::string(op) + ": weight type " + str(int64_t(w.type)) + " is not supported by the GPU backend");
   const int64_t in = w.ne[0], rows = w.rows();
-  const int64_t elem = w.type == DType::F32 ? 4 : 2;
   int64_t count, bytes;
-  if (in <= 0 || rows <= 0 || overflow_mul(in, rows, &count) || overflow_mul(count, elem, &bytes))
+  if (in <= 0 || rows <= 0 || overflow_mul(in, rows, &count))
     throw Error(std::string(op) + ": invalid weight shape " + str(in) + " x " + str(rows));
-  if (reinterpret_cast<uintptr_t>(w.data) % size_t(elem) != 0)
-    throw Error(std::string(op) + ": weight data is not aligned to its element size");
+  if (quant) {
+    const int64_t be = nbh_quant::block_elems(int(w.type));
+    if (in % be != 0)
+      throw Error(std::string(op) + ": quantized weight width " + str(in) + " is not a multiple of " + str(be));
+    if (overflow_mul(count / be, nbh_quant::block_bytes(int(w.type)), &bytes))
+      throw Error(std::string(op) + ": weight size overflows");
+  } else {
+    const int64_t elem = w.type == DType::F32 ? 4 : 2;
+    if (overflow_mul(count, elem, &bytes)) throw Error(std::string(op) + ": weight size overflows");
+    if (reinterpret_cast<uintptr_t>(w.data) % size_t(elem) != 0)
+      throw Error(std::string(op) + ": weight data is not aligned to its element size");
+  }
   DeviceWeight d;
   d.type = w.type;
   d.in = in;
   d.rows = rows;
   if (in_buffer(w.data, bytes)) {  // already in HBM: use in place
+    if (quant)
+      throw Error(std::string(op) + ": a quantized weight must be host memory (it is repacked on upload)");
     d.dev = w.data;
     return d;
   }
@@ -215,15 +261,24 @@ HipBackend::DeviceWeight HipBackend::device_weight(const Tensor& w, const char* 
     nbhs_free(it->second.f32);
     weights_.erase(it);
   }
+  std::vector<uint8_t> planes;
+  const void* src = w.data;
+  if (quant) {
+    planes = repack_quant(int(w.type), static_cast<const uint8_t*>(w.data), rows,
+                          in / nbh_quant::block_elems(int(w.type)));
+    src = planes.data();
+    bytes = int64_t(planes.size());
+  }
   void* p = nullptr;
   check(nbhs_malloc(&p, size_t(bytes)), "weight allocation");
-  const int cr = nbhs_memcpy_h2d(p, w.data, size_t(bytes), stream_);
+  const int cr = nbhs_memcpy_h2d(p, src, size_t(bytes), stream_);
   if (cr != 0) {
     nbhs_free(p);
     check(cr, "weight upload");
   }
   d.dev = p;
   d.key = w.data;
+  d.bytes = bytes;
   weights_.emplace(w.data, d);
   return d;
 }
@@ -262,11 +317,12 @@ void HipBackend::release_weights() {
 
 size_t HipBackend::weight_bytes() const {
   size_t s = 0;
-  for (auto& [key, d] : weights_) {
-    const size_t count = size_t(d.in) * size_t(d.rows);
-    s += count * (d.type == DType::F32 ? 4 : 2) + (d.f32 ? count * 4 : 0);
-  }
+  for (auto& [key, d] : weights_) s += size_t(d.bytes) + (d.f32 ? size_t(d.in) * size_t(d.rows) * 4 : 0);
   return s;
+}
+
+bool HipBackend::supports(DType t) const {
+  return t == DType::F32 || t == DType::F16 || nbh_quant::is_quant(int(t));
 }
 
 void HipBackend::matmul(const Tensor& w, const float* x, float* y, int64_t n) {
@@ -303,6 +359,40 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
     if (ya < xa + uint64_t(x_count) * 4 && xa < ya + uint64_t(y_count) * 4)
       throw Error("matmul: output " + str(int64_t(i)) + " overlaps the input");
   }
+  // Quantized weights: x is quantized once per activation format and every weight takes the block-dot kernel in
+  // chunks of up to 16 activation rows (ref_ops.cpp:109-135, CpuBackend::matmul_multi's shared quantization).
+  std::vector<size_t> fl;
+  int done_act = -1;
+  for (size_t i = 0; i < dw.size(); ++i) {
+    const int t = int(dw[i].type);
+    if (!nbh_quant::is_quant(t)) {
+      fl.push_back(i);
+      continue;
+    }
+    const int act = nbh_quant::act_of(t);
+    const int64_t ab = nbhs_quant_act_bytes(t, n, in);
+    if (ab < 0) throw Error("matmul: invalid quantized shape");
+    if (act != done_act) {
+      ensure(acts_buf_, acts_buf_bytes_, size_t(ab));
+      check(nbhs_quantize_acts(t, x, n, in, acts_buf_, stream_), "matmul (activation quantization)");
+      done_act = act;
+    }
+    for (int64_t t0 = 0; t0 < n; t0 += kGemvMaxRows)
+      check(nbhs_qgemv(t, dw[i].dev, dw[i].rows, in, acts_buf_, n, t0, std::min(kGemvMaxRows, n - t0),
+                       ys[i] + t0 * dw[i].rows, stream_),
+            "matmul (quantized)");
+  }
+  if (fl.size() != dw.size()) {
+    std::vector<DeviceWeight> fw;
+    std::vector<float*> fy;
+    for (size_t i : fl) fw.push_back(dw[i]), fy.push_back(ys[i]);
+    dw.swap(fw);
+    ys_float_.assign(fy.begin(), fy.end());
+  } else {
+    ys_float_.assign(ys.begin(), ys.end());
+  }
+  if (dw.empty()) return;
+  const std::vector<float*>& yv = ys_float_;
   if (n <= kGemvMaxRows) {
     // One launch per (up to) eight weights: every weight row is read once for all n rows.
     for (size_t b = 0; b < dw.size(); b += kGemvMaxWeights) {
@@ -314,7 +404,7 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
       for (size_t j = 0; j < cnt; ++j) {
         f16[j] = dw[b + j].type == DType::F16;
         wp[j] = dw[b + j].dev;
-        yp[j] = ys[b + j];
+        yp[j] = yv[b + j];
         rows[j] = dw[b + j].rows;
       }
       check(nbhs_gemv_multi(int(cnt), f16, wp, yp, rows, in, x, n, stream_), "matmul (gemv)");
@@ -323,7 +413,7 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
   }
   if (!blas_) check(nbhs_blas_create(&blas_, stream_), "rocBLAS handle");
   for (size_t i = 0; i < dw.size(); ++i)
-    check(nbhs_sgemm_xwt(blas_, x, weight_f32(dw[i]), ys[i], n, in, dw[i].rows), "matmul (sgemm)");
+    check(nbhs_sgemm_xwt(blas_, x, weight_f32(dw[i]), yv[i], n, in, dw[i].rows), "matmul (sgemm)");
 }
 
 void HipBackend::embed(const Tensor& table, std::span<const int32_t> ids, float* out) {
@@ -338,6 +428,12 @@ void HipBackend::embed(const Tensor& table, std::span<const int32_t> ids, float*
   const DeviceWeight w = device_weight(table, "embed");
   ensure(ids_buf_, ids_buf_bytes_, size_t(n) * sizeof(int32_t));
   check(nbhs_memcpy_h2d(ids_buf_, ids.data(), size_t(n) * sizeof(int32_t), stream_), "embed ids upload");
+  if (nbh_quant::is_quant(int(w.type))) {
+    check(nbhs_dequant_rows(int(w.type), w.dev, w.rows, d, reinterpret_cast<const int32_t*>(ids_buf_), n, out,
+                            stream_),
+          "embed (dequantize)");
+    return;
+  }
   check(nbhs_embed(w.type == DType::F16, w.dev, reinterpret_cast<const int32_t*>(ids_buf_), n, d, out, stream_),
         "embed");
 }

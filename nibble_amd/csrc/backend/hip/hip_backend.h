@@ -3,8 +3,9 @@
 // It replaces CpuBackend (reference src/backend/cpu/cpu_backend.h:18-91) for the ops the attention path uses:
 // reserve/alloc/free/read/copy, rope and attention, plus HIP-only extensions (host upload, the fused KV append
 // with RoPE, synthetic fill, events), the QKV projection that feeds it (matmul / matmul_multi and add_bias), and the
-// remaining per-token ops (embed, rmsnorm, add, silu_mul), so a whole forward stays on the GPU. Weights may be F32 or
-// F16 (supports() is true for those two); quantized types are not on the GPU and are rejected up front.
+// remaining per-token ops (embed, rmsnorm, add, silu_mul), so a whole forward stays on the GPU. Weights may be F32,
+// F16 or any of the reference's quantized types (Q4_0, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K): supports() is true for
+// all of them. Quantized matmuls and embeds are bit-exact with the reference's quant.cpp.
 //
 // Weights: a Tensor's data is host memory (nibble maps the GGUF file), or memory from alloc(). Host weights are
 // copied to HBM on first use and kept, keyed by their data pointer, until release_weights() or destruction; the
@@ -34,7 +35,7 @@ class HipBackend final : public Backend {
   HipBackend(const HipBackend&) = delete;
   HipBackend& operator=(const HipBackend&) = delete;
 
-  bool supports(DType t) const override { return t == DType::F32 || t == DType::F16; }
+  bool supports(DType t) const override;
   // Sizes the decode workspace for n_heads query heads at up to n_ctx positions. Shapes it cannot know from
   // ReserveParams (KV heads, head_dim) are sized by reserve_attention() or on first use.
   void reserve(const ReserveParams&) override;
@@ -124,6 +125,7 @@ class HipBackend final : public Backend {
     int64_t in = 0, rows = 0;
     const void* dev = nullptr;
     const void* key = nullptr;  // host data pointer of a kept copy; null for a weight used in place
+    int64_t bytes = 0;          // device bytes of a kept copy (quantized weights: the repacked planes)
     float* f32 = nullptr;       // kept copies only: widening of an F16 weight for the GEMM route
   };
   struct AppendRows {
@@ -169,6 +171,9 @@ class HipBackend final : public Backend {
   bool attention_fp32_ = false;
   float* ids_buf_ = nullptr;  // token ids of the last embed, on the device
   size_t ids_buf_bytes_ = 0;
+  float* acts_buf_ = nullptr;  // activations quantized for quantized weights
+  size_t acts_buf_bytes_ = 0;
+  std::vector<float*> ys_float_;  // outputs of a matmul_multi's float weights
 };
 
 }  // namespace nibble::hip

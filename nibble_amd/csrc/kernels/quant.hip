@@ -1,0 +1,523 @@
+// Quantized weight matmuls and dequantization on gfx950: Backend::matmul / matmul_multi / embed for the ggml block
+// formats Q4_0, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K (src/quant.h), bit-exact with the reference's scalar kernels
+// src/quant.cpp (itself llama.cpp's generic code) and hence with its AVX2 tier.
+//
+// A matmul never dequantizes the weights (ref_ops.cpp:109-135): each activation row is quantized to the weight
+// type's companion format (Q8_0, Q8_1 or Q8_K), and y[t, r] = sum over blocks b of a per-block term, summed in block
+// order. The integer part of every term is exact, so it is computed in any order (here with v_dot4 where it
+// applies); the float part - the scale products and the running sum over blocks - is the reference's expression,
+// evaluated with explicitly rounded operations (no contraction) and in its order:
+//   Q4_0  sum += (float(isum) * d_w) * d_a          quant.cpp:309-325
+//   Q8_0  sum += float(isum) * (d_w * d_a)          :329-342
+//   Q5_0  sum += (d_w * d_a) * float(isum)          :346-365
+//   Q5_1  sum += (d_w * d_a) * float(isum) + m_w * s_a  :369-390
+//   Q4_K / Q5_K (quant.cpp:118-144) and Q6_K (:394-416): eight int32 lanes (element e feeds lane e % 8) per
+//   super-block, sums[l] += (d_w * d_a) * float(aux[l]) in super-block order, Q4_K / Q5_K also sumf -= (dmin_w *
+//   d_a) * float(sumi) per super-block, and the eight sums added to sumf last.
+//
+// qgemv_kernel: one 64-lane wave per 4 weight rows and up to NT activation rows. Phase 1 spreads blocks over lanes
+// (a legacy block per lane; a K super-block over 8 lanes, one 32-element sub-block each, their integer partials
+// summed by shuffles) and writes each block's float term(s) to LDS; phase 2 gives each (row, activation row) pair
+// one lane, which adds its terms in block order. Weights arrive in the plane layout of quant_layout.h, so every
+// load is aligned (16-byte quant loads, 2-byte scales).
+#include <hip/hip_runtime.h>
+
+#include "backend/hip/kernel_timing.h"
+#include "kernels/quant_layout.h"
+#include "nibble_hip_shim.h"
+
+namespace {
+
+using namespace nbh_quant;
+
+constexpr int kRows = 4;  // weight rows per wave
+
+struct QW {
+  const uint8_t* q;
+  const uint8_t* h;
+  const uint8_t* s;
+  const uint16_t* d;
+  const uint16_t* m;
+  int64_t rows, nb;
+};
+struct QA {
+  const int8_t* qs;
+  const float* d;
+  const float* s;
+  const int16_t* bsums;
+  int64_t nb;
+};
+
+__device__ __forceinline__ float h2f(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }  // RNE
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4(int(a), int(b), c, false);
+}
+
+// ---- activation quantizers (quant.cpp:37-49, 245-303) ----
+
+// One thread per 32-element block of row t: Q8_0 (and Q8_1's sum term when Q81).
+template <bool Q81>
+__global__ __launch_bounds__(256) void quantize_q8_kernel(const float* __restrict__ x, int64_t in, int64_t n,
+                                                          int8_t* __restrict__ qs, float* __restrict__ dq,
+                                                          float* __restrict__ sq) {
+  const int64_t nb = in / 32;
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n * nb) return;
+  const float* xb = x + (i / nb) * in + (i % nb) * 32;
+  float v[32];
+  float amax = 0.f;
+  bool nan = false;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    v[j] = xb[j];
+    amax = fmaxf(amax, fabsf(v[j]));
+    nan |= v[j] != v[j];
+  }
+  const float d = nan ? __builtin_nanf("") : __fdiv_rn(amax, 127.f);
+  const float id = d != 0.f ? __fdiv_rn(1.0f, d) : 0.0f;
+  int sum = 0;
+  uint32_t packed[8];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float r = roundf(__fmul_rn(v[4 * w + e], id));
+      const int q = r != r ? 0 : int(fminf(127.f, fmaxf(-127.f, r)));
+      sum += q;
+      word |= uint32_t(q & 0xFF) << (8 * e);
+    }
+    packed[w] = word;
+  }
+  uint4* o = reinterpret_cast<uint4*>(qs + i * 32);
+  o[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  o[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+  dq[i] = h2f(f2h(d));
+  if constexpr (Q81) sq[i] = h2f(f2h(__fmul_rn(float(sum), d)));
+}
+
+// ggml nearest_int (quant.cpp:146-152): round half to even through the float mantissa.
+__device__ __forceinline__ int nearest_int(float f) {
+  const float val = __fadd_rn(f, 12582912.f);
+  return (__float_as_int(val) & 0x007fffff) - 0x00400000;
+}
+
+// One wave per 256-element super-block; lane l holds elements 4l..4l+3.
+__global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restrict__ x, int64_t in,
+                                                          int8_t* __restrict__ qs, float* __restrict__ dq,
+                                                          int16_t* __restrict__ bsums) {
+  const int64_t nb = in / 256, i = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* xb = x + (i / nb) * in + (i % nb) * 256;
+  const float v[4] = {xb[4 * lane], xb[4 * lane + 1], xb[4 * lane + 2], xb[4 * lane + 3]};
+  // the first element of largest magnitude (strictly greater replaces; NaN never does)
+  float amax = 0.f, mx = 0.f;
+  int idx = 1 << 30;
+  bool nan = false;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float ax = fabsf(v[e]);
+    if (ax > amax) amax = ax, mx = v[e], idx = 4 * lane + e;
+    nan |= v[e] != v[e];
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const float oa = __shfl_xor(amax, m, 64), om = __shfl_xor(mx, m, 64);
+    const int oi = __shfl_xor(idx, m, 64);
+    if (oa > amax || (oa == amax && oi < idx)) amax = oa, mx = om, idx = oi;
+  }
+  nan = __builtin_amdgcn_ballot_w64(nan) != 0;
+  uint32_t word = 0;
+  int part = 0;
+  float d = 0.f;
+  if (amax != 0.f) {
+    const float iscale = __fdiv_rn(-127.f, mx);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float s = __fmul_rn(iscale, v[e]);
+      const int q = s != s ? 0 : nearest_int(fminf(127.f, fmaxf(-127.f, s)));
+      part += q;
+      word |= uint32_t(q & 0xFF) << (8 * e);
+    }
+    d = __fdiv_rn(1.f, iscale);
+  }
+  part += __shfl_xor(part, 1, 64);
+  part += __shfl_xor(part, 2, 64);
+  reinterpret_cast<uint32_t*>(qs + i * 256)[lane] = word;
+  if ((lane & 3) == 0) bsums[i * 16 + lane / 4] = int16_t(part);
+  if (lane == 0) dq[i] = nan ? __builtin_nanf("") : d;
+}
+
+// ---- block terms ----
+
+__device__ __forceinline__ void load16(const uint8_t* p, uint32_t (&w)[4]) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+}
+
+// Legacy block b of weight row rr against activation row t: the block's float term.
+template <int T>
+__device__ __forceinline__ float legacy_term(const QW& W, const QA& A, int64_t rr, int64_t t, int64_t b) {
+  const int64_t wb = rr * W.nb + b, ab = t * A.nb + b;
+  uint32_t a[8];
+  {
+    const uint4* ap = reinterpret_cast<const uint4*>(A.qs + ab * 32);
+    const uint4 a0 = ap[0], a1 = ap[1];
+    a[0] = a0.x, a[1] = a0.y, a[2] = a0.z, a[3] = a0.w, a[4] = a1.x, a[5] = a1.y, a[6] = a1.z, a[7] = a1.w;
+  }
+  const float dw = h2f(W.d[wb]), da = A.d[ab];
+  if constexpr (T == kQ8_0) {
+    const uint4* wp = reinterpret_cast<const uint4*>(W.q + wb * 32);
+    const uint4 w0 = wp[0], w1 = wp[1];
+    int s = sdot4(w0.x, a[0], 0);
+    s = sdot4(w0.y, a[1], s), s = sdot4(w0.z, a[2], s), s = sdot4(w0.w, a[3], s);
+    s = sdot4(w1.x, a[4], s), s = sdot4(w1.y, a[5], s), s = sdot4(w1.z, a[6], s), s = sdot4(w1.w, a[7], s);
+    return __fmul_rn(float(s), __fmul_rn(dw, da));
+  } else {
+    uint32_t w[4];
+    load16(W.q + wb * 16, w);
+    // element j of the block: low nibble of byte j (j < 16), high nibble of byte j - 16 (j >= 16)
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo[i] = w[i] & 0x0F0F0F0Fu, hi[i] = (w[i] >> 4) & 0x0F0F0F0Fu;
+    if constexpr (T == kQ5_0 || T == kQ5_1) {
+      const uint32_t qh = *reinterpret_cast<const uint32_t*>(W.h + wb * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 4 * i + e;
+          lo[i] |= ((qh >> j) & 1u) << (8 * e + 4);
+          hi[i] |= ((qh >> (j + 16)) & 1u) << (8 * e + 4);
+        }
+    }
+    int s = 0, sa = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s = sdot4(lo[i], a[i], s), s = sdot4(hi[i], a[i + 4], s);
+    if constexpr (T == kQ4_0 || T == kQ5_0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sa = sdot4(a[i], 0x01010101u, sa);  // sum of the 32 activations
+    }
+    if constexpr (T == kQ4_0) return __fmul_rn(__fmul_rn(float(s - 8 * sa), dw), da);
+    if constexpr (T == kQ5_0) return __fmul_rn(__fmul_rn(dw, da), float(s - 16 * sa));
+    if constexpr (T == kQ5_1)
+      return __fadd_rn(__fmul_rn(__fmul_rn(dw, da), float(s)), __fmul_rn(h2f(W.m[wb]), A.s[ab]));
+  }
+  return 0.f;
+}
+
+// ggml get_scale_min_k4 (quant.cpp:52-61)
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& d, int& m) {
+  if (j < 4) {
+    d = q[j] & 63;
+    m = q[j + 4] & 63;
+  } else {
+    d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+    m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+// The integer partials of sub-block k (elements 32k..32k+31) of super-block sb, row rr, activation row t:
+// aux[l] = sum over its elements e with e % 8 == l of scale(e) * (a_e * q_e), and (Q4_K / Q5_K) sumi's share.
+template <int T>
+__device__ __forceinline__ void k_partials(const QW& W, const QA& A, int64_t rr, int64_t t, int64_t sb, int k,
+                                           int (&aux)[8], int& sumi) {
+  const int64_t wb = rr * W.nb + sb, ab = t * A.nb + sb;
+  const int8_t* a = A.qs + ab * 256 + 32 * k;
+  int8_t av[32];
+  {
+    const uint4* ap = reinterpret_cast<const uint4*>(a);
+    const uint4 a0 = ap[0], a1 = ap[1];
+    *reinterpret_cast<uint4*>(av) = a0;
+    *reinterpret_cast<uint4*>(av + 16) = a1;
+  }
+  int q[32];
+  int sc_lo, sc_hi;
+  if constexpr (T == kQ4_K || T == kQ5_K) {
+    const uint8_t* qs = W.q + wb * 128 + 32 * (k >> 1);
+    const int shift = 4 * (k & 1);
+    uint8_t qb[32];
+    *reinterpret_cast<uint4*>(qb) = reinterpret_cast<const uint4*>(qs)[0];
+    *reinterpret_cast<uint4*>(qb + 16) = reinterpret_cast<const uint4*>(qs)[1];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) q[e] = (qb[e] >> shift) & 0xF;
+    if constexpr (T == kQ5_K) {
+      uint8_t hb[32];
+      const uint8_t* qh = W.h + wb * 32;
+      *reinterpret_cast<uint4*>(hb) = reinterpret_cast<const uint4*>(qh)[0];
+      *reinterpret_cast<uint4*>(hb + 16) = reinterpret_cast<const uint4*>(qh)[1];
+#pragma unroll
+      for (int e = 0; e < 32; ++e) q[e] += ((hb[e] >> k) & 1) ? 16 : 0;
+    }
+    int sc, m;
+    scale_min_k4(k, W.s + wb * 16, sc, m);
+    sc_lo = sc_hi = sc;
+    const int16_t* bs = A.bsums + ab * 16;
+    sumi = (int(bs[2 * k]) + int(bs[2 * k + 1])) * m;
+  } else {  // Q6_K: sub-block k = 4h + g of the 128-element half h (quant.cpp:84-96)
+    const int h = k >> 2, g = k & 3;
+    const uint8_t* ql = W.q + wb * 128 + 64 * h + 32 * (g & 1);
+    const uint8_t* qh = W.h + wb * 64 + 32 * h;
+    uint8_t lb[32], hb[32];
+    *reinterpret_cast<uint4*>(lb) = reinterpret_cast<const uint4*>(ql)[0];
+    *reinterpret_cast<uint4*>(lb + 16) = reinterpret_cast<const uint4*>(ql)[1];
+    *reinterpret_cast<uint4*>(hb) = reinterpret_cast<const uint4*>(qh)[0];
+    *reinterpret_cast<uint4*>(hb + 16) = reinterpret_cast<const uint4*>(qh)[1];
+    const int ls = (g >> 1) * 4, hs = 2 * g;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) q[e] = (((lb[e] >> ls) & 0xF) | (((hb[e] >> hs) & 3) << 4)) - 32;
+    const int8_t* scl = reinterpret_cast<const int8_t*>(W.s + wb * 16);
+    sc_lo = scl[2 * k];
+    sc_hi = scl[2 * k + 1];
+    sumi = 0;
+  }
+#pragma unroll
+  for (int l = 0; l < 8; ++l) aux[l] = 0;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) aux[e & 7] += (e < 16 ? sc_lo : sc_hi) * (int(av[e]) * q[e]);
+}
+
+// ---- the matmul ----
+
+template <int T, int NT>
+__global__ __launch_bounds__(64) void qgemv_kernel(QW W, QA A, float* __restrict__ y, int n) {
+  constexpr int O = kRows * NT;  // outputs of this wave
+  constexpr bool K = T == kQ4_K || T == kQ5_K || T == kQ6_K;
+  constexpr int CH = K ? 8 : 64;  // blocks per chunk
+  constexpr int TERMS = K ? 9 : 1;
+  __shared__ float terms[O][CH][TERMS];
+  const int lane = threadIdx.x;
+  const int64_t r0 = int64_t(blockIdx.x) * kRows;
+  const int nr = int(W.rows - r0 < kRows ? W.rows - r0 : kRows);
+  float acc = 0.f, sums[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) sums[l] = 0.f;
+  for (int64_t c0 = 0; c0 < W.nb; c0 += CH) {
+    const int nc = int(W.nb - c0 < CH ? W.nb - c0 : CH);
+    // phase 1: block terms
+    if constexpr (!K) {
+      if (lane < nc) {
+        for (int r = 0; r < kRows; ++r) {
+          const int64_t rr = r0 + (r < nr ? r : nr - 1);
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            if (t < n) terms[r * NT + t][lane][0] = legacy_term<T>(W, A, rr, t, c0 + lane);
+        }
+      }
+    } else {
+      const int sbl = lane >> 3, k = lane & 7;
+      const bool live = sbl < nc;
+      const int64_t sb = c0 + (live ? sbl : 0);
+      for (int r = 0; r < kRows; ++r) {
+        const int64_t rr = r0 + (r < nr ? r : nr - 1);
+        for (int t = 0; t < NT; ++t) {
+          if (t >= n) break;
+          int aux[8], sumi;
+          k_partials<T>(W, A, rr, t, sb, k, aux, sumi);
+#pragma unroll
+          for (int m = 1; m < 8; m <<= 1) {
+#pragma unroll
+            for (int l = 0; l < 8; ++l) aux[l] += __shfl_xor(aux[l], m, 64);
+            sumi += __shfl_xor(sumi, m, 64);
+          }
+          if (live && k == 0) {
+            const int64_t wb = rr * W.nb + sb, ab = int64_t(t) * A.nb + sb;
+            const float d = __fmul_rn(h2f(W.d[wb]), A.d[ab]);
+#pragma unroll
+            for (int l = 0; l < 8; ++l) terms[r * NT + t][sbl][l] = __fmul_rn(d, float(aux[l]));
+            terms[r * NT + t][sbl][8] =
+                T == kQ6_K ? 0.f : __fmul_rn(__fmul_rn(h2f(W.m[wb]), A.d[ab]), float(sumi));
+          }
+        }
+      }
+    }
+    __syncthreads();
+    // phase 2: each output adds its terms in block order
+    if (lane < O) {
+      if constexpr (!K) {
+        for (int b = 0; b < nc; ++b) acc = __fadd_rn(acc, terms[lane][b][0]);
+      } else {
+        for (int b = 0; b < nc; ++b) {
+#pragma unroll
+          for (int l = 0; l < 8; ++l) sums[l] = __fadd_rn(sums[l], terms[lane][b][l]);
+          if constexpr (T != kQ6_K) acc = __fsub_rn(acc, terms[lane][b][8]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (lane < O) {
+    if constexpr (K) {
+#pragma unroll
+      for (int l = 0; l < 8; ++l) acc = __fadd_rn(acc, sums[l]);
+    }
+    const int r = lane / NT, t = lane % NT;
+    if (r < nr && t < n) y[int64_t(t) * W.rows + r0 + r] = acc;
+  }
+}
+
+// ---- dequantization (quant.cpp:157-242), one thread per block of one output row ----
+
+template <int T>
+__global__ __launch_bounds__(256) void dequant_rows_kernel(QW W, const int32_t* __restrict__ ids, int64_t n,
+                                                           float* __restrict__ out) {
+  const int64_t be = block_elems(T), d_ = W.nb * be;
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n * W.nb) return;
+  const int64_t t = i / W.nb, b = i % W.nb, wb = int64_t(ids[t]) * W.nb + b;
+  float* o = out + t * d_ + b * be;
+  const float d = h2f(W.d[wb]);
+  if constexpr (T == kQ8_0) {
+    const int8_t* q = reinterpret_cast<const int8_t*>(W.q + wb * 32);
+    for (int j = 0; j < 32; ++j) o[j] = __fmul_rn(float(q[j]), d);
+  } else if constexpr (T == kQ4_0 || T == kQ5_0 || T == kQ5_1) {
+    const uint8_t* q = W.q + wb * 16;
+    const uint32_t qh = T == kQ4_0 ? 0u : *reinterpret_cast<const uint32_t*>(W.h + wb * 4);
+    const float m = T == kQ5_1 ? h2f(W.m[wb]) : 0.f;
+    for (int j = 0; j < 16; ++j) {
+      int x0 = q[j] & 0x0F, x1 = q[j] >> 4;
+      if constexpr (T != kQ4_0) x0 |= ((qh >> j) & 1) << 4, x1 |= ((qh >> (j + 16)) & 1) << 4;
+      if constexpr (T == kQ5_1) {
+        o[j] = __fadd_rn(__fmul_rn(float(x0), d), m);
+        o[j + 16] = __fadd_rn(__fmul_rn(float(x1), d), m);
+      } else {
+        constexpr int bias = T == kQ4_0 ? 8 : 16;
+        o[j] = __fmul_rn(float(x0 - bias), d);
+        o[j + 16] = __fmul_rn(float(x1 - bias), d);
+      }
+    }
+  } else if constexpr (T == kQ4_K || T == kQ5_K) {
+    const uint8_t* qs = W.q + wb * 128;
+    const float mn = h2f(W.m[wb]);
+    for (int k = 0; k < 8; ++k) {
+      int sc, m;
+      scale_min_k4(k, W.s + wb * 16, sc, m);
+      const float d1 = __fmul_rn(d, float(sc)), m1 = __fmul_rn(mn, float(m));
+      for (int e = 0; e < 32; ++e) {
+        int q = (qs[32 * (k >> 1) + e] >> (4 * (k & 1))) & 0xF;
+        if constexpr (T == kQ5_K) q += ((W.h[wb * 32 + e] >> k) & 1) ? 16 : 0;
+        o[32 * k + e] = __fsub_rn(__fmul_rn(d1, float(q)), m1);
+      }
+    }
+  } else {  // Q6_K
+    const int8_t* scl = reinterpret_cast<const int8_t*>(W.s + wb * 16);
+    for (int k = 0; k < 8; ++k) {
+      const int h = k >> 2, g = k & 3;
+      const uint8_t* ql = W.q + wb * 128 + 64 * h + 32 * (g & 1);
+      const uint8_t* qh = W.h + wb * 64 + 32 * h;
+      for (int e = 0; e < 32; ++e) {
+        const int q = (((ql[e] >> ((g >> 1) * 4)) & 0xF) | (((qh[e] >> (2 * g)) & 3) << 4)) - 32;
+        const float dk = __fmul_rn(d, float(scl[2 * k + (e >> 4)]));
+        o[32 * k + e] = __fmul_rn(dk, float(q));
+      }
+    }
+  }
+}
+
+QW weight_of(int type, const void* w, int64_t rows, int64_t in) {
+  const int64_t nb = in / block_elems(type);
+  const WeightLayout l = weight_layout(type, rows, nb);
+  const uint8_t* base = static_cast<const uint8_t*>(w);
+  return QW{base + l.q_off, base + l.h_off, base + l.s_off, reinterpret_cast<const uint16_t*>(base + l.d_off),
+            reinterpret_cast<const uint16_t*>(base + l.m_off), rows, nb};
+}
+
+template <int T>
+int launch_gemv(const QW& W, const QA& A, float* y, int64_t n, hipStream_t s) {
+  const dim3 grid{unsigned((W.rows + kRows - 1) / kRows), 1, 1}, block{64, 1, 1};
+  if (n == 1) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 1>, grid, block, s, W, A, y, int(n));
+  if (n <= 4) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4>, grid, block, s, W, A, y, int(n));
+  return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 16>, grid, block, s, W, A, y, int(n));
+}
+
+template <int T>
+int launch_dequant(const QW& W, const int32_t* ids, int64_t n, float* out, hipStream_t s) {
+  const int64_t blocks = (n * W.nb + 255) / 256;
+  return nbhs_timing::launch(NBHS_K_ELEMENTWISE, dequant_rows_kernel<T>, dim3(unsigned(blocks)), dim3(256), s, W, ids,
+                             n, out);
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t nbhs_quant_weight_bytes(int type, int64_t rows, int64_t in) {
+  if (!is_quant(type) || rows <= 0 || in <= 0 || in % block_elems(type)) return -1;
+  return weight_layout(type, rows, in / block_elems(type)).bytes;
+}
+
+int64_t nbhs_quant_act_bytes(int type, int64_t n, int64_t in) {
+  if (!is_quant(type) || n <= 0 || in <= 0 || in % block_elems(type)) return -1;
+  return act_layout(act_of(type), n, in / block_elems(type)).bytes;
+}
+
+int nbhs_quantize_acts(int type, const float* x, int64_t n, int64_t in, void* acts, nbhs_stream stream) {
+  if (!is_quant(type) || !x || !acts || n <= 0 || in <= 0 || in % block_elems(type)) return NBHS_EINVAL;
+  const int act = act_of(type);
+  const int64_t nb = in / block_elems(type), blocks = n * nb;
+  const ActLayout l = act_layout(act, n, nb);
+  uint8_t* base = static_cast<uint8_t*>(acts);
+  int8_t* qs = reinterpret_cast<int8_t*>(base + l.qs_off);
+  float* d = reinterpret_cast<float*>(base + l.d_off);
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (act == kActQ8_K) {
+    if (blocks >= (int64_t(1) << 31)) return NBHS_EINVAL;
+    return nbhs_timing::launch(NBHS_K_QUANTIZE, quantize_q8k_kernel, dim3(unsigned(blocks)), dim3(64), s, x, in, qs, d,
+                               reinterpret_cast<int16_t*>(base + l.bsums_off));
+  }
+  const dim3 grid{unsigned((blocks + 255) / 256), 1, 1};
+  if (act == kActQ8_1)
+    return nbhs_timing::launch(NBHS_K_QUANTIZE, quantize_q8_kernel<true>, grid, dim3(256), s, x, in, n, qs, d,
+                               reinterpret_cast<float*>(base + l.s_off));
+  return nbhs_timing::launch(NBHS_K_QUANTIZE, quantize_q8_kernel<false>, grid, dim3(256), s, x, in, n, qs, d,
+                             static_cast<float*>(nullptr));
+}
+
+int nbhs_qgemv(int type, const void* w, int64_t rows, int64_t in, const void* acts, int64_t n_acts, int64_t t0,
+               int64_t n, float* y, nbhs_stream stream) {
+  if (!is_quant(type) || !w || !acts || !y || rows <= 0 || in <= 0 || in % block_elems(type) || n <= 0 ||
+      n > NBHS_GEMV_MAX_ROWS || t0 < 0 || t0 + n > n_acts || (rows + kRows - 1) / kRows >= (int64_t(1) << 31))
+    return NBHS_EINVAL;
+  const QW W = weight_of(type, w, rows, in);
+  const int act = act_of(type);
+  const ActLayout l = act_layout(act, n_acts, W.nb);
+  const uint8_t* base = static_cast<const uint8_t*>(acts);
+  const int64_t b0 = t0 * W.nb;  // first block of activation row t0
+  const QA A{reinterpret_cast<const int8_t*>(base + l.qs_off) + b0 * (act == kActQ8_K ? 256 : 32),
+             reinterpret_cast<const float*>(base + l.d_off) + b0, reinterpret_cast<const float*>(base + l.s_off) + b0,
+             reinterpret_cast<const int16_t*>(base + l.bsums_off) + b0 * 16, W.nb};
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (type) {
+    case kQ4_0: return launch_gemv<kQ4_0>(W, A, y, n, s);
+    case kQ5_0: return launch_gemv<kQ5_0>(W, A, y, n, s);
+    case kQ5_1: return launch_gemv<kQ5_1>(W, A, y, n, s);
+    case kQ8_0: return launch_gemv<kQ8_0>(W, A, y, n, s);
+    case kQ4_K: return launch_gemv<kQ4_K>(W, A, y, n, s);
+    case kQ5_K: return launch_gemv<kQ5_K>(W, A, y, n, s);
+    case kQ6_K: return launch_gemv<kQ6_K>(W, A, y, n, s);
+    default: return NBHS_EINVAL;
+  }
+}
+
+int nbhs_dequant_rows(int type, const void* w, int64_t rows, int64_t in, const int32_t* ids, int64_t n, float* out,
+                      nbhs_stream stream) {
+  if (!is_quant(type) || !w || !ids || !out || rows <= 0 || in <= 0 || in % block_elems(type) || n <= 0)
+    return NBHS_EINVAL;
+  const QW W = weight_of(type, w, rows, in);
+  if ((n * W.nb + 255) / 256 >= (int64_t(1) << 31)) return NBHS_EINVAL;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (type) {
+    case kQ4_0: return launch_dequant<kQ4_0>(W, ids, n, out, s);
+    case kQ5_0: return launch_dequant<kQ5_0>(W, ids, n, out, s);
+    case kQ5_1: return launch_dequant<kQ5_1>(W, ids, n, out, s);
+    case kQ8_0: return launch_dequant<kQ8_0>(W, ids, n, out, s);
+    case kQ4_K: return launch_dequant<kQ4_K>(W, ids, n, out, s);
+    case kQ5_K: return launch_dequant<kQ5_K>(W, ids, n, out, s);
+    case kQ6_K: return launch_dequant<kQ6_K>(W, ids, n, out, s);
+    default: return NBHS_EINVAL;
+  }
+}
+
+}  // extern "C"

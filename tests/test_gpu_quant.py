@@ -1,0 +1,134 @@
+"""GPU quantized weights: Backend::matmul / matmul_multi / embed for Q4_0, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K and Q6_K,
+through the C ABI, bit for bit against the oracle's restatement of quant.cpp (itself pinned to the reference's
+golden vectors and to the compiled reference, tests/test_quant_oracle.py), and a quantized tiny model against the
+fp64 naive model on the dequantized weights with the reference's own bar (tests/test_model.cpp:206-233: cosine >=
+0.999 and the same argmax)."""
+import numpy as np
+import pytest
+
+import nibble_amd
+import oracle
+from oracle import naive_model
+from tests import model_util
+from tests import quant_util as U
+from tests.gpu_util import Buffers, bits
+
+pytestmark = pytest.mark.gpu
+TYPES = list(U.NAMES)
+
+
+@pytest.mark.parametrize("t", TYPES, ids=[U.NAMES[t] for t in TYPES])
+@pytest.mark.parametrize("n", [1, 3, 16, 17, 40])
+def test_quant_matmul_bit_exact(backend, t, n):
+    """Activation quantization and the block dots, every activation-row chunking (n <= 16 and beyond)."""
+    be_ = oracle.block_elems(t)
+    in_ = 2 * 256 if be_ == 256 else 7 * 32 + 32 * 64  # two super-blocks / 71 legacy blocks (a partial chunk)
+    rows = 37  # not a multiple of the 4 rows per wave
+    w = U.random_qmat(t, rows, in_, seed=1000 + t)
+    x = (np.random.default_rng(n + t).standard_normal((n, in_)) * 3).astype(np.float32)
+    x[0, :5] = [0.0, 1e-3, -7.0, 2.5, -2.5]
+    with Buffers(backend) as B:
+        dx, dy = B.upload(x), B.alloc(n * rows)
+        backend.matmul(w, dx, dy, n)
+        got = backend.download(dy, (n, rows))
+    ref = oracle.matmul_q(t, w.raw, in_, rows, x)
+    diff = int(np.sum(bits(got) != bits(ref)))
+    print(f"{U.NAMES[t]} n={n}: {diff} of {got.size} outputs differ from the restated reference", flush=True)
+    assert diff == 0
+    backend.release_weights()
+
+
+def test_quant_matmul_multi_mixed_types(backend):
+    """A Q4_K_M-style projection: wq, wk Q4_K and wv Q6_K sharing one quantized input, plus an F16 and a Q8_0
+    weight in the same call (their own paths), into separate outputs."""
+    in_, n = 512, 5
+    ws = [U.random_qmat(oracle.Q4_K, 64, in_, 1), U.random_qmat(oracle.Q4_K, 16, in_, 2),
+          U.random_qmat(oracle.Q6_K, 16, in_, 3), U.random_qmat(oracle.Q8_0, 8, in_, 4)]
+    w16 = (np.random.default_rng(1).standard_normal((24, in_)) * 0.1).astype(np.float16)
+    x = np.random.default_rng(2).standard_normal((n, in_)).astype(np.float32)
+    with Buffers(backend) as B:
+        dx = B.upload(x)
+        ys = [B.alloc(n * w.rows) for w in ws] + [B.alloc(n * 24)]
+        backend.matmul_multi(ws + [w16], dx, ys, n)
+        got = [backend.download(y, (n, w.rows)) for y, w in zip(ys, ws)]
+        got16 = backend.download(ys[-1], (n, 24))
+    for g, w in zip(got, ws):
+        assert np.array_equal(bits(g), bits(oracle.matmul_q(w.t, w.raw, in_, w.rows, x))), U.NAMES[w.t]
+    exact = x.astype(np.float64) @ w16.astype(np.float64).T
+    assert np.all(np.abs(got16 - exact) <= in_ * 2.0 ** -24 * (np.abs(x) @ np.abs(w16.astype(np.float64)).T) + 1e-30)
+    backend.release_weights()
+
+
+@pytest.mark.parametrize("t", TYPES, ids=[U.NAMES[t] for t in TYPES])
+def test_quant_embed_bit_exact(backend, t):
+    d = 512 if oracle.block_elems(t) == 256 else 96
+    table = U.random_qmat(t, 50, d, seed=77 + t)
+    ids = np.array([0, 49, 3, 3, 17], np.int32)
+    with Buffers(backend) as B:
+        out = B.alloc(ids.size * d)
+        backend.embed(table, ids, out)
+        got = backend.download(out, (ids.size, d))
+    ref = np.asarray(table)[ids]
+    assert np.array_equal(bits(got), bits(ref))
+    backend.release_weights()
+
+
+def test_quant_non_finite_activations(backend):
+    """A NaN in an activation block makes its scale NaN (quant.cpp:37-49, 273-303): every output that reads the
+    block is NaN, as in the reference; rows without it stay finite and exact."""
+    for t in (oracle.Q8_0, oracle.Q4_K):
+        in_ = 512
+        w = U.random_qmat(t, 8, in_, seed=5)
+        x = np.random.default_rng(0).standard_normal((2, in_)).astype(np.float32)
+        x[1, 300] = np.nan
+        with Buffers(backend) as B:
+            dx, dy = B.upload(x), B.alloc(2 * 8)
+            backend.matmul(w, dx, dy, 2)
+            got = backend.download(dy, (2, 8))
+        ref = oracle.matmul_q(t, w.raw, in_, 8, x)
+        assert np.all(np.isnan(got[1])) and np.all(np.isnan(ref[1]))
+        assert np.array_equal(bits(got[0]), bits(ref[0]))
+    backend.release_weights()
+
+
+def test_quant_rejects_bad_shapes(backend):
+    with Buffers(backend) as B:
+        dx, dy = B.alloc(64), B.alloc(64)
+        bad = U.QMat(oracle.Q4_0, np.zeros(18 * 4, np.uint8), 2, 48)  # 48 is not a multiple of 32
+        with pytest.raises(nibble_amd.BackendError, match="not a multiple"):
+            backend.matmul(bad, dx, dy, 1)
+        dev = B.alloc(64)
+        with pytest.raises(nibble_amd.BackendError, match="host memory"):
+            backend.matmul(nibble_amd.weight(dev, shape=(1, 32), dtype=oracle.Q8_0), dx, dy, 1)
+    assert all(backend.supports(t) for t in TYPES + [0, 1])
+
+
+@pytest.mark.parametrize("t", [oracle.Q8_0, oracle.Q4_0], ids=["Q8_0", "Q4_0"])
+def test_quantized_tiny_model_matches_naive(backend, t):
+    """tests/test_model.cpp:206-233 on the GPU: the reference's quant_dims tiny model (n_embd 32, n_ff 64, head_dim
+    8) with every matrix quantized, against the fp64 naive model on the dequantized weights."""
+    m = model_util.tiny_model(7, np.float32, "qwen2", False, E=32, FF=64)
+    m["token_embd"] = U.quantize_matrix(m["token_embd"], t)
+    for L in m["layers"]:
+        for k in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
+            L[k] = U.quantize_matrix(L[k], t)
+    toks = [1, 50, 257, 3, 99]
+    g = model_util.GpuModel(backend, m, n_ctx=64)
+    try:
+        got = g.forward(toks)
+        inc = None
+        g2 = model_util.GpuModel(backend, m, n_ctx=64)
+        try:
+            for i, tok in enumerate(toks):
+                inc = g2.forward([tok], pos0=i)
+        finally:
+            g2.close()
+    finally:
+        g.close()
+    ref = naive_model.naive_logits(m, toks)
+    cos = float(np.dot(got, ref) / np.sqrt(np.dot(got, got) * np.dot(ref, ref)))
+    print(f"{U.NAMES[t]} tiny model: cosine vs naive {cos:.6f}, argmax {int(np.argmax(got))} vs "
+          f"{int(np.argmax(ref))}; incremental max |diff| {np.max(np.abs(inc - got)):.2e}", flush=True)
+    assert cos >= 0.999
+    assert int(np.argmax(got)) == int(np.argmax(ref))
+    assert np.all(np.isfinite(inc))
