@@ -186,10 +186,12 @@ int64_t nbhs_quant_weight_bytes(int type, int64_t rows, int64_t in); /* -1 when 
 int64_t nbhs_quant_act_bytes(int type, int64_t n, int64_t in);
 /* The n x in activation rows x quantized to type's companion format (quant.cpp:37-49, 245-303), bit-exact. */
 int nbhs_quantize_acts(int type, const float* x, int64_t n, int64_t in, void* acts, nbhs_stream s);
-/* y[t * rows + r] for t < n (n <= 16): the block dot of weight row r with activation row t0 + t of the n_acts rows
- * quantized into acts (quant.cpp:305-419, same bits). */
-int nbhs_qgemv(int type, const void* w, int64_t rows, int64_t in, const void* acts, int64_t n_acts, int64_t t0,
-               int64_t n, float* y, nbhs_stream s);
+/* For each of n_w (<= 8) weights of one type sharing the input, y[i][t * rows[i] + r] for t < n (n <= 16): the
+ * block dot of weight row r with activation row t0 + t (quant.cpp:305-419, same bits). The activations are the
+ * n_acts rows quantized into acts by nbhs_quantize_acts; or, with acts NULL (n <= 4, t0 = 0, x 16-byte aligned),
+ * rows of x quantized inside the launch (the same bits). */
+int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* rows, float* const* y, int64_t in,
+                     const float* x, const void* acts, int64_t n_acts, int64_t t0, int64_t n, nbhs_stream s);
 /* out[t, :] = dequantized row ids[t] (device ids) of the weight, quant.cpp:157-242 bit for bit. */
 int nbhs_dequant_rows(int type, const void* w, int64_t rows, int64_t in, const int32_t* ids, int64_t n, float* out,
                       nbhs_stream s);

@@ -359,28 +359,48 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
     if (ya < xa + uint64_t(x_count) * 4 && xa < ya + uint64_t(y_count) * 4)
       throw Error("matmul: output " + str(int64_t(i)) + " overlaps the input");
   }
-  // Quantized weights: x is quantized once per activation format and every weight takes the block-dot kernel in
-  // chunks of up to 16 activation rows (ref_ops.cpp:109-135, CpuBackend::matmul_multi's shared quantization).
+  // Quantized weights (ref_ops.cpp:109-135): the weights of one type share one launch per chunk of up to 16
+  // activation rows. Up to 4 rows are quantized inside that launch; more are quantized once per activation format
+  // first, as CpuBackend::matmul_multi quantizes the shared input once (cpu_backend.cpp:146-240).
   std::vector<size_t> fl;
-  int done_act = -1;
+  std::vector<int> types;
   for (size_t i = 0; i < dw.size(); ++i) {
     const int t = int(dw[i].type);
-    if (!nbh_quant::is_quant(t)) {
+    if (!nbh_quant::is_quant(t))
       fl.push_back(i);
-      continue;
-    }
-    const int act = nbh_quant::act_of(t);
-    const int64_t ab = nbhs_quant_act_bytes(t, n, in);
-    if (ab < 0) throw Error("matmul: invalid quantized shape");
-    if (act != done_act) {
+    else if (std::find(types.begin(), types.end(), t) == types.end())
+      types.push_back(t);
+  }
+  const bool fuse = n <= 4 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && in % 4 == 0;
+  int done_act = -1;
+  for (const int t : types) {
+    if (!fuse && nbh_quant::act_of(t) != done_act) {
+      const int64_t ab = nbhs_quant_act_bytes(t, n, in);
+      if (ab < 0) throw Error("matmul: invalid quantized shape");
       ensure(acts_buf_, acts_buf_bytes_, size_t(ab));
       check(nbhs_quantize_acts(t, x, n, in, acts_buf_, stream_), "matmul (activation quantization)");
-      done_act = act;
+      done_act = nbh_quant::act_of(t);
     }
-    for (int64_t t0 = 0; t0 < n; t0 += kGemvMaxRows)
-      check(nbhs_qgemv(t, dw[i].dev, dw[i].rows, in, acts_buf_, n, t0, std::min(kGemvMaxRows, n - t0),
-                       ys[i] + t0 * dw[i].rows, stream_),
-            "matmul (quantized)");
+    std::vector<size_t> idx;
+    for (size_t i = 0; i < dw.size(); ++i)
+      if (int(dw[i].type) == t) idx.push_back(i);
+    for (size_t b = 0; b < idx.size(); b += kGemvMaxWeights) {
+      const size_t cnt = std::min(idx.size() - b, kGemvMaxWeights);
+      const void* wp[kGemvMaxWeights];
+      int64_t rows[kGemvMaxWeights];
+      float* yp[kGemvMaxWeights];
+      for (int64_t t0 = 0; t0 < n; t0 += kGemvMaxRows) {
+        for (size_t j = 0; j < cnt; ++j) {
+          const size_t i = idx[b + j];
+          wp[j] = dw[i].dev;
+          rows[j] = dw[i].rows;
+          yp[j] = ys[i] + t0 * dw[i].rows;
+        }
+        check(nbhs_qgemv_multi(t, int(cnt), wp, rows, yp, in, x, fuse ? nullptr : acts_buf_, n, t0,
+                               std::min(kGemvMaxRows, n - t0), stream_),
+              "matmul (quantized)");
+      }
+    }
   }
   if (fl.size() != dw.size()) {
     std::vector<DeviceWeight> fw;

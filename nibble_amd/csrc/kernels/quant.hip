@@ -150,34 +150,158 @@ __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restric
   if (lane == 0) dq[i] = nan ? __builtin_nanf("") : d;
 }
 
-// ---- block terms ----
+// ---- activation blocks in registers ----
 
-__device__ __forceinline__ void load16(const uint8_t* p, uint32_t (&w)[4]) {
-  const uint4 v = *reinterpret_cast<const uint4*>(p);
-  w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+// One legacy activation block (32 quants as 8 words), its scale d (fp16-rounded, widened), Q8_1's s, and the sum
+// of its quants (for the Q4_0 / Q5_0 offsets).
+struct ActL {
+  uint32_t a[8];
+  float d, s;
+  int sum;
+};
+
+__device__ __forceinline__ ActL load_act_l(const QA& A, int64_t t, int64_t b) {
+  ActL r;
+  const int64_t ab = t * A.nb + b;
+  const uint4* ap = reinterpret_cast<const uint4*>(A.qs + ab * 32);
+  const uint4 a0 = ap[0], a1 = ap[1];
+  r.a[0] = a0.x, r.a[1] = a0.y, r.a[2] = a0.z, r.a[3] = a0.w, r.a[4] = a1.x, r.a[5] = a1.y, r.a[6] = a1.z,
+  r.a[7] = a1.w;
+  r.d = A.d[ab];
+  r.s = A.s ? A.s[ab] : 0.f;
+  r.sum = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r.sum = sdot4(r.a[i], 0x01010101u, r.sum);
+  return r;
 }
 
-// Legacy block b of weight row rr against activation row t: the block's float term.
-template <int T>
-__device__ __forceinline__ float legacy_term(const QW& W, const QA& A, int64_t rr, int64_t t, int64_t b) {
-  const int64_t wb = rr * W.nb + b, ab = t * A.nb + b;
-  uint32_t a[8];
-  {
-    const uint4* ap = reinterpret_cast<const uint4*>(A.qs + ab * 32);
-    const uint4 a0 = ap[0], a1 = ap[1];
-    a[0] = a0.x, a[1] = a0.y, a[2] = a0.z, a[3] = a0.w, a[4] = a1.x, a[5] = a1.y, a[6] = a1.z, a[7] = a1.w;
+// quantize_block_q8 (quant.cpp:37-49) of the 32 floats at xb, in registers: the same bits quantize_q8_kernel writes.
+template <bool Q81>
+__device__ __forceinline__ ActL quant_act_l(const float* xb) {
+  float v[32];
+  float amax = 0.f;
+  bool nan = false;
+#pragma unroll
+  for (int j = 0; j < 32; j += 4) {
+    const float4 f = *reinterpret_cast<const float4*>(xb + j);
+    v[j] = f.x, v[j + 1] = f.y, v[j + 2] = f.z, v[j + 3] = f.w;
   }
-  const float dw = h2f(W.d[wb]), da = A.d[ab];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    amax = fmaxf(amax, fabsf(v[j]));
+    nan |= v[j] != v[j];
+  }
+  const float d = nan ? __builtin_nanf("") : __fdiv_rn(amax, 127.f);
+  const float id = d != 0.f ? __fdiv_rn(1.0f, d) : 0.0f;
+  ActL r;
+  r.sum = 0;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float q = roundf(__fmul_rn(v[4 * w + e], id));
+      const int qi = q != q ? 0 : int(fminf(127.f, fmaxf(-127.f, q)));
+      r.sum += qi;
+      word |= uint32_t(qi & 0xFF) << (8 * e);
+    }
+    r.a[w] = word;
+  }
+  r.d = h2f(f2h(d));
+  r.s = Q81 ? h2f(f2h(__fmul_rn(float(r.sum), d))) : 0.f;
+  return r;
+}
+
+// One 32-element sub-block k of a Q8_K activation super-block: its quants, the block scale d and the two 16-sums.
+struct ActK {
+  uint32_t a[8];
+  float d;
+  int bs0, bs1;
+};
+
+__device__ __forceinline__ ActK load_act_k(const QA& A, int64_t t, int64_t sb, int k) {
+  ActK r;
+  const int64_t ab = t * A.nb + sb;
+  const uint4* ap = reinterpret_cast<const uint4*>(A.qs + ab * 256 + 32 * k);
+  const uint4 a0 = ap[0], a1 = ap[1];
+  r.a[0] = a0.x, r.a[1] = a0.y, r.a[2] = a0.z, r.a[3] = a0.w, r.a[4] = a1.x, r.a[5] = a1.y, r.a[6] = a1.z,
+  r.a[7] = a1.w;
+  r.d = A.d[ab];
+  r.bs0 = A.bsums[ab * 16 + 2 * k];
+  r.bs1 = A.bsums[ab * 16 + 2 * k + 1];
+  return r;
+}
+
+// quantize_row_q8_K (quant.cpp:273-303) for the super-block spread over the 8 lanes of this lane's group (lane k
+// holds elements 32k..32k+31 at xs): the first element of largest magnitude sets the scale. All 64 lanes call it.
+__device__ __forceinline__ ActK quant_act_k(const float* xs, int k) {
+  float v[32];
+#pragma unroll
+  for (int j = 0; j < 32; j += 4) {
+    const float4 f = *reinterpret_cast<const float4*>(xs + j);
+    v[j] = f.x, v[j + 1] = f.y, v[j + 2] = f.z, v[j + 3] = f.w;
+  }
+  float amax = 0.f, mx = 0.f;
+  int idx = 1 << 30;
+  bool nan = false;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const float ax = fabsf(v[e]);
+    if (ax > amax) amax = ax, mx = v[e], idx = 32 * k + e;
+    nan |= v[e] != v[e];
+  }
+  int nanf = nan ? 1 : 0;
+#pragma unroll
+  for (int m = 1; m < 8; m <<= 1) {
+    const float oa = __shfl_xor(amax, m, 64), om = __shfl_xor(mx, m, 64);
+    const int oi = __shfl_xor(idx, m, 64);
+    if (oa > amax || (oa == amax && oi < idx)) amax = oa, mx = om, idx = oi;
+    nanf |= __shfl_xor(nanf, m, 64);
+  }
+  ActK r;
+  r.bs0 = r.bs1 = 0;
+  float d = 0.f;
+  if (amax != 0.f) {
+    const float iscale = __fdiv_rn(-127.f, mx);
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float sv = __fmul_rn(iscale, v[4 * w + e]);
+        const int q = sv != sv ? 0 : nearest_int(fminf(127.f, fmaxf(-127.f, sv)));
+        if (w < 4) r.bs0 += q; else r.bs1 += q;
+        word |= uint32_t(q & 0xFF) << (8 * e);
+      }
+      r.a[w] = word;
+    }
+    d = __fdiv_rn(1.f, iscale);
+  } else {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) r.a[w] = 0;
+  }
+  // bsums are stored as int16 (quant.h:104-108): a 16-sum of values in [-127, 127] always fits
+  r.d = nanf ? __builtin_nanf("") : d;
+  return r;
+}
+
+// ---- block terms ----
+
+// Legacy block b of weight row rr against one activation block: the block's float term (header comment).
+template <int T>
+__device__ __forceinline__ float legacy_term(const QW& W, int64_t rr, int64_t b, const ActL& A) {
+  const int64_t wb = rr * W.nb + b;
+  const float dw = h2f(W.d[wb]), da = A.d;
   if constexpr (T == kQ8_0) {
     const uint4* wp = reinterpret_cast<const uint4*>(W.q + wb * 32);
     const uint4 w0 = wp[0], w1 = wp[1];
-    int s = sdot4(w0.x, a[0], 0);
-    s = sdot4(w0.y, a[1], s), s = sdot4(w0.z, a[2], s), s = sdot4(w0.w, a[3], s);
-    s = sdot4(w1.x, a[4], s), s = sdot4(w1.y, a[5], s), s = sdot4(w1.z, a[6], s), s = sdot4(w1.w, a[7], s);
+    int s = sdot4(w0.x, A.a[0], 0);
+    s = sdot4(w0.y, A.a[1], s), s = sdot4(w0.z, A.a[2], s), s = sdot4(w0.w, A.a[3], s);
+    s = sdot4(w1.x, A.a[4], s), s = sdot4(w1.y, A.a[5], s), s = sdot4(w1.z, A.a[6], s), s = sdot4(w1.w, A.a[7], s);
     return __fmul_rn(float(s), __fmul_rn(dw, da));
   } else {
-    uint32_t w[4];
-    load16(W.q + wb * 16, w);
+    const uint4 wv = *reinterpret_cast<const uint4*>(W.q + wb * 16);
+    const uint32_t w[4] = {wv.x, wv.y, wv.z, wv.w};
     // element j of the block: low nibble of byte j (j < 16), high nibble of byte j - 16 (j >= 16)
     uint32_t lo[4], hi[4];
 #pragma unroll
@@ -193,17 +317,12 @@ __device__ __forceinline__ float legacy_term(const QW& W, const QA& A, int64_t r
           hi[i] |= ((qh >> (j + 16)) & 1u) << (8 * e + 4);
         }
     }
-    int s = 0, sa = 0;
+    int s = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s = sdot4(lo[i], a[i], s), s = sdot4(hi[i], a[i + 4], s);
-    if constexpr (T == kQ4_0 || T == kQ5_0) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) sa = sdot4(a[i], 0x01010101u, sa);  // sum of the 32 activations
-    }
-    if constexpr (T == kQ4_0) return __fmul_rn(__fmul_rn(float(s - 8 * sa), dw), da);
-    if constexpr (T == kQ5_0) return __fmul_rn(__fmul_rn(dw, da), float(s - 16 * sa));
-    if constexpr (T == kQ5_1)
-      return __fadd_rn(__fmul_rn(__fmul_rn(dw, da), float(s)), __fmul_rn(h2f(W.m[wb]), A.s[ab]));
+    for (int i = 0; i < 4; ++i) s = sdot4(lo[i], A.a[i], s), s = sdot4(hi[i], A.a[i + 4], s);
+    if constexpr (T == kQ4_0) return __fmul_rn(__fmul_rn(float(s - 8 * A.sum), dw), da);
+    if constexpr (T == kQ5_0) return __fmul_rn(__fmul_rn(dw, da), float(s - 16 * A.sum));
+    if constexpr (T == kQ5_1) return __fadd_rn(__fmul_rn(__fmul_rn(dw, da), float(s)), __fmul_rn(h2f(W.m[wb]), A.s));
   }
   return 0.f;
 }
@@ -219,20 +338,16 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& d, in
   }
 }
 
-// The integer partials of sub-block k (elements 32k..32k+31) of super-block sb, row rr, activation row t:
-// aux[l] = sum over its elements e with e % 8 == l of scale(e) * (a_e * q_e), and (Q4_K / Q5_K) sumi's share.
+// The integer partials of sub-block k (elements 32k..32k+31) of super-block sb of row rr against the activation
+// sub-block A: aux[l] = sum over its elements e with e % 8 == l of scale(e) * (a_e * q_e), and (Q4_K / Q5_K)
+// sumi's share (bsums of its two 16-groups times the sub-block minimum).
 template <int T>
-__device__ __forceinline__ void k_partials(const QW& W, const QA& A, int64_t rr, int64_t t, int64_t sb, int k,
-                                           int (&aux)[8], int& sumi) {
-  const int64_t wb = rr * W.nb + sb, ab = t * A.nb + sb;
-  const int8_t* a = A.qs + ab * 256 + 32 * k;
+__device__ __forceinline__ void k_partials(const QW& W, int64_t rr, int64_t sb, int k, const ActK& A, int (&aux)[8],
+                                           int& sumi) {
+  const int64_t wb = rr * W.nb + sb;
   int8_t av[32];
-  {
-    const uint4* ap = reinterpret_cast<const uint4*>(a);
-    const uint4 a0 = ap[0], a1 = ap[1];
-    *reinterpret_cast<uint4*>(av) = a0;
-    *reinterpret_cast<uint4*>(av + 16) = a1;
-  }
+#pragma unroll
+  for (int w = 0; w < 8; ++w) *reinterpret_cast<uint32_t*>(av + 4 * w) = A.a[w];
   int q[32];
   int sc_lo, sc_hi;
   if constexpr (T == kQ4_K || T == kQ5_K) {
@@ -254,8 +369,7 @@ __device__ __forceinline__ void k_partials(const QW& W, const QA& A, int64_t rr,
     int sc, m;
     scale_min_k4(k, W.s + wb * 16, sc, m);
     sc_lo = sc_hi = sc;
-    const int16_t* bs = A.bsums + ab * 16;
-    sumi = (int(bs[2 * k]) + int(bs[2 * k + 1])) * m;
+    sumi = (A.bs0 + A.bs1) * m;
   } else {  // Q6_K: sub-block k = 4h + g of the 128-element half h (quant.cpp:84-96)
     const int h = k >> 2, g = k & 3;
     const uint8_t* ql = W.q + wb * 128 + 64 * h + 32 * (g & 1);
@@ -281,15 +395,30 @@ __device__ __forceinline__ void k_partials(const QW& W, const QA& A, int64_t rr,
 
 // ---- the matmul ----
 
-template <int T, int NT>
-__global__ __launch_bounds__(64) void qgemv_kernel(QW W, QA A, float* __restrict__ y, int n) {
+constexpr int kMaxQWeights = NBHS_GEMV_MAX_WEIGHTS;
+struct QBatch {  // weights of one type sharing one input; wave0: first wave of each weight's rows
+  QW w[kMaxQWeights];
+  float* y[kMaxQWeights];
+  int64_t wave0[kMaxQWeights];
+  int n_w;
+};
+
+// FUSED: the activation rows are quantized here, from x (NT <= 4), instead of read from A.
+template <int T, int NT, bool FUSED>
+__global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* __restrict__ x, int64_t in, int n) {
   constexpr int O = kRows * NT;  // outputs of this wave
   constexpr bool K = T == kQ4_K || T == kQ5_K || T == kQ6_K;
   constexpr int CH = K ? 8 : 64;  // blocks per chunk
   constexpr int TERMS = K ? 9 : 1;
+  static_assert(!FUSED || NT <= 4, "fused activation quantization keeps NT rows in registers");
   __shared__ float terms[O][CH][TERMS];
   const int lane = threadIdx.x;
-  const int64_t r0 = int64_t(blockIdx.x) * kRows;
+  int wi = 0;
+  for (int j = 1; j < B.n_w; ++j)
+    if (int64_t(blockIdx.x) >= B.wave0[j]) wi = j;
+  const QW& W = B.w[wi];
+  float* __restrict__ y = B.y[wi];
+  const int64_t r0 = (int64_t(blockIdx.x) - B.wave0[wi]) * kRows;
   const int nr = int(W.rows - r0 < kRows ? W.rows - r0 : kRows);
   float acc = 0.f, sums[8];
 #pragma unroll
@@ -299,23 +428,38 @@ __global__ __launch_bounds__(64) void qgemv_kernel(QW W, QA A, float* __restrict
     // phase 1: block terms
     if constexpr (!K) {
       if (lane < nc) {
-        for (int r = 0; r < kRows; ++r) {
-          const int64_t rr = r0 + (r < nr ? r : nr - 1);
+        const int64_t b = c0 + lane;
+        if constexpr (FUSED) {
+          ActL act[NT];
 #pragma unroll
           for (int t = 0; t < NT; ++t)
-            if (t < n) terms[r * NT + t][lane][0] = legacy_term<T>(W, A, rr, t, c0 + lane);
+            if (t < n) act[t] = quant_act_l<T == kQ5_1>(x + int64_t(t) * in + b * 32);
+          for (int r = 0; r < kRows; ++r) {
+            const int64_t rr = r0 + (r < nr ? r : nr - 1);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+              if (t < n) terms[r * NT + t][lane][0] = legacy_term<T>(W, rr, b, act[t]);
+          }
+        } else {
+          for (int t = 0; t < NT; ++t) {
+            if (t >= n) break;
+            const ActL act = load_act_l(A, t, b);
+            for (int r = 0; r < kRows; ++r)
+              terms[r * NT + t][lane][0] = legacy_term<T>(W, r0 + (r < nr ? r : nr - 1), b, act);
+          }
         }
       }
     } else {
       const int sbl = lane >> 3, k = lane & 7;
       const bool live = sbl < nc;
       const int64_t sb = c0 + (live ? sbl : 0);
-      for (int r = 0; r < kRows; ++r) {
-        const int64_t rr = r0 + (r < nr ? r : nr - 1);
-        for (int t = 0; t < NT; ++t) {
-          if (t >= n) break;
+      for (int t = 0; t < NT; ++t) {
+        if (t >= n) break;
+        const ActK act = FUSED ? quant_act_k(x + int64_t(t) * in + sb * 256 + 32 * k, k) : load_act_k(A, t, sb, k);
+        for (int r = 0; r < kRows; ++r) {
+          const int64_t rr = r0 + (r < nr ? r : nr - 1);
           int aux[8], sumi;
-          k_partials<T>(W, A, rr, t, sb, k, aux, sumi);
+          k_partials<T>(W, rr, sb, k, act, aux, sumi);
 #pragma unroll
           for (int m = 1; m < 8; m <<= 1) {
 #pragma unroll
@@ -323,12 +467,11 @@ __global__ __launch_bounds__(64) void qgemv_kernel(QW W, QA A, float* __restrict
             sumi += __shfl_xor(sumi, m, 64);
           }
           if (live && k == 0) {
-            const int64_t wb = rr * W.nb + sb, ab = int64_t(t) * A.nb + sb;
-            const float d = __fmul_rn(h2f(W.d[wb]), A.d[ab]);
+            const int64_t wb = rr * W.nb + sb;
+            const float d = __fmul_rn(h2f(W.d[wb]), act.d);
 #pragma unroll
             for (int l = 0; l < 8; ++l) terms[r * NT + t][sbl][l] = __fmul_rn(d, float(aux[l]));
-            terms[r * NT + t][sbl][8] =
-                T == kQ6_K ? 0.f : __fmul_rn(__fmul_rn(h2f(W.m[wb]), A.d[ab]), float(sumi));
+            terms[r * NT + t][sbl][8] = T == kQ6_K ? 0.f : __fmul_rn(__fmul_rn(h2f(W.m[wb]), act.d), float(sumi));
           }
         }
       }
@@ -425,11 +568,15 @@ QW weight_of(int type, const void* w, int64_t rows, int64_t in) {
 }
 
 template <int T>
-int launch_gemv(const QW& W, const QA& A, float* y, int64_t n, hipStream_t s) {
-  const dim3 grid{unsigned((W.rows + kRows - 1) / kRows), 1, 1}, block{64, 1, 1};
-  if (n == 1) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 1>, grid, block, s, W, A, y, int(n));
-  if (n <= 4) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4>, grid, block, s, W, A, y, int(n));
-  return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 16>, grid, block, s, W, A, y, int(n));
+int launch_gemv(const QBatch& B, int64_t waves, const QA& A, const float* x, int64_t in, int64_t n, bool fused,
+                hipStream_t s) {
+  const dim3 grid{unsigned(waves), 1, 1}, block{64, 1, 1};
+  if (fused) {
+    if (n == 1) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 1, true>, grid, block, s, B, A, x, in, int(n));
+    return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4, true>, grid, block, s, B, A, x, in, int(n));
+  }
+  if (n <= 4) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4, false>, grid, block, s, B, A, x, in, int(n));
+  return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 16, false>, grid, block, s, B, A, x, in, int(n));
 }
 
 template <int T>
@@ -475,28 +622,47 @@ int nbhs_quantize_acts(int type, const float* x, int64_t n, int64_t in, void* ac
                              static_cast<float*>(nullptr));
 }
 
-int nbhs_qgemv(int type, const void* w, int64_t rows, int64_t in, const void* acts, int64_t n_acts, int64_t t0,
-               int64_t n, float* y, nbhs_stream stream) {
-  if (!is_quant(type) || !w || !acts || !y || rows <= 0 || in <= 0 || in % block_elems(type) || n <= 0 ||
-      n > NBHS_GEMV_MAX_ROWS || t0 < 0 || t0 + n > n_acts || (rows + kRows - 1) / kRows >= (int64_t(1) << 31))
+int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* rows, float* const* y, int64_t in,
+                     const float* x, const void* acts, int64_t n_acts, int64_t t0, int64_t n, nbhs_stream stream) {
+  if (!is_quant(type) || n_w <= 0 || n_w > kMaxQWeights || !w || !rows || !y || in <= 0 ||
+      in % block_elems(type) || n <= 0 || n > NBHS_GEMV_MAX_ROWS)
     return NBHS_EINVAL;
-  const QW W = weight_of(type, w, rows, in);
-  const int act = act_of(type);
-  const ActLayout l = act_layout(act, n_acts, W.nb);
-  const uint8_t* base = static_cast<const uint8_t*>(acts);
-  const int64_t b0 = t0 * W.nb;  // first block of activation row t0
-  const QA A{reinterpret_cast<const int8_t*>(base + l.qs_off) + b0 * (act == kActQ8_K ? 256 : 32),
-             reinterpret_cast<const float*>(base + l.d_off) + b0, reinterpret_cast<const float*>(base + l.s_off) + b0,
-             reinterpret_cast<const int16_t*>(base + l.bsums_off) + b0 * 16, W.nb};
+  const bool fused = acts == nullptr;
+  if (fused ? (!x || n > 4 || t0 != 0 || reinterpret_cast<uintptr_t>(x) % 16 || in % 4) : (t0 < 0 || t0 + n > n_acts))
+    return NBHS_EINVAL;
+  QBatch B{};
+  int64_t waves = 0;
+  for (int i = 0; i < n_w; ++i) {
+    if (!w[i] || !y[i] || rows[i] <= 0) return NBHS_EINVAL;
+    B.w[i] = weight_of(type, w[i], rows[i], in);
+    B.y[i] = y[i];
+    B.wave0[i] = waves;
+    waves += (rows[i] + kRows - 1) / kRows;
+  }
+  B.n_w = n_w;
+  if (waves >= (int64_t(1) << 31)) return NBHS_EINVAL;
+  const int64_t nb = in / block_elems(type);
+  QA A{};
+  A.nb = nb;
+  if (!fused) {
+    const int act = act_of(type);
+    const ActLayout l = act_layout(act, n_acts, nb);
+    const uint8_t* base = static_cast<const uint8_t*>(acts);
+    const int64_t b0 = t0 * nb;  // first block of activation row t0
+    A.qs = reinterpret_cast<const int8_t*>(base + l.qs_off) + b0 * (act == kActQ8_K ? 256 : 32);
+    A.d = reinterpret_cast<const float*>(base + l.d_off) + b0;
+    A.s = act == kActQ8_1 ? reinterpret_cast<const float*>(base + l.s_off) + b0 : nullptr;
+    A.bsums = reinterpret_cast<const int16_t*>(base + l.bsums_off) + b0 * 16;
+  }
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (type) {
-    case kQ4_0: return launch_gemv<kQ4_0>(W, A, y, n, s);
-    case kQ5_0: return launch_gemv<kQ5_0>(W, A, y, n, s);
-    case kQ5_1: return launch_gemv<kQ5_1>(W, A, y, n, s);
-    case kQ8_0: return launch_gemv<kQ8_0>(W, A, y, n, s);
-    case kQ4_K: return launch_gemv<kQ4_K>(W, A, y, n, s);
-    case kQ5_K: return launch_gemv<kQ5_K>(W, A, y, n, s);
-    case kQ6_K: return launch_gemv<kQ6_K>(W, A, y, n, s);
+    case kQ4_0: return launch_gemv<kQ4_0>(B, waves, A, x, in, n, fused, s);
+    case kQ5_0: return launch_gemv<kQ5_0>(B, waves, A, x, in, n, fused, s);
+    case kQ5_1: return launch_gemv<kQ5_1>(B, waves, A, x, in, n, fused, s);
+    case kQ8_0: return launch_gemv<kQ8_0>(B, waves, A, x, in, n, fused, s);
+    case kQ4_K: return launch_gemv<kQ4_K>(B, waves, A, x, in, n, fused, s);
+    case kQ5_K: return launch_gemv<kQ5_K>(B, waves, A, x, in, n, fused, s);
+    case kQ6_K: return launch_gemv<kQ6_K>(B, waves, A, x, in, n, fused, s);
     default: return NBHS_EINVAL;
   }
 }
