@@ -263,6 +263,71 @@ def qkv_projection(be, steps, warmup, chunk=512, chunk_reps=3):
                               "note": "rocBLAS sgemm x3 per layer on fp32-widened weights (fp32 math)"}}
 
 
+QUANT_NAMES = {2: "Q4_0", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}
+
+
+def quant_projection(be, steps, warmup, chunk=512, chunk_reps=2):
+    """The same QKV projection with quantized weights (Llama-3.2-1B shape, 16 layers; synthetic blocks of each
+    type): one launch per layer for the three weights, the activation row quantized inside it, bit-exact with the
+    reference's quant.cpp. Decode (n = 1): HBM GB/s of the weight blocks (file bytes) streamed per launch. Prefill
+    chunks (n = 512): integer-op rate of the block dots."""
+    from nibble_amd import synth
+    shape = configs.LLAMA32_1B
+    E, Q, kvw, NL = shape.n_embd, shape.n_heads * shape.head_dim, shape.n_kv_heads * shape.head_dim, 16
+    out = {}
+    x = be.alloc(chunk * E)
+    be.fill_normal(x, chunk * E, seed=43)
+    q, kc, vc = be.alloc(chunk * Q), be.alloc(chunk * kvw), be.alloc(chunk * kvw)
+    for t, name in QUANT_NAMES.items():
+        raws = [[synth.quant_weight(t, r, E, 1000 * l + i) for i, r in enumerate((Q, kvw, kvw))] for l in range(NL)]
+        ws = [[nibble_amd.weight(raws[l][i], shape=(r, E), dtype=t) for i, r in enumerate((Q, kvw, kvw))]
+              for l in range(NL)]
+        w_bytes = sum(r.nbytes for r in raws[0])
+
+        def step(n):
+            for l in range(NL):
+                be.matmul_multi(ws[l], x, [q, kc, vc], n)
+
+        for _ in range(warmup):
+            step(1)
+        be.sync()
+        e0, e1 = be.event(), be.event()
+        e0.record()
+        for _ in range(steps):
+            step(1)
+        e1.record()
+        dec_ms = e0.elapsed_ms(e1)
+        KernelTiming.enable(True, only=KernelTiming.QGEMV)
+        for _ in range(steps):
+            step(1)
+        be.sync()
+        g_ms, g_n = KernelTiming.read(KernelTiming.QGEMV)
+        KernelTiming.enable(False)
+        step(chunk)
+        be.sync()
+        e0.record()
+        for _ in range(chunk_reps):
+            step(chunk)
+        e1.record()
+        pre_ms = e0.elapsed_ms(e1) / chunk_reps
+        alg = w_bytes + E * 4 + (Q + 2 * kvw) * 4
+        us = g_ms / g_n * 1e3
+        gbs = alg / (us * 1e-6) / 1e9
+        tops = NL * 2 * chunk * E * (Q + 2 * kvw) / (pre_ms * 1e-3) / 1e12
+        out[name] = {"decode": {"avg_launch_us": round(us, 3), "value": round(gbs, 1), "unit": "GB/s",
+                                "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": alg,
+                                "us_per_step_16_layers": round(dec_ms / steps * 1e3, 1)},
+                     "prefill_chunk": {"rows": chunk, "us_per_layer": round(pre_ms / NL * 1e3, 1),
+                                       "value": round(tops, 2), "unit": "TOPS (block-dot MACs x 2)"}}
+        log(f"quant projection {name}: decode launch {us:.2f} us -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}) of "
+            f"{alg / 1e6:.2f} MB; prefill chunk {chunk}: {pre_ms / NL * 1e3:.1f} us/layer -> {tops:.1f} TOPS")
+        be.release_weights()
+    for p in (x, q, kc, vc):
+        be.free(p)
+    return {"metric": "QKV projection with quantized weights (bit-exact with quant.cpp), llama-3.2-1b shape",
+            "types": out}
+
+
 COPY_CAL_BYTES = 1 << 30  # calibration copy for the HBM byte counters: 1 GiB read + 1 GiB written
 PROBE_DECODE_STEPS = 8
 
@@ -593,6 +658,7 @@ def main():
         result["config5"] = ragged_decode(be, args.cfg5_steps, 2)
     if args.qkv_steps > 0:
         result["qkv_projection"] = qkv_projection(be, args.qkv_steps, 4)
+        result["quant_projection"] = quant_projection(be, args.qkv_steps, 4)
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(be, shape, ck[0], cv[0], qd, ctx, q_pre0_host, args.cpu_seconds)

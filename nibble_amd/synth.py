@@ -73,3 +73,23 @@ def llama3_freq_factors(head_dim: int, base: float, factor: float = 32.0, low: f
     f = np.where(wavelen < orig_ctx / high, 1.0,
                  np.where(wavelen > orig_ctx / low, factor, 1.0 / ((1.0 - s) / factor + s)))
     return f.astype(np.float32)
+
+
+# ggml block layouts (reference src/quant.h:34-110): block bytes, elements per block, and the byte offsets of the
+# fp16 scale fields (d and, where present, the minimum) inside a block.
+QUANT_BLOCKS = {2: (18, 32, (0,)), 6: (22, 32, (0,)), 7: (24, 32, (0, 2)), 8: (34, 32, (0,)),
+                12: (144, 256, (0, 2)), 13: (176, 256, (0, 2)), 14: (210, 256, (208,))}
+
+
+def quant_weight(t: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """Synthetic raw blocks of ggml type t for a rows x cols weight (benchmarks): random quant bytes and fp16 scales
+    of magnitude 2^-9..2^-6, as trained weights' per-block scales are. Returns the uint8 block array."""
+    bb, be, offs = QUANT_BLOCKS[t]
+    nb = rows * cols // be
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
+    for o in offs:
+        mag = rng.uniform(2.0 ** -9, 2.0 ** -6, nb).astype(np.float16)
+        sign = np.where(rng.random(nb) < 0.5, -1, 1).astype(np.float16) if o == 0 and t in (2, 6, 8) else 1
+        raw[:, o:o + 2] = (mag * sign).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return raw.reshape(-1)
