@@ -44,12 +44,21 @@ std::vector<uint8_t> repack_quant(int t, const uint8_t* src, int64_t rows, int64
     default: break;
   }
   const int64_t s_len = t == kQ6_K ? 16 : 12;
+  // K types: 32-byte groups indexed by the element's position in its sub-block go to residue order
+  auto put = [&](uint8_t* dst, const uint8_t* from, int64_t len) {
+    if (!is_k(t)) {
+      std::memcpy(dst, from, size_t(len));
+      return;
+    }
+    for (int64_t g = 0; g < len; g += 32)
+      for (int j = 0; j < 32; ++j) dst[g + residue_pos(j)] = from[g + j];
+  };
   for (int64_t i = 0; i < rows * nb; ++i) {
     const uint8_t* b = src + i * bb;
-    std::memcpy(&out[size_t(l.q_off + i * qb)], b + oq, size_t(qb));
+    put(&out[size_t(l.q_off + i * qb)], b + oq, qb);
     std::memcpy(&out[size_t(l.d_off + i * 2)], b + od, 2);
     if (om >= 0) std::memcpy(&out[size_t(l.m_off + i * 2)], b + om, 2);
-    if (oh >= 0) std::memcpy(&out[size_t(l.h_off + i * hb)], b + oh, size_t(hb));
+    if (oh >= 0) put(&out[size_t(l.h_off + i * hb)], b + oh, hb);
     if (os >= 0) std::memcpy(&out[size_t(l.s_off + i * sb)], b + os, size_t(s_len));
   }
   return out;

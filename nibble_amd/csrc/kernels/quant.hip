@@ -15,12 +15,13 @@
 //   super-block, sums[l] += (d_w * d_a) * float(aux[l]) in super-block order, Q4_K / Q5_K also sumf -= (dmin_w *
 //   d_a) * float(sumi) per super-block, and the eight sums added to sumf last.
 //
-// qgemv_kernel: one 64-lane wave per 4 weight rows and up to NT activation rows. Phase 1 spreads blocks over lanes
-// (a legacy block per lane; a K super-block over 8 lanes, one 32-element sub-block each, their integer partials
-// summed by shuffles) and writes each block's float term(s) to LDS; phase 2 gives each (row, activation row) pair
-// one lane, which adds its terms in block order. Weights arrive in the plane layout of quant_layout.h, so every
-// load is aligned (16-byte quant loads, 2-byte scales).
+// qgemv_kernel (n <= 16 activation rows): a 64-lane wave takes RW weight rows; its lanes take (row, block) pairs -
+// a legacy block or a whole K super-block each - and write each pair's float term(s) to LDS; then one lane per
+// (row, activation row) adds its terms in block order. K quants are stored in residue order (quant_layout.h), so a
+// sub-block's eight integer lanes are eight v_dot4. With up to 4 activation rows the rows are quantized inside the
+// launch (into LDS, once per wave and block), with the same bits as the standalone quantizer.
 #include <hip/hip_runtime.h>
+
 
 #include "backend/hip/kernel_timing.h"
 #include "kernels/quant_layout.h"
@@ -29,8 +30,6 @@
 namespace {
 
 using namespace nbh_quant;
-
-constexpr int kRows = 4;  // weight rows per wave
 
 struct QW {
   const uint8_t* q;
@@ -104,14 +103,15 @@ __device__ __forceinline__ int nearest_int(float f) {
   return (__float_as_int(val) & 0x007fffff) - 0x00400000;
 }
 
-// One wave per 256-element super-block; lane l holds elements 4l..4l+3.
+// One wave per 256-element super-block; lane l = 8k + w holds elements 32k + w + 8i (i < 4) of sub-block k: the four
+// elements of residue word w, which it stores as word w of the sub-block (residue order, quant_layout.h).
 __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restrict__ x, int64_t in,
                                                           int8_t* __restrict__ qs, float* __restrict__ dq,
                                                           int16_t* __restrict__ bsums) {
   const int64_t nb = in / 256, i = blockIdx.x;
-  const int lane = threadIdx.x;
-  const float* xb = x + (i / nb) * in + (i % nb) * 256;
-  const float v[4] = {xb[4 * lane], xb[4 * lane + 1], xb[4 * lane + 2], xb[4 * lane + 3]};
+  const int lane = threadIdx.x, k = lane >> 3, w = lane & 7;
+  const float* xb = x + (i / nb) * in + (i % nb) * 256 + 32 * k + w;
+  const float v[4] = {xb[0], xb[8], xb[16], xb[24]};
   // the first element of largest magnitude (strictly greater replaces; NaN never does)
   float amax = 0.f, mx = 0.f;
   int idx = 1 << 30;
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restric
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const float ax = fabsf(v[e]);
-    if (ax > amax) amax = ax, mx = v[e], idx = 4 * lane + e;
+    if (ax > amax) amax = ax, mx = v[e], idx = 32 * k + w + 8 * e;
     nan |= v[e] != v[e];
   }
 #pragma unroll
@@ -130,30 +130,30 @@ __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restric
   }
   nan = __builtin_amdgcn_ballot_w64(nan) != 0;
   uint32_t word = 0;
-  int part = 0;
+  int b0 = 0, b1 = 0;  // this lane's share of the sub-block's two 16-sums (elements w, w + 8 | w + 16, w + 24)
   float d = 0.f;
   if (amax != 0.f) {
     const float iscale = __fdiv_rn(-127.f, mx);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float s = __fmul_rn(iscale, v[e]);
-      const int q = s != s ? 0 : nearest_int(fminf(127.f, fmaxf(-127.f, s)));
-      part += q;
+      const float sv = __fmul_rn(iscale, v[e]);
+      const int q = sv != sv ? 0 : nearest_int(fminf(127.f, fmaxf(-127.f, sv)));
+      if (e < 2) b0 += q; else b1 += q;
       word |= uint32_t(q & 0xFF) << (8 * e);
     }
     d = __fdiv_rn(1.f, iscale);
   }
-  part += __shfl_xor(part, 1, 64);
-  part += __shfl_xor(part, 2, 64);
+#pragma unroll
+  for (int m = 1; m < 8; m <<= 1) b0 += __shfl_xor(b0, m, 64), b1 += __shfl_xor(b1, m, 64);
   reinterpret_cast<uint32_t*>(qs + i * 256)[lane] = word;
-  if ((lane & 3) == 0) bsums[i * 16 + lane / 4] = int16_t(part);
+  if (w == 0) bsums[i * 16 + 2 * k] = int16_t(b0), bsums[i * 16 + 2 * k + 1] = int16_t(b1);
   if (lane == 0) dq[i] = nan ? __builtin_nanf("") : d;
 }
 
-// ---- activation blocks in registers ----
+// ---- activation blocks ----
 
-// One legacy activation block (32 quants as 8 words), its scale d (fp16-rounded, widened), Q8_1's s, and the sum
-// of its quants (for the Q4_0 / Q5_0 offsets).
+// One legacy activation block: 32 quants as 8 words, the scale d (fp16-rounded, widened), Q8_1's s, and the sum
+// of the quants (for the Q4_0 / Q5_0 offsets).
 struct ActL {
   uint32_t a[8];
   float d, s;
@@ -175,7 +175,8 @@ __device__ __forceinline__ ActL load_act_l(const QA& A, int64_t t, int64_t b) {
   return r;
 }
 
-// quantize_block_q8 (quant.cpp:37-49) of the 32 floats at xb, in registers: the same bits quantize_q8_kernel writes.
+// quantize_block_q8 (quant.cpp:37-49) of the 32 floats at xb (16-byte aligned), in registers: the same bits
+// quantize_q8_kernel writes.
 template <bool Q81>
 __device__ __forceinline__ ActL quant_act_l(const float* xb) {
   float v[32];
@@ -212,29 +213,10 @@ __device__ __forceinline__ ActL quant_act_l(const float* xb) {
   return r;
 }
 
-// One 32-element sub-block k of a Q8_K activation super-block: its quants, the block scale d and the two 16-sums.
-struct ActK {
-  uint32_t a[8];
-  float d;
-  int bs0, bs1;
-};
-
-__device__ __forceinline__ ActK load_act_k(const QA& A, int64_t t, int64_t sb, int k) {
-  ActK r;
-  const int64_t ab = t * A.nb + sb;
-  const uint4* ap = reinterpret_cast<const uint4*>(A.qs + ab * 256 + 32 * k);
-  const uint4 a0 = ap[0], a1 = ap[1];
-  r.a[0] = a0.x, r.a[1] = a0.y, r.a[2] = a0.z, r.a[3] = a0.w, r.a[4] = a1.x, r.a[5] = a1.y, r.a[6] = a1.z,
-  r.a[7] = a1.w;
-  r.d = A.d[ab];
-  r.bs0 = A.bsums[ab * 16 + 2 * k];
-  r.bs1 = A.bsums[ab * 16 + 2 * k + 1];
-  return r;
-}
-
-// quantize_row_q8_K (quant.cpp:273-303) for the super-block spread over the 8 lanes of this lane's group (lane k
-// holds elements 32k..32k+31 at xs): the first element of largest magnitude sets the scale. All 64 lanes call it.
-__device__ __forceinline__ ActK quant_act_k(const float* xs, int k) {
+// quantize_row_q8_K (quant.cpp:273-303) of one super-block spread over the 8 lanes of this lane's group (lane k
+// holds elements 32k..32k+31 at xs, 16-byte aligned): the first element of largest magnitude sets the scale.
+// Returns sub-block k's words in residue order and its two 16-sums; every lane of the wave must call it.
+__device__ __forceinline__ void quant_act_k(const float* xs, int k, uint32_t (&aw)[8], int& bs0, int& bs1, float& d) {
   float v[32];
 #pragma unroll
   for (int j = 0; j < 32; j += 4) {
@@ -242,15 +224,13 @@ __device__ __forceinline__ ActK quant_act_k(const float* xs, int k) {
     v[j] = f.x, v[j + 1] = f.y, v[j + 2] = f.z, v[j + 3] = f.w;
   }
   float amax = 0.f, mx = 0.f;
-  int idx = 1 << 30;
-  bool nan = false;
+  int idx = 1 << 30, nanf = 0;
 #pragma unroll
   for (int e = 0; e < 32; ++e) {
     const float ax = fabsf(v[e]);
     if (ax > amax) amax = ax, mx = v[e], idx = 32 * k + e;
-    nan |= v[e] != v[e];
+    nanf |= v[e] != v[e];
   }
-  int nanf = nan ? 1 : 0;
 #pragma unroll
   for (int m = 1; m < 8; m <<= 1) {
     const float oa = __shfl_xor(amax, m, 64), om = __shfl_xor(mx, m, 64);
@@ -258,31 +238,27 @@ __device__ __forceinline__ ActK quant_act_k(const float* xs, int k) {
     if (oa > amax || (oa == amax && oi < idx)) amax = oa, mx = om, idx = oi;
     nanf |= __shfl_xor(nanf, m, 64);
   }
-  ActK r;
-  r.bs0 = r.bs1 = 0;
-  float d = 0.f;
+  int q[32];
+  d = 0.f;
+  bs0 = bs1 = 0;
   if (amax != 0.f) {
     const float iscale = __fdiv_rn(-127.f, mx);
 #pragma unroll
-    for (int w = 0; w < 8; ++w) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float sv = __fmul_rn(iscale, v[4 * w + e]);
-        const int q = sv != sv ? 0 : nearest_int(fminf(127.f, fmaxf(-127.f, sv)));
-        if (w < 4) r.bs0 += q; else r.bs1 += q;
-        word |= uint32_t(q & 0xFF) << (8 * e);
-      }
-      r.a[w] = word;
+    for (int e = 0; e < 32; ++e) {
+      const float sv = __fmul_rn(iscale, v[e]);
+      q[e] = sv != sv ? 0 : nearest_int(fminf(127.f, fmaxf(-127.f, sv)));
+      if (e < 16) bs0 += q[e]; else bs1 += q[e];
     }
     d = __fdiv_rn(1.f, iscale);
   } else {
 #pragma unroll
-    for (int w = 0; w < 8; ++w) r.a[w] = 0;
+    for (int e = 0; e < 32; ++e) q[e] = 0;
   }
-  // bsums are stored as int16 (quant.h:104-108): a 16-sum of values in [-127, 127] always fits
-  r.d = nanf ? __builtin_nanf("") : d;
-  return r;
+#pragma unroll
+  for (int w = 0; w < 8; ++w)
+    aw[w] = uint32_t(q[w] & 0xFF) | uint32_t(q[w + 8] & 0xFF) << 8 | uint32_t(q[w + 16] & 0xFF) << 16 |
+            uint32_t(q[w + 24] & 0xFF) << 24;
+  if (nanf) d = __builtin_nanf("");
 }
 
 // ---- block terms ----
@@ -338,59 +314,70 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& d, in
   }
 }
 
-// The integer partials of sub-block k (elements 32k..32k+31) of super-block sb of row rr against the activation
-// sub-block A: aux[l] = sum over its elements e with e % 8 == l of scale(e) * (a_e * q_e), and (Q4_K / Q5_K)
-// sumi's share (bsums of its two 16-groups times the sub-block minimum).
-template <int T>
-__device__ __forceinline__ void k_partials(const QW& W, int64_t rr, int64_t sb, int k, const ActK& A, int (&aux)[8],
-                                           int& sumi) {
+__device__ __forceinline__ void load32(const uint8_t* p, uint32_t (&w)[8]) {
+  const uint4 a = reinterpret_cast<const uint4*>(p)[0], b = reinterpret_cast<const uint4*>(p)[1];
+  w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w, w[4] = b.x, w[5] = b.y, w[6] = b.z, w[7] = b.w;
+}
+
+// The integer lanes of super-block sb of row rr against an activation super-block whose sub-block k words are
+// act(k, w) (residue order) and 16-sums bsum(g): aux[w] = sum over the block's elements e with e % 8 == w of
+// scale(e) * (a_e * q_e) (quant.cpp:118-144, 394-416), and for Q4_K / Q5_K sumi = sum_k (bsums) * m_k.
+template <int T, class ActW, class BSum>
+__device__ __forceinline__ void k_lanes(const QW& W, int64_t rr, int64_t sb, ActW act, BSum bsum, int (&aux)[8],
+                                        int& sumi) {
   const int64_t wb = rr * W.nb + sb;
-  int8_t av[32];
 #pragma unroll
-  for (int w = 0; w < 8; ++w) *reinterpret_cast<uint32_t*>(av + 4 * w) = A.a[w];
-  int q[32];
-  int sc_lo, sc_hi;
+  for (int w = 0; w < 8; ++w) aux[w] = 0;
+  sumi = 0;
+  const uint8_t* sc = W.s + wb * 16;
   if constexpr (T == kQ4_K || T == kQ5_K) {
-    const uint8_t* qs = W.q + wb * 128 + 32 * (k >> 1);
-    const int shift = 4 * (k & 1);
-    uint8_t qb[32];
-    *reinterpret_cast<uint4*>(qb) = reinterpret_cast<const uint4*>(qs)[0];
-    *reinterpret_cast<uint4*>(qb + 16) = reinterpret_cast<const uint4*>(qs)[1];
+    uint32_t hw[8];
+    if constexpr (T == kQ5_K) load32(W.h + wb * 32, hw);
 #pragma unroll
-    for (int e = 0; e < 32; ++e) q[e] = (qb[e] >> shift) & 0xF;
-    if constexpr (T == kQ5_K) {
-      uint8_t hb[32];
-      const uint8_t* qh = W.h + wb * 32;
-      *reinterpret_cast<uint4*>(hb) = reinterpret_cast<const uint4*>(qh)[0];
-      *reinterpret_cast<uint4*>(hb + 16) = reinterpret_cast<const uint4*>(qh)[1];
+    for (int c = 0; c < 4; ++c) {
+      uint32_t qw[8];
+      load32(W.q + wb * 128 + 32 * c, qw);
 #pragma unroll
-      for (int e = 0; e < 32; ++e) q[e] += ((hb[e] >> k) & 1) ? 16 : 0;
+      for (int half = 0; half < 2; ++half) {
+        const int k = 2 * c + half;
+        int s, m;
+        scale_min_k4(k, sc, s, m);
+        sumi += (bsum(2 * k) + bsum(2 * k + 1)) * m;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          uint32_t v = (qw[w] >> (4 * half)) & 0x0F0F0F0Fu;
+          if constexpr (T == kQ5_K) v |= ((hw[w] >> k) & 0x01010101u) << 4;
+          aux[w] += s * sdot4(v, act(k, w), 0);
+        }
+      }
     }
-    int sc, m;
-    scale_min_k4(k, W.s + wb * 16, sc, m);
-    sc_lo = sc_hi = sc;
-    sumi = (A.bs0 + A.bs1) * m;
-  } else {  // Q6_K: sub-block k = 4h + g of the 128-element half h (quant.cpp:84-96)
-    const int h = k >> 2, g = k & 3;
-    const uint8_t* ql = W.q + wb * 128 + 64 * h + 32 * (g & 1);
-    const uint8_t* qh = W.h + wb * 64 + 32 * h;
-    uint8_t lb[32], hb[32];
-    *reinterpret_cast<uint4*>(lb) = reinterpret_cast<const uint4*>(ql)[0];
-    *reinterpret_cast<uint4*>(lb + 16) = reinterpret_cast<const uint4*>(ql)[1];
-    *reinterpret_cast<uint4*>(hb) = reinterpret_cast<const uint4*>(qh)[0];
-    *reinterpret_cast<uint4*>(hb + 16) = reinterpret_cast<const uint4*>(qh)[1];
-    const int ls = (g >> 1) * 4, hs = 2 * g;
+  } else {  // Q6_K: sub-block k = 4h + g of the 128-element half h; values 0..63 less 32 (quant.cpp:84-96)
+    const int8_t* scl = reinterpret_cast<const int8_t*>(sc);
 #pragma unroll
-    for (int e = 0; e < 32; ++e) q[e] = (((lb[e] >> ls) & 0xF) | (((hb[e] >> hs) & 3) << 4)) - 32;
-    const int8_t* scl = reinterpret_cast<const int8_t*>(W.s + wb * 16);
-    sc_lo = scl[2 * k];
-    sc_hi = scl[2 * k + 1];
-    sumi = 0;
+    for (int h = 0; h < 2; ++h) {
+      uint32_t hw[8];
+      load32(W.h + wb * 64 + 32 * h, hw);
+#pragma unroll
+      for (int lg = 0; lg < 2; ++lg) {  // ql group: bytes 64h + 32lg .. +31 (sub-blocks g = lg and lg + 2)
+        uint32_t lw[8];
+        load32(W.q + wb * 128 + 64 * h + 32 * lg, lw);
+#pragma unroll
+        for (int sel = 0; sel < 2; ++sel) {
+          const int g = lg + 2 * sel, k = 4 * h + g;
+          const int s_lo = scl[2 * k], s_hi = scl[2 * k + 1];
+#pragma unroll
+          for (int w = 0; w < 8; ++w) {
+            const uint32_t v = ((lw[w] >> (4 * sel)) & 0x0F0F0F0Fu) | (((hw[w] >> (2 * g)) & 0x03030303u) << 4);
+            const uint32_t a = act(k, w);
+            // bytes 0, 1 of a residue word are elements w, w + 8 (the first 16: scale s_lo); bytes 2, 3 the rest
+            const int dlo = sdot4(v & 0x0000FFFFu, a, 0) - 32 * sdot4(0x00000101u, a, 0);
+            const int dhi = sdot4(v & 0xFFFF0000u, a, 0) - 32 * sdot4(0x01010000u, a, 0);
+            aux[w] += s_lo * dlo + s_hi * dhi;
+          }
+        }
+      }
+    }
   }
-#pragma unroll
-  for (int l = 0; l < 8; ++l) aux[l] = 0;
-#pragma unroll
-  for (int e = 0; e < 32; ++e) aux[e & 7] += (e < 16 ? sc_lo : sc_hi) * (int(av[e]) * q[e]);
 }
 
 // ---- the matmul ----
@@ -403,76 +390,101 @@ struct QBatch {  // weights of one type sharing one input; wave0: first wave of 
   int n_w;
 };
 
+// Weight rows per wave: a legacy row has a block per lane (in = 2048: 64 blocks), a K row a super-block per lane
+// (in = 2048: 8), so K waves take twice the rows; with 16 activation rows a wave's outputs are capped at 64.
+constexpr int rows_per_wave(bool k, int NT) { return NT > 4 ? 4 : k ? 8 : 4; }
+
+// A K activation super-block staged in LDS on the fused path: 256 quants in residue order, d, the 16-sums.
+struct LdsActK {
+  uint32_t a[64];
+  float d;
+  int bs[16];
+};
+
 // FUSED: the activation rows are quantized here, from x (NT <= 4), instead of read from A.
 template <int T, int NT, bool FUSED>
 __global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* __restrict__ x, int64_t in, int n) {
-  constexpr int O = kRows * NT;  // outputs of this wave
   constexpr bool K = T == kQ4_K || T == kQ5_K || T == kQ6_K;
+  constexpr int RW = rows_per_wave(K, NT);
+  constexpr int O = RW * NT;  // outputs of this wave
   constexpr int CH = K ? 8 : 64;  // blocks per chunk
   constexpr int TERMS = K ? 9 : 1;
-  static_assert(!FUSED || NT <= 4, "fused activation quantization keeps NT rows in registers");
+  static_assert(O <= 64, "one lane per output in the ordered sum");
+  static_assert(!FUSED || NT <= 4, "fused activation quantization stages at most 4 rows");
   __shared__ float terms[O][CH][TERMS];
+  __shared__ LdsActK acts[K && FUSED ? NT : 1][K ? CH : 1];
   const int lane = threadIdx.x;
   int wi = 0;
   for (int j = 1; j < B.n_w; ++j)
     if (int64_t(blockIdx.x) >= B.wave0[j]) wi = j;
   const QW& W = B.w[wi];
   float* __restrict__ y = B.y[wi];
-  const int64_t r0 = (int64_t(blockIdx.x) - B.wave0[wi]) * kRows;
-  const int nr = int(W.rows - r0 < kRows ? W.rows - r0 : kRows);
+  const int64_t r0 = (int64_t(blockIdx.x) - B.wave0[wi]) * RW;
+  const int nr = int(W.rows - r0 < RW ? W.rows - r0 : RW);
   float acc = 0.f, sums[8];
 #pragma unroll
   for (int l = 0; l < 8; ++l) sums[l] = 0.f;
   for (int64_t c0 = 0; c0 < W.nb; c0 += CH) {
     const int nc = int(W.nb - c0 < CH ? W.nb - c0 : CH);
-    // phase 1: block terms
-    if constexpr (!K) {
+    if constexpr (FUSED && K) {  // quantize this chunk's activation super-blocks once, into LDS
+      const int sbl = lane >> 3, k = lane & 7;
+      const int64_t sb = c0 + (sbl < nc ? sbl : 0);
+      for (int t = 0; t < NT; ++t) {
+        if (t >= n) break;
+        uint32_t aw[8];
+        int bs0, bs1;
+        float d;
+        quant_act_k(x + int64_t(t) * in + sb * 256 + 32 * k, k, aw, bs0, bs1, d);
+        if (sbl < nc) {
+          LdsActK& o = acts[t][sbl];
+#pragma unroll
+          for (int w = 0; w < 8; ++w) o.a[8 * k + w] = aw[w];
+          o.bs[2 * k] = bs0, o.bs[2 * k + 1] = bs1;
+          if (k == 0) o.d = d;
+        }
+      }
+      __syncthreads();
+    }
+    // phase 1: the term(s) of every (row, block) pair, for each activation row
+    if constexpr (!K) {  // a block per lane; its activation block (quantized here when fused) serves every row
       if (lane < nc) {
         const int64_t b = c0 + lane;
-        if constexpr (FUSED) {
-          ActL act[NT];
-#pragma unroll
-          for (int t = 0; t < NT; ++t)
-            if (t < n) act[t] = quant_act_l<T == kQ5_1>(x + int64_t(t) * in + b * 32);
-          for (int r = 0; r < kRows; ++r) {
-            const int64_t rr = r0 + (r < nr ? r : nr - 1);
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-              if (t < n) terms[r * NT + t][lane][0] = legacy_term<T>(W, rr, b, act[t]);
-          }
-        } else {
-          for (int t = 0; t < NT; ++t) {
-            if (t >= n) break;
-            const ActL act = load_act_l(A, t, b);
-            for (int r = 0; r < kRows; ++r)
-              terms[r * NT + t][lane][0] = legacy_term<T>(W, r0 + (r < nr ? r : nr - 1), b, act);
-          }
+        for (int t = 0; t < NT; ++t) {
+          if (t >= n) break;
+          ActL a;
+          if constexpr (FUSED)
+            a = quant_act_l<T == kQ5_1>(x + int64_t(t) * in + b * 32);
+          else
+            a = load_act_l(A, t, b);
+          for (int r = 0; r < RW; ++r) terms[r * NT + t][lane][0] = legacy_term<T>(W, r0 + (r < nr ? r : nr - 1), b, a);
         }
       }
     } else {
-      const int sbl = lane >> 3, k = lane & 7;
-      const bool live = sbl < nc;
-      const int64_t sb = c0 + (live ? sbl : 0);
-      for (int t = 0; t < NT; ++t) {
-        if (t >= n) break;
-        const ActK act = FUSED ? quant_act_k(x + int64_t(t) * in + sb * 256 + 32 * k, k) : load_act_k(A, t, sb, k);
-        for (int r = 0; r < kRows; ++r) {
-          const int64_t rr = r0 + (r < nr ? r : nr - 1);
+      for (int p = lane; p < RW * nc; p += 64) {
+        const int r = p / nc, bl = p % nc;
+        const int64_t rr = r0 + (r < nr ? r : nr - 1), b = c0 + bl;
+        for (int t = 0; t < NT; ++t) {
+          if (t >= n) break;
           int aux[8], sumi;
-          k_partials<T>(W, rr, sb, k, act, aux, sumi);
-#pragma unroll
-          for (int m = 1; m < 8; m <<= 1) {
-#pragma unroll
-            for (int l = 0; l < 8; ++l) aux[l] += __shfl_xor(aux[l], m, 64);
-            sumi += __shfl_xor(sumi, m, 64);
+          float da;
+          if constexpr (FUSED) {
+            const LdsActK& s = acts[t][bl];
+            k_lanes<T>(W, rr, b, [&](int k, int w) { return s.a[8 * k + w]; }, [&](int g) { return s.bs[g]; }, aux,
+                       sumi);
+            da = s.d;
+          } else {
+            const int64_t ab = int64_t(t) * A.nb + b;
+            const uint32_t* aq = reinterpret_cast<const uint32_t*>(A.qs + ab * 256);
+            const int16_t* bs = A.bsums + ab * 16;
+            k_lanes<T>(W, rr, b, [&](int k, int w) { return aq[8 * k + w]; }, [&](int g) { return int(bs[g]); },
+                       aux, sumi);
+            da = A.d[ab];
           }
-          if (live && k == 0) {
-            const int64_t wb = rr * W.nb + sb;
-            const float d = __fmul_rn(h2f(W.d[wb]), act.d);
+          const int64_t wb = rr * W.nb + b;
+          const float d = __fmul_rn(h2f(W.d[wb]), da);
 #pragma unroll
-            for (int l = 0; l < 8; ++l) terms[r * NT + t][sbl][l] = __fmul_rn(d, float(aux[l]));
-            terms[r * NT + t][sbl][8] = T == kQ6_K ? 0.f : __fmul_rn(__fmul_rn(h2f(W.m[wb]), act.d), float(sumi));
-          }
+          for (int l = 0; l < 8; ++l) terms[r * NT + t][bl][l] = __fmul_rn(d, float(aux[l]));
+          terms[r * NT + t][bl][8] = T == kQ6_K ? 0.f : __fmul_rn(__fmul_rn(h2f(W.m[wb]), da), float(sumi));
         }
       }
     }
@@ -539,8 +551,9 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(QW W, const int32_t* 
       scale_min_k4(k, W.s + wb * 16, sc, m);
       const float d1 = __fmul_rn(d, float(sc)), m1 = __fmul_rn(mn, float(m));
       for (int e = 0; e < 32; ++e) {
-        int q = (qs[32 * (k >> 1) + e] >> (4 * (k & 1))) & 0xF;
-        if constexpr (T == kQ5_K) q += ((W.h[wb * 32 + e] >> k) & 1) ? 16 : 0;
+        const int p = residue_pos(e);
+        int q = (qs[32 * (k >> 1) + p] >> (4 * (k & 1))) & 0xF;
+        if constexpr (T == kQ5_K) q += ((W.h[wb * 32 + p] >> k) & 1) ? 16 : 0;
         o[32 * k + e] = __fsub_rn(__fmul_rn(d1, float(q)), m1);
       }
     }
@@ -551,7 +564,8 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(QW W, const int32_t* 
       const uint8_t* ql = W.q + wb * 128 + 64 * h + 32 * (g & 1);
       const uint8_t* qh = W.h + wb * 64 + 32 * h;
       for (int e = 0; e < 32; ++e) {
-        const int q = (((ql[e] >> ((g >> 1) * 4)) & 0xF) | (((qh[e] >> (2 * g)) & 3) << 4)) - 32;
+        const int p = residue_pos(e);
+        const int q = (((ql[p] >> ((g >> 1) * 4)) & 0xF) | (((qh[p] >> (2 * g)) & 3) << 4)) - 32;
         const float dk = __fmul_rn(d, float(scl[2 * k + (e >> 4)]));
         o[32 * k + e] = __fmul_rn(dk, float(q));
       }
@@ -568,15 +582,20 @@ QW weight_of(int type, const void* w, int64_t rows, int64_t in) {
 }
 
 template <int T>
-int launch_gemv(const QBatch& B, int64_t waves, const QA& A, const float* x, int64_t in, int64_t n, bool fused,
-                hipStream_t s) {
+int launch_gemv(const QBatch& B, const int64_t* rows, int n_w, const QA& A, const float* x, int64_t in, int64_t n,
+                bool fused, hipStream_t s) {
+  const int rw = rows_per_wave(is_k(T), fused ? (n == 1 ? 1 : 4) : (n <= 4 ? 4 : 16));
+  QBatch b = B;
+  int64_t waves = 0;
+  for (int i = 0; i < n_w; ++i) b.wave0[i] = waves, waves += (rows[i] + rw - 1) / rw;
+  if (waves >= (int64_t(1) << 31)) return NBHS_EINVAL;
   const dim3 grid{unsigned(waves), 1, 1}, block{64, 1, 1};
   if (fused) {
-    if (n == 1) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 1, true>, grid, block, s, B, A, x, in, int(n));
-    return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4, true>, grid, block, s, B, A, x, in, int(n));
+    if (n == 1) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 1, true>, grid, block, s, b, A, x, in, int(n));
+    return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4, true>, grid, block, s, b, A, x, in, int(n));
   }
-  if (n <= 4) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4, false>, grid, block, s, B, A, x, in, int(n));
-  return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 16, false>, grid, block, s, B, A, x, in, int(n));
+  if (n <= 4) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4, false>, grid, block, s, b, A, x, in, int(n));
+  return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 16, false>, grid, block, s, b, A, x, in, int(n));
 }
 
 template <int T>
@@ -631,16 +650,12 @@ int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* row
   if (fused ? (!x || n > 4 || t0 != 0 || reinterpret_cast<uintptr_t>(x) % 16 || in % 4) : (t0 < 0 || t0 + n > n_acts))
     return NBHS_EINVAL;
   QBatch B{};
-  int64_t waves = 0;
   for (int i = 0; i < n_w; ++i) {
     if (!w[i] || !y[i] || rows[i] <= 0) return NBHS_EINVAL;
     B.w[i] = weight_of(type, w[i], rows[i], in);
     B.y[i] = y[i];
-    B.wave0[i] = waves;
-    waves += (rows[i] + kRows - 1) / kRows;
   }
   B.n_w = n_w;
-  if (waves >= (int64_t(1) << 31)) return NBHS_EINVAL;
   const int64_t nb = in / block_elems(type);
   QA A{};
   A.nb = nb;
@@ -656,13 +671,13 @@ int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* row
   }
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (type) {
-    case kQ4_0: return launch_gemv<kQ4_0>(B, waves, A, x, in, n, fused, s);
-    case kQ5_0: return launch_gemv<kQ5_0>(B, waves, A, x, in, n, fused, s);
-    case kQ5_1: return launch_gemv<kQ5_1>(B, waves, A, x, in, n, fused, s);
-    case kQ8_0: return launch_gemv<kQ8_0>(B, waves, A, x, in, n, fused, s);
-    case kQ4_K: return launch_gemv<kQ4_K>(B, waves, A, x, in, n, fused, s);
-    case kQ5_K: return launch_gemv<kQ5_K>(B, waves, A, x, in, n, fused, s);
-    case kQ6_K: return launch_gemv<kQ6_K>(B, waves, A, x, in, n, fused, s);
+    case kQ4_0: return launch_gemv<kQ4_0>(B, rows, n_w, A, x, in, n, fused, s);
+    case kQ5_0: return launch_gemv<kQ5_0>(B, rows, n_w, A, x, in, n, fused, s);
+    case kQ5_1: return launch_gemv<kQ5_1>(B, rows, n_w, A, x, in, n, fused, s);
+    case kQ8_0: return launch_gemv<kQ8_0>(B, rows, n_w, A, x, in, n, fused, s);
+    case kQ4_K: return launch_gemv<kQ4_K>(B, rows, n_w, A, x, in, n, fused, s);
+    case kQ5_K: return launch_gemv<kQ5_K>(B, rows, n_w, A, x, in, n, fused, s);
+    case kQ6_K: return launch_gemv<kQ6_K>(B, rows, n_w, A, x, in, n, fused, s);
     default: return NBHS_EINVAL;
   }
 }

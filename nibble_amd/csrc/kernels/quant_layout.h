@@ -9,7 +9,12 @@
 //   h  high bits: Q5_0 / Q5_1 the 32-bit qh word, Q5_K qh (32 bytes), Q6_K qh (64 bytes)
 //   s  sub-block scales: Q4_K / Q5_K the 12 packed bytes (padded to 16), Q6_K the 16 int8 scales
 //   d  the fp16 scale of every block; m the fp16 minimum (Q5_1) or dmin (Q4_K, Q5_K)
-// Bytes and their meaning are unchanged, so the arithmetic on them is the reference's.
+// Bytes and their meaning are unchanged, so the arithmetic on them is the reference's. One reordering: for the
+// K types every group of 32 bytes indexed by an element's position j in its 32-element sub-block (Q4_K / Q5_K qs
+// and qh, Q6_K ql and qh) is stored in residue order, byte j at position residue_pos(j) = 4 (j % 8) + j / 8, so
+// that 32-bit word w holds elements w, w + 8, w + 16, w + 24 - the four elements that feed the reference's integer
+// lane w (quant.cpp:118-144, 394-416: element e feeds lane e % 8) - and one v_dot4 gives a lane's partial sum.
+// Q8_K activation quants are stored in the same order.
 //
 // Activations are quantized on the device into planes too: qs (int8, 32 or 256 per block), d (float: the
 // block's scale, for Q8_0 / Q8_1 the fp16-rounded value widened exactly), s (float, Q8_1's fp16-rounded sum term)
@@ -41,6 +46,8 @@ constexpr int64_t block_bytes(int t) {  // ggml block size in the file
   }
 }
 constexpr int act_of(int t) { return t == kQ5_1 ? kActQ8_1 : is_k(t) ? kActQ8_K : kActQ8_0; }
+
+constexpr int residue_pos(int j) { return 4 * (j & 7) + (j >> 3); }
 
 // Bytes per block in each plane (0: the plane is absent).
 constexpr int64_t q_bytes(int t) { return t == kQ8_0 ? 32 : is_k(t) ? 128 : 16; }
