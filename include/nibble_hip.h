@@ -33,10 +33,11 @@ extern "C" {
 typedef struct nbh_backend nbh_backend;
 typedef struct nbh_event nbh_event;
 
-/* A weight view, field for field nibble::Tensor (src/tensor.h:21-66): type is the ggml type id (0 = F32, 1 = F16),
- * ne[1] * ne[2] * ne[3] rows of ne[0] elements, row-major at data. data is host memory (copied to HBM on first use
- * and kept until nbh_backend_release_weights; its bytes must not change meanwhile) or lies inside a buffer from
- * nbh_backend_alloc (used in place). */
+/* A weight view, field for field nibble::Tensor (src/tensor.h:21-66): type is the ggml type id (0 = F32, 1 = F16,
+ * 2 = Q4_0, 6 = Q5_0, 7 = Q5_1, 8 = Q8_0, 12 = Q4_K, 13 = Q5_K, 14 = Q6_K), ne[1] * ne[2] * ne[3] rows of ne[0]
+ * elements, row-major at data (quantized: rows of ggml blocks, src/quant.h). data is host memory (copied to HBM on
+ * first use - quantized weights repacked into aligned planes - and kept until nbh_backend_release_weights; its
+ * bytes must not change meanwhile) or, for F32 / F16, lies inside a buffer from nbh_backend_alloc (used in place). */
 typedef struct nbh_tensor {
   uint32_t type;
   int32_t n_dims;
@@ -54,8 +55,8 @@ int nbh_backend_create(int device, nbh_backend** out);
 /* Frees every buffer still allocated. Replaces CpuBackend::~CpuBackend (cpu_backend.cpp:70-72). */
 void nbh_backend_destroy(nbh_backend* be);
 
-/* Backend::supports (backend.h:41): whether weight type `dtype` (ggml id) can run matmul/embed: 1 for F32 (0) and
- * F16 (1), 0 for the quantized types. */
+/* Backend::supports (backend.h:41): whether weight type `dtype` (ggml id) can run matmul/embed: 1 for every type
+ * the reference supports (F32, F16, Q4_0, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K). */
 int nbh_backend_supports(const nbh_backend* be, uint32_t dtype, int* out);
 
 /* Backend::reserve (backend.h:45; ReserveParams backend.h:24-26). */
@@ -122,8 +123,10 @@ int nbh_backend_append_rope_attention_batch(nbh_backend* be, int64_t n_seq, cons
                                             int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float freq_base,
                                             int neox, const float* freq_factors);
 
-/* Backend::matmul (backend.h:56): y[n, w.rows] = x[n, w.ne[0]] . W^T for F32/F16 weights (ref_ops.cpp:109-135),
- * fp32 products and sums in another order than the reference's (equal within float rounding). x, y device. */
+/* Backend::matmul (backend.h:56): y[n, w.rows] = x[n, w.ne[0]] . W^T (ref_ops.cpp:109-135). F32/F16 weights: fp32
+ * products and sums in another order than the reference's (equal within float rounding). Quantized weights: the
+ * activation rows quantized to the type's companion format and the block dots of quant.cpp:305-419, bit-exact.
+ * x, y device. */
 int nbh_backend_matmul(nbh_backend* be, const nbh_tensor* w, const float* x, float* y, int64_t n);
 
 /* Backend::matmul_multi (backend.h:57-60): ys[i] = matmul(ws[i], x, n) for n_w weights sharing the input x; the
