@@ -357,7 +357,7 @@ class KernelTiming:
     include/nibble_hip_shim.h). Used by the benchmark for roofline figures."""
 
     (ROPE, APPEND_ROPE, DECODE_PARTIAL, DECODE_COMBINE, GENERIC, STAGE_KV, PREFILL_MFMA, GEMV, CONVERT, ADD_BIAS, RMSNORM,
-     ELEMENTWISE, QUANTIZE, QGEMV) = range(14)
+     ELEMENTWISE, QUANTIZE, QGEMV, QGEMM) = range(15)
 
     @staticmethod
     def enable(on: bool = True, only: int | None = None):

@@ -3,8 +3,8 @@
 //  * embed (ref_ops.cpp:80-99): row copy for F32 tables, exact widening for F16; bit-exact.
 //  * rmsnorm (ref_ops.cpp:137-148): sum of squares in double (float * float is exact in double, so only the order
 //    of the sum differs from the reference), scale = 1 / sqrt(ss / d + eps) in double, y = float(x * scale * w)
-//    with the reference's two double products in its order. The double operations are written as explicitly
-//    rounded intrinsics, so no contraction into fused multiply-adds changes them.
+//    with the reference's two double products in its order. The file is compiled with -ffp-contract=off, so no
+//    multiply-add is fused (the reference's ref_ops.cpp is built the same way).
 //  * add (ref_ops.cpp:151-153): one float add per element; bit-exact.
 //  * silu_mul (ref_ops.cpp:217-222): gate = g / (1 + exp(-g)) * up in float; exp is the device library's expf,
 //    so results match the reference within a few ulp (the reference's own SIMD tier uses its own exp too).

@@ -6,7 +6,8 @@
 // type's companion format (Q8_0, Q8_1 or Q8_K), and y[t, r] = sum over blocks b of a per-block term, summed in block
 // order. The integer part of every term is exact, so it is computed in any order (here with v_dot4 where it
 // applies); the float part - the scale products and the running sum over blocks - is the reference's expression,
-// evaluated with explicitly rounded operations (no contraction) and in its order:
+// in its order, with no multiply-add contraction (this file is compiled with -ffp-contract=off, as the reference's
+// quant.cpp is; the __f*_rn spellings only mark the rounding points):
 //   Q4_0  sum += (float(isum) * d_w) * d_a          quant.cpp:309-325
 //   Q8_0  sum += float(isum) * (d_w * d_a)          :329-342
 //   Q5_0  sum += (d_w * d_a) * float(isum)          :346-365
@@ -513,6 +514,129 @@ __global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* 
   }
 }
 
+// ---- the tiled matmul for longer calls (prefill chunks) ----
+//
+// qgemm_legacy_kernel: a 256-thread workgroup computes 64 weight rows x 64 activation rows; thread (ri, ti) owns rows
+// ri + 16i and activation rows ti + 16j (i, j < 4). Chunks of 8 blocks of both operands are staged in LDS; each
+// thread walks the chunk's blocks in order and adds each block's term to its 16 sums, so every output is the
+// reference's ordered sum (the same terms as qgemv_kernel, the same bits).
+constexpr int kGemmCB = 8;  // blocks per staged chunk
+
+template <int T>
+__global__ __launch_bounds__(256) void qgemm_legacy_kernel(QW W, QA A, float* __restrict__ y, int64_t n) {
+  constexpr int QB = T == kQ8_0 ? 32 : 16;           // quant bytes per block
+  constexpr int QW4 = QB / 16;                        // uint4 per block
+  constexpr int WROW = kGemmCB * QW4 + 1;             // uint4 per staged weight row (one of padding: spreads banks)
+  __shared__ uint4 wq[64 * WROW];
+  __shared__ uint16_t wd[64][kGemmCB], wm[64][kGemmCB];
+  __shared__ uint32_t wh[64][kGemmCB];
+  __shared__ uint4 aq[64][kGemmCB][2];
+  __shared__ float ad[64][kGemmCB], as_[64][kGemmCB];
+  const int tid = threadIdx.x, ri = tid & 15, ti = tid >> 4;
+  const int64_t row0 = int64_t(blockIdx.x) * 64, t0 = int64_t(blockIdx.y) * 64;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+  for (int64_t c0 = 0; c0 < W.nb; c0 += kGemmCB) {
+    const int nc = int(W.nb - c0 < kGemmCB ? W.nb - c0 : kGemmCB);
+    // stage: rows and activation rows past the ends, and blocks past the chunk's end, load clamped (unused)
+    for (int e = tid; e < 64 * kGemmCB * QW4; e += 256) {
+      const int r = e / (kGemmCB * QW4), rem = e % (kGemmCB * QW4), b = rem / QW4, part = rem % QW4;
+      const int64_t rr = min(row0 + r, W.rows - 1), bb = c0 + min(b, nc - 1);
+      wq[r * WROW + b * QW4 + part] = reinterpret_cast<const uint4*>(W.q + (rr * W.nb + bb) * QB)[part];
+    }
+    for (int e = tid; e < 64 * kGemmCB; e += 256) {
+      const int r = e / kGemmCB, b = e % kGemmCB;
+      const int64_t wb = min(row0 + r, W.rows - 1) * W.nb + c0 + min(b, nc - 1);
+      wd[r][b] = W.d[wb];
+      if constexpr (T == kQ5_1) wm[r][b] = W.m[wb];
+      if constexpr (T == kQ5_0 || T == kQ5_1) wh[r][b] = reinterpret_cast<const uint32_t*>(W.h)[wb];
+      const int64_t ab = min(t0 + r, n - 1) * A.nb + c0 + min(b, nc - 1);
+      ad[r][b] = A.d[ab];
+      if constexpr (T == kQ5_1) as_[r][b] = A.s[ab];
+      const uint4* ap = reinterpret_cast<const uint4*>(A.qs + ab * 32);
+      aq[r][b][0] = ap[0];
+      aq[r][b][1] = ap[1];
+    }
+    __syncthreads();
+    for (int b = 0; b < nc; ++b) {
+      ActL act[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = ti + 16 * j;
+        const uint4 a0 = aq[t][b][0], a1 = aq[t][b][1];
+        ActL& a = act[j];
+        a.a[0] = a0.x, a.a[1] = a0.y, a.a[2] = a0.z, a.a[3] = a0.w, a.a[4] = a1.x, a.a[5] = a1.y, a.a[6] = a1.z,
+        a.a[7] = a1.w;
+        a.d = ad[t][b];
+        a.s = T == kQ5_1 ? as_[t][b] : 0.f;
+        a.sum = 0;
+        if constexpr (T == kQ4_0 || T == kQ5_0) {
+#pragma unroll
+          for (int w = 0; w < 8; ++w) a.sum = sdot4(a.a[w], 0x01010101u, a.sum);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = ri + 16 * i;
+        const float dw = h2f(wd[r][b]);
+        if constexpr (T == kQ8_0) {
+          const uint4 w0 = wq[r * WROW + 2 * b], w1 = wq[r * WROW + 2 * b + 1];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const ActL& a = act[j];
+            int s = sdot4(w0.x, a.a[0], 0);
+            s = sdot4(w0.y, a.a[1], s), s = sdot4(w0.z, a.a[2], s), s = sdot4(w0.w, a.a[3], s);
+            s = sdot4(w1.x, a.a[4], s), s = sdot4(w1.y, a.a[5], s), s = sdot4(w1.z, a.a[6], s);
+            s = sdot4(w1.w, a.a[7], s);
+            acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(float(s), __fmul_rn(dw, a.d)));
+          }
+        } else {
+          const uint4 wv = wq[r * WROW + b];
+          const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
+          uint32_t lo[4], hi[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) lo[k] = w4[k] & 0x0F0F0F0Fu, hi[k] = (w4[k] >> 4) & 0x0F0F0F0Fu;
+          if constexpr (T == kQ5_0 || T == kQ5_1) {
+            const uint32_t qh = wh[r][b];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int jj = 4 * k + e;
+                lo[k] |= ((qh >> jj) & 1u) << (8 * e + 4);
+                hi[k] |= ((qh >> (jj + 16)) & 1u) << (8 * e + 4);
+              }
+          }
+          const float mw = T == kQ5_1 ? h2f(wm[r][b]) : 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const ActL& a = act[j];
+            int s = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) s = sdot4(lo[k], a.a[k], s), s = sdot4(hi[k], a.a[k + 4], s);
+            float term;
+            if constexpr (T == kQ4_0) term = __fmul_rn(__fmul_rn(float(s - 8 * a.sum), dw), a.d);
+            if constexpr (T == kQ5_0) term = __fmul_rn(__fmul_rn(dw, a.d), float(s - 16 * a.sum));
+            if constexpr (T == kQ5_1) term = __fadd_rn(__fmul_rn(__fmul_rn(dw, a.d), float(s)), __fmul_rn(mw, a.s));
+            acc[i][j] = __fadd_rn(acc[i][j], term);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t r = row0 + ri + 16 * i, t = t0 + ti + 16 * j;
+      if (r < W.rows && t < n) y[t * W.rows + r] = acc[i][j];
+    }
+}
+
 // ---- dequantization (quant.cpp:157-242), one thread per block of one output row ----
 
 template <int T>
@@ -678,6 +802,28 @@ int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* row
     case kQ4_K: return launch_gemv<kQ4_K>(B, rows, n_w, A, x, in, n, fused, s);
     case kQ5_K: return launch_gemv<kQ5_K>(B, rows, n_w, A, x, in, n, fused, s);
     case kQ6_K: return launch_gemv<kQ6_K>(B, rows, n_w, A, x, in, n, fused, s);
+    default: return NBHS_EINVAL;
+  }
+}
+
+int nbhs_qgemm(int type, const void* w, int64_t rows, int64_t in, const void* acts, int64_t n, float* y,
+               nbhs_stream stream) {
+  if (!is_quant(type) || is_k(type) || !w || !acts || !y || rows <= 0 || in <= 0 || in % block_elems(type) ||
+      n <= 0 || (rows + 63) / 64 >= (int64_t(1) << 31) || (n + 63) / 64 > 65535)
+    return NBHS_EINVAL;
+  const QW W = weight_of(type, w, rows, in);
+  const int act = act_of(type);
+  const ActLayout l = act_layout(act, n, W.nb);
+  const uint8_t* base = static_cast<const uint8_t*>(acts);
+  const QA A{reinterpret_cast<const int8_t*>(base + l.qs_off), reinterpret_cast<const float*>(base + l.d_off),
+             act == kActQ8_1 ? reinterpret_cast<const float*>(base + l.s_off) : nullptr, nullptr, W.nb};
+  const dim3 grid{unsigned((rows + 63) / 64), unsigned((n + 63) / 64), 1}, block{256, 1, 1};
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (type) {
+    case kQ4_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ4_0>, grid, block, s, W, A, y, n);
+    case kQ5_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_0>, grid, block, s, W, A, y, n);
+    case kQ5_1: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_1>, grid, block, s, W, A, y, n);
+    case kQ8_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ8_0>, grid, block, s, W, A, y, n);
     default: return NBHS_EINVAL;
   }
 }
