@@ -304,6 +304,63 @@ __device__ __forceinline__ float legacy_term(const QW& W, int64_t rr, int64_t b,
   return 0.f;
 }
 
+// A legacy weight block in registers (loaded ahead of the activation work that hides its latency).
+struct WBlk {
+  uint4 q0, q1;  // quants (q1: Q8_0's second half)
+  uint32_t h;    // Q5_0 / Q5_1 high bits
+  uint16_t d, m;
+};
+
+template <int T>
+__device__ __forceinline__ WBlk load_wblk(const QW& W, int64_t rr, int64_t b) {
+  const int64_t wb = rr * W.nb + b;
+  WBlk k;
+  if constexpr (T == kQ8_0) {
+    const uint4* wp = reinterpret_cast<const uint4*>(W.q + wb * 32);
+    k.q0 = wp[0], k.q1 = wp[1];
+  } else {
+    k.q0 = *reinterpret_cast<const uint4*>(W.q + wb * 16);
+  }
+  if constexpr (T == kQ5_0 || T == kQ5_1) k.h = reinterpret_cast<const uint32_t*>(W.h)[wb];
+  k.d = W.d[wb];
+  if constexpr (T == kQ5_1) k.m = W.m[wb];
+  return k;
+}
+
+// legacy_term on a preloaded weight block.
+template <int T>
+__device__ __forceinline__ float wblk_term(const WBlk& k, const ActL& A) {
+  const float dw = h2f(k.d), da = A.d;
+  if constexpr (T == kQ8_0) {
+    int s = sdot4(k.q0.x, A.a[0], 0);
+    s = sdot4(k.q0.y, A.a[1], s), s = sdot4(k.q0.z, A.a[2], s), s = sdot4(k.q0.w, A.a[3], s);
+    s = sdot4(k.q1.x, A.a[4], s), s = sdot4(k.q1.y, A.a[5], s), s = sdot4(k.q1.z, A.a[6], s), s = sdot4(k.q1.w, A.a[7], s);
+    return __fmul_rn(float(s), __fmul_rn(dw, da));
+  } else {
+    const uint32_t w[4] = {k.q0.x, k.q0.y, k.q0.z, k.q0.w};
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo[i] = w[i] & 0x0F0F0F0Fu, hi[i] = (w[i] >> 4) & 0x0F0F0F0Fu;
+    if constexpr (T == kQ5_0 || T == kQ5_1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 4 * i + e;
+          lo[i] |= ((k.h >> j) & 1u) << (8 * e + 4);
+          hi[i] |= ((k.h >> (j + 16)) & 1u) << (8 * e + 4);
+        }
+    }
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s = sdot4(lo[i], A.a[i], s), s = sdot4(hi[i], A.a[i + 4], s);
+    if constexpr (T == kQ4_0) return __fmul_rn(__fmul_rn(float(s - 8 * A.sum), dw), da);
+    if constexpr (T == kQ5_0) return __fmul_rn(__fmul_rn(dw, da), float(s - 16 * A.sum));
+    if constexpr (T == kQ5_1) return __fadd_rn(__fmul_rn(__fmul_rn(dw, da), float(s)), __fmul_rn(h2f(k.m), A.s));
+  }
+  return 0.f;
+}
+
 // ggml get_scale_min_k4 (quant.cpp:52-61)
 __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& d, int& m) {
   if (j < 4) {
@@ -392,8 +449,11 @@ struct QBatch {  // weights of one type sharing one input; wave0: first wave of 
 };
 
 // Weight rows per wave: a legacy row has a block per lane (in = 2048: 64 blocks), a K row a super-block per lane
-// (in = 2048: 8), so K waves take twice the rows; with 16 activation rows a wave's outputs are capped at 64.
-constexpr int rows_per_wave(bool k, int NT) { return NT > 4 ? 4 : k ? 8 : 4; }
+// (in = 2048: 8), so K waves take twice the rows; with 16 activation rows a wave's outputs are capped at 64. A
+// single-row launch over many rows (an FFN's 16384) takes 16 rows per wave: the activation row each wave quantizes
+// is then shared by more weight rows, and there are still a thousand or more waves.
+constexpr int rows_per_wave(bool k, int NT, bool wide) { return NT > 4 ? 4 : k ? 8 : wide && NT == 1 ? 16 : 4; }
+constexpr int64_t kWideRows = 16384;  // total rows of a launch from which single-row launches go wide
 
 // A K activation super-block staged in LDS on the fused path: 256 quants in residue order, d, the 16-sums.
 struct LdsActK {
@@ -403,10 +463,10 @@ struct LdsActK {
 };
 
 // FUSED: the activation rows are quantized here, from x (NT <= 4), instead of read from A.
-template <int T, int NT, bool FUSED>
+template <int T, int NT, bool FUSED, bool WIDE>
 __global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* __restrict__ x, int64_t in, int n) {
   constexpr bool K = T == kQ4_K || T == kQ5_K || T == kQ6_K;
-  constexpr int RW = rows_per_wave(K, NT);
+  constexpr int RW = rows_per_wave(K, NT, WIDE);
   constexpr int O = RW * NT;  // outputs of this wave
   constexpr int CH = K ? 8 : 64;  // blocks per chunk
   constexpr int TERMS = K ? 9 : 1;
@@ -450,6 +510,10 @@ __global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* 
     if constexpr (!K) {  // a block per lane; its activation block (quantized here when fused) serves every row
       if (lane < nc) {
         const int64_t b = c0 + lane;
+        // every row's weight block is requested before the activation work, which hides the loads' latency
+        WBlk wk[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) wk[r] = load_wblk<T>(W, r0 + (r < nr ? r : nr - 1), b);
         for (int t = 0; t < NT; ++t) {
           if (t >= n) break;
           ActL a;
@@ -457,7 +521,8 @@ __global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* 
             a = quant_act_l<T == kQ5_1>(x + int64_t(t) * in + b * 32);
           else
             a = load_act_l(A, t, b);
-          for (int r = 0; r < RW; ++r) terms[r * NT + t][lane][0] = legacy_term<T>(W, r0 + (r < nr ? r : nr - 1), b, a);
+#pragma unroll
+          for (int r = 0; r < RW; ++r) terms[r * NT + t][lane][0] = wblk_term<T>(wk[r], a);
         }
       }
     } else {
@@ -708,18 +773,25 @@ QW weight_of(int type, const void* w, int64_t rows, int64_t in) {
 template <int T>
 int launch_gemv(const QBatch& B, const int64_t* rows, int n_w, const QA& A, const float* x, int64_t in, int64_t n,
                 bool fused, hipStream_t s) {
-  const int rw = rows_per_wave(is_k(T), fused ? (n == 1 ? 1 : 4) : (n <= 4 ? 4 : 16));
+  int64_t total = 0;
+  for (int i = 0; i < n_w; ++i) total += rows[i];
+  const bool wide = fused && n == 1 && total >= kWideRows;
+  const int rw = rows_per_wave(is_k(T), fused ? (n == 1 ? 1 : 4) : (n <= 4 ? 4 : 16), wide);
   QBatch b = B;
   int64_t waves = 0;
   for (int i = 0; i < n_w; ++i) b.wave0[i] = waves, waves += (rows[i] + rw - 1) / rw;
   if (waves >= (int64_t(1) << 31)) return NBHS_EINVAL;
   const dim3 grid{unsigned(waves), 1, 1}, block{64, 1, 1};
   if (fused) {
-    if (n == 1) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 1, true>, grid, block, s, b, A, x, in, int(n));
-    return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4, true>, grid, block, s, b, A, x, in, int(n));
+    if (wide)
+      return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 1, true, true>, grid, block, s, b, A, x, in, int(n));
+    if (n == 1)
+      return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 1, true, false>, grid, block, s, b, A, x, in, int(n));
+    return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4, true, false>, grid, block, s, b, A, x, in, int(n));
   }
-  if (n <= 4) return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4, false>, grid, block, s, b, A, x, in, int(n));
-  return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 16, false>, grid, block, s, b, A, x, in, int(n));
+  if (n <= 4)
+    return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 4, false, false>, grid, block, s, b, A, x, in, int(n));
+  return nbhs_timing::launch(NBHS_K_QGEMV, qgemv_kernel<T, 16, false, false>, grid, block, s, b, A, x, in, int(n));
 }
 
 template <int T>

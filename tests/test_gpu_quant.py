@@ -137,3 +137,20 @@ def test_quantized_tiny_model_matches_naive(backend, t):
     assert cos >= 0.999
     assert int(np.argmax(got)) == int(np.argmax(ref))
     assert np.all(np.isfinite(inc))
+
+
+@pytest.mark.parametrize("t", [oracle.Q4_0, oracle.Q5_1, oracle.Q8_0, oracle.Q4_K], ids=["Q4_0", "Q5_1", "Q8_0", "Q4_K"])
+def test_quant_single_row_over_many_rows(backend, t):
+    """A single activation row against 16400 weight rows in one call (an FFN-sized launch, which takes 16 rows per
+    wave for the legacy types), bit-exact."""
+    in_ = 256
+    rows = 16400
+    w = U.random_qmat(t, rows, in_, seed=31 + t)
+    x = np.random.default_rng(t).standard_normal((1, in_)).astype(np.float32)
+    with Buffers(backend) as B:
+        dx, dy = B.upload(x), B.alloc(rows)
+        backend.matmul(w, dx, dy, 1)
+        got = backend.download(dy, (1, rows))
+    ref = oracle.matmul_q(t, w.raw, in_, rows, x)
+    assert np.array_equal(bits(got), bits(ref))
+    backend.release_weights()
