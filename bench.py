@@ -269,8 +269,9 @@ QUANT_NAMES = {2: "Q4_0", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}
 def quant_projection(be, steps, warmup, chunk=512, chunk_reps=2):
     """The same QKV projection with quantized weights (Llama-3.2-1B shape, 16 layers; synthetic blocks of each
     type): one launch per layer for the three weights, the activation row quantized inside it, bit-exact with the
-    reference's quant.cpp. Decode (n = 1): HBM GB/s of the weight blocks (file bytes) streamed per launch. Prefill
-    chunks (n = 512): integer-op rate of the block dots."""
+    reference's quant.cpp. Decode (n = 1): HBM GB/s of the weight blocks (file bytes) streamed per launch, for the
+    QKV launch and for the FFN's gate + up launch (2 x 8192 x 2048). Prefill chunks (n = 512): integer-op rate of
+    the block dots."""
     from nibble_amd import synth
     shape = configs.LLAMA32_1B
     E, Q, kvw, NL = shape.n_embd, shape.n_heads * shape.head_dim, shape.n_kv_heads * shape.head_dim, 16
@@ -314,13 +315,38 @@ def quant_projection(be, steps, warmup, chunk=512, chunk_reps=2):
         us = g_ms / g_n * 1e3
         gbs = alg / (us * 1e-6) / 1e9
         tops = NL * 2 * chunk * E * (Q + 2 * kvw) / (pre_ms * 1e-3) / 1e12
+        be.release_weights()
+        # the FFN's gate + up projection (2 x 8192 x 2048) at decode: the largest single-row launch of a layer
+        FF = 8192
+        fraws = [[synth.quant_weight(t, FF, E, 7000 + 10 * l + i) for i in range(2)] for l in range(4)]
+        fws = [[nibble_amd.weight(r, shape=(FF, E), dtype=t) for r in rl] for rl in fraws]
+        g_buf, u_buf = be.alloc(FF), be.alloc(FF)
+        for l in range(4):
+            be.matmul_multi(fws[l], x, [g_buf, u_buf], 1)
+        be.sync()
+        KernelTiming.enable(True, only=KernelTiming.QGEMV)
+        for _ in range(steps // 4):
+            for l in range(4):
+                be.matmul_multi(fws[l], x, [g_buf, u_buf], 1)
+        be.sync()
+        f_ms, f_n = KernelTiming.read(KernelTiming.QGEMV)
+        KernelTiming.enable(False)
+        be.free(g_buf)
+        be.free(u_buf)
+        f_alg = sum(r.nbytes for r in fraws[0]) + E * 4 + 2 * FF * 4
+        f_us = f_ms / f_n * 1e3
+        f_gbs = f_alg / (f_us * 1e-6) / 1e9
         out[name] = {"decode": {"avg_launch_us": round(us, 3), "value": round(gbs, 1), "unit": "GB/s",
                                 "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": alg,
                                 "us_per_step_16_layers": round(dec_ms / steps * 1e3, 1)},
+                     "ffn_gate_up_decode": {"avg_launch_us": round(f_us, 3), "value": round(f_gbs, 1), "unit": "GB/s",
+                                            "frac": round(f_gbs / HBM_PEAK_GBS, 4),
+                                            "algorithmic_bytes_per_launch": f_alg},
                      "prefill_chunk": {"rows": chunk, "us_per_layer": round(pre_ms / NL * 1e3, 1),
                                        "value": round(tops, 2), "unit": "TOPS (block-dot MACs x 2)"}}
-        log(f"quant projection {name}: decode launch {us:.2f} us -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}) of "
-            f"{alg / 1e6:.2f} MB; prefill chunk {chunk}: {pre_ms / NL * 1e3:.1f} us/layer -> {tops:.1f} TOPS")
+        log(f"quant projection {name}: QKV decode launch {us:.2f} us -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}) of "
+            f"{alg / 1e6:.2f} MB; FFN gate+up decode {f_us:.2f} us -> {f_gbs:.0f} GB/s ({f_gbs / HBM_PEAK_GBS:.1%}) of "
+            f"{f_alg / 1e6:.2f} MB; QKV prefill chunk {chunk}: {pre_ms / NL * 1e3:.1f} us/layer -> {tops:.1f} TOPS")
         be.release_weights()
     for p in (x, q, kc, vc):
         be.free(p)
