@@ -186,8 +186,8 @@ def test_matmul_rejects_bad_arguments(backend):
     with Buffers(backend) as B:
         dx, dy = B.alloc(4 * 64), B.alloc(4 * 32)
         with pytest.raises(nibble_amd.BackendError, match="not supported"):
-            q8 = nibble_amd.weight(dx, shape=(2, 64), dtype=8)  # Q8_0
-            backend.matmul_multi([q8], dx, [dy], 1)
+            q3k = nibble_amd.weight(dx, shape=(2, 256), dtype=11)  # Q3_K: a ggml type the reference does not load
+            backend.matmul_multi([q3k], dx, [dy], 1)
         with pytest.raises(nibble_amd.BackendError, match="overlaps the input"):
             backend.matmul(w, dx, dx.at(64), 2)
         with pytest.raises(nibble_amd.BackendError, match="not inside one buffer"):
