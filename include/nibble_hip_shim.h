@@ -192,10 +192,11 @@ int nbhs_quantize_acts(int type, const float* x, int64_t n, int64_t in, void* ac
  * rows of x quantized inside the launch (the same bits). */
 int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* rows, float* const* y, int64_t in,
                      const float* x, const void* acts, int64_t n_acts, int64_t t0, int64_t n, nbhs_stream s);
-/* The same products for any n (prefill chunks), tiled: y[t * rows + r] for t < n over all n quantized activation
- * rows in acts; legacy types (Q4_0, Q5_0, Q5_1, Q8_0). Same bits as nbhs_qgemv_multi. */
-int nbhs_qgemm(int type, const void* w, int64_t rows, int64_t in, const void* acts, int64_t n, float* y,
-               nbhs_stream s);
+/* The same products for any n (prefill chunks), tiled, in one launch for up to NBHS_GEMV_MAX_WEIGHTS weights of
+ * one type: y[i][t * rows[i] + r] for t < n over all n quantized activation rows in acts; legacy types (Q4_0,
+ * Q5_0, Q5_1, Q8_0). Same bits as nbhs_qgemv_multi. */
+int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* rows, float* const* y, int64_t in,
+                     const void* acts, int64_t n, nbhs_stream s);
 /* out[t, :] = dequantized row ids[t] (device ids) of the weight, quant.cpp:157-242 bit for bit. */
 int nbhs_dequant_rows(int type, const void* w, int64_t rows, int64_t in, const int32_t* ids, int64_t n, float* out,
                       nbhs_stream s);

@@ -393,9 +393,20 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
     std::vector<size_t> idx;
     for (size_t i = 0; i < dw.size(); ++i)
       if (int(dw[i].type) == t) idx.push_back(i);
-    if (n > kGemvMaxRows && !nbh_quant::is_k(t)) {  // prefill chunks: the tiled kernel, one launch per weight
-      for (const size_t i : idx)
-        check(nbhs_qgemm(t, dw[i].dev, dw[i].rows, in, acts_buf_, n, ys[i], stream_), "matmul (quantized, tiled)");
+    if (n > kGemvMaxRows && !nbh_quant::is_k(t)) {  // prefill chunks: the tiled kernel, up to 8 weights a launch
+      for (size_t b = 0; b < idx.size(); b += kGemvMaxWeights) {
+        const size_t cnt = std::min(idx.size() - b, kGemvMaxWeights);
+        const void* wp[kGemvMaxWeights];
+        int64_t rows[kGemvMaxWeights];
+        float* yp[kGemvMaxWeights];
+        for (size_t j = 0; j < cnt; ++j) {
+          const size_t i = idx[b + j];
+          wp[j] = dw[i].dev;
+          rows[j] = dw[i].rows;
+          yp[j] = ys[i];
+        }
+        check(nbhs_qgemm_multi(t, int(cnt), wp, rows, yp, in, acts_buf_, n, stream_), "matmul (quantized, tiled)");
+      }
       continue;
     }
     for (size_t b = 0; b < idx.size(); b += kGemvMaxWeights) {

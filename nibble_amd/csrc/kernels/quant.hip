@@ -51,6 +51,14 @@ struct QA {
 __device__ __forceinline__ float h2f(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }  // RNE
 
+// v as a float in a register, opaque to the optimizer. fp16(a * b) is otherwise compiled to one v_fma_mix, which
+// rounds the exact product to fp16 once; the reference rounds to float first and then to fp16, and the two differ
+// when the float product lands on an fp16 tie.
+__device__ __forceinline__ float opaque(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4(int(a), int(b), c, false);
 }
@@ -95,7 +103,7 @@ __global__ __launch_bounds__(256) void quantize_q8_kernel(const float* __restric
   o[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
   o[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
   dq[i] = h2f(f2h(d));
-  if constexpr (Q81) sq[i] = h2f(f2h(__fmul_rn(float(sum), d)));
+  if constexpr (Q81) sq[i] = h2f(f2h(opaque(__fmul_rn(float(sum), d))));
 }
 
 // ggml nearest_int (quant.cpp:146-152): round half to even through the float mantissa.
@@ -210,7 +218,7 @@ __device__ __forceinline__ ActL quant_act_l(const float* xb) {
     r.a[w] = word;
   }
   r.d = h2f(f2h(d));
-  r.s = Q81 ? h2f(f2h(__fmul_rn(float(r.sum), d))) : 0.f;
+  r.s = Q81 ? h2f(f2h(opaque(__fmul_rn(float(r.sum), d)))) : 0.f;
   return r;
 }
 
@@ -584,11 +592,25 @@ __global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* 
 // qgemm_legacy_kernel: a 256-thread workgroup computes 64 weight rows x 64 activation rows; thread (ri, ti) owns rows
 // ri + 16i and activation rows ti + 16j (i, j < 4). Chunks of 8 blocks of both operands are staged in LDS; each
 // thread walks the chunk's blocks in order and adds each block's term to its 16 sums, so every output is the
-// reference's ordered sum (the same terms as qgemv_kernel, the same bits).
+// reference's ordered sum (the same terms as qgemv_kernel, the same bits). One launch covers the weights of one
+// type that share the input (a layer's Q, K and V): grid x runs over the row tiles of all of them, so small
+// weights do not leave most CUs idle.
 constexpr int kGemmCB = 8;  // blocks per staged chunk
 
+struct QGemmBatch {  // weights of one type sharing one input; tile0[i]: first row tile of weight i
+  QW w[kMaxQWeights];
+  float* y[kMaxQWeights];
+  int tile0[kMaxQWeights];
+  int n_w;
+};
+
 template <int T>
-__global__ __launch_bounds__(256) void qgemm_legacy_kernel(QW W, QA A, float* __restrict__ y, int64_t n) {
+__global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, int64_t n) {
+  int wi = 0;
+  for (int i = 1; i < B.n_w; ++i)
+    if (int(blockIdx.x) >= B.tile0[i]) wi = i;
+  const QW W = B.w[wi];
+  float* __restrict__ y = B.y[wi];
   constexpr int QB = T == kQ8_0 ? 32 : 16;           // quant bytes per block
   constexpr int QW4 = QB / 16;                        // uint4 per block
   constexpr int WROW = kGemmCB * QW4 + 1;             // uint4 per staged weight row (one of padding: spreads banks)
@@ -598,7 +620,7 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QW W, QA A, float* __
   __shared__ uint4 aq[64][kGemmCB][2];
   __shared__ float ad[64][kGemmCB], as_[64][kGemmCB];
   const int tid = threadIdx.x, ri = tid & 15, ti = tid >> 4;
-  const int64_t row0 = int64_t(blockIdx.x) * 64, t0 = int64_t(blockIdx.y) * 64;
+  const int64_t row0 = int64_t(int(blockIdx.x) - B.tile0[wi]) * 64, t0 = int64_t(blockIdx.y) * 64;
   float acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -878,24 +900,34 @@ int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* row
   }
 }
 
-int nbhs_qgemm(int type, const void* w, int64_t rows, int64_t in, const void* acts, int64_t n, float* y,
-               nbhs_stream stream) {
-  if (!is_quant(type) || is_k(type) || !w || !acts || !y || rows <= 0 || in <= 0 || in % block_elems(type) ||
-      n <= 0 || (rows + 63) / 64 >= (int64_t(1) << 31) || (n + 63) / 64 > 65535)
+int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* rows, float* const* y, int64_t in,
+                     const void* acts, int64_t n, nbhs_stream stream) {
+  if (!is_quant(type) || is_k(type) || n_w <= 0 || n_w > kMaxQWeights || !w || !rows || !y || !acts || in <= 0 ||
+      in % block_elems(type) || n <= 0 || (n + 63) / 64 > 65535)
     return NBHS_EINVAL;
-  const QW W = weight_of(type, w, rows, in);
+  QGemmBatch B{};
+  int64_t tiles = 0;
+  for (int i = 0; i < n_w; ++i) {
+    if (!w[i] || !y[i] || rows[i] <= 0) return NBHS_EINVAL;
+    B.w[i] = weight_of(type, w[i], rows[i], in);
+    B.y[i] = y[i];
+    B.tile0[i] = int(tiles);
+    tiles += (rows[i] + 63) / 64;
+    if (tiles >= (int64_t(1) << 31)) return NBHS_EINVAL;
+  }
+  B.n_w = n_w;
   const int act = act_of(type);
-  const ActLayout l = act_layout(act, n, W.nb);
+  const ActLayout l = act_layout(act, n, B.w[0].nb);
   const uint8_t* base = static_cast<const uint8_t*>(acts);
   const QA A{reinterpret_cast<const int8_t*>(base + l.qs_off), reinterpret_cast<const float*>(base + l.d_off),
-             act == kActQ8_1 ? reinterpret_cast<const float*>(base + l.s_off) : nullptr, nullptr, W.nb};
-  const dim3 grid{unsigned((rows + 63) / 64), unsigned((n + 63) / 64), 1}, block{256, 1, 1};
+             act == kActQ8_1 ? reinterpret_cast<const float*>(base + l.s_off) : nullptr, nullptr, B.w[0].nb};
+  const dim3 grid{unsigned(tiles), unsigned((n + 63) / 64), 1}, block{256, 1, 1};
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (type) {
-    case kQ4_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ4_0>, grid, block, s, W, A, y, n);
-    case kQ5_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_0>, grid, block, s, W, A, y, n);
-    case kQ5_1: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_1>, grid, block, s, W, A, y, n);
-    case kQ8_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ8_0>, grid, block, s, W, A, y, n);
+    case kQ4_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ4_0>, grid, block, s, B, A, n);
+    case kQ5_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_0>, grid, block, s, B, A, n);
+    case kQ5_1: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_1>, grid, block, s, B, A, n);
+    case kQ8_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ8_0>, grid, block, s, B, A, n);
     default: return NBHS_EINVAL;
   }
 }

@@ -108,6 +108,46 @@ def test_quant_rejects_bad_shapes(backend):
     assert all(backend.supports(t) for t in TYPES + [0, 1])
 
 
+LEGACY = [oracle.Q4_0, oracle.Q5_0, oracle.Q5_1, oracle.Q8_0]
+
+
+@pytest.mark.parametrize("t", LEGACY, ids=[U.NAMES[t] for t in LEGACY])
+def test_quant_tiled_many_weights_one_type(backend, t):
+    """Prefill-sized calls (n > 16) over nine weights of one legacy type: a tiled launch takes up to eight weights,
+    its grid runs over the row tiles of all of them (row counts that end inside a tile), and the ninth weight goes
+    to a second launch. Every output bit-exact."""
+    in_, n = 256, 80
+    rows = [70, 33, 130, 64, 1, 65, 7, 128, 40]
+    ws = [U.random_qmat(t, r, in_, seed=50 + i) for i, r in enumerate(rows)]
+    x = np.random.default_rng(9).standard_normal((n, in_)).astype(np.float32)
+    with Buffers(backend) as B:
+        dx = B.upload(x)
+        ys = [B.alloc(n * r) for r in rows]
+        backend.matmul_multi(ws, dx, ys, n)
+        got = [backend.download(y, (n, r)) for y, r in zip(ys, rows)]
+    for i, (g, w) in enumerate(zip(got, ws)):
+        assert np.array_equal(bits(g), bits(oracle.matmul_q(t, w.raw, in_, w.rows, x))), (U.NAMES[t], i)
+    backend.release_weights()
+
+
+@pytest.mark.parametrize("n", [1, 5, 20])
+def test_quant_q8_1_sum_term_tie(backend, n):
+    """Q5_1 against activations holding a block whose Q8_1 sum term float(sum) * d is an exact fp16 tie (the
+    reference rounds the product to float, then to fp16: down to the even neighbour here). Every activation path:
+    quantized inside the launch (n = 1), by the quantizer launch (n = 5) and under the tiled kernel (n = 20)."""
+    from tests.test_quant_oracle import tie_block
+    in_, rows = 256, 24
+    x = np.random.default_rng(3).standard_normal((n, in_)).astype(np.float32)
+    x[-1, 96:128] = tie_block()
+    w = U.random_qmat(oracle.Q5_1, rows, in_, seed=77)
+    with Buffers(backend) as B:
+        dx, dy = B.upload(x), B.alloc(n * rows)
+        backend.matmul(w, dx, dy, n)
+        got = backend.download(dy, (n, rows))
+    assert np.array_equal(bits(got), bits(oracle.matmul_q(oracle.Q5_1, w.raw, in_, rows, x)))
+    backend.release_weights()
+
+
 @pytest.mark.parametrize("t", [oracle.Q8_0, oracle.Q4_0], ids=["Q8_0", "Q4_0"])
 def test_quantized_tiny_model_matches_naive(backend, t):
     """tests/test_model.cpp:206-233 on the GPU: the reference's quant_dims tiny model (n_embd 32, n_ff 64, head_dim

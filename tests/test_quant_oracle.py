@@ -97,6 +97,26 @@ def test_fp32_to_fp16_against_numpy():
         assert np.array_equal(got, x.astype(np.float16).view(np.uint16))
 
 
+def tie_block():
+    """A 32-float block whose Q8_1 sum term float(sum) * d is, as a float, exactly 1358.5 * 2^-7 (an fp16 tie: the
+    reference rounds it to the even 1358 * 2^-7), while the exact product of sum and d lies just above the tie
+    (rounded once, straight to fp16, it would give 1359 * 2^-7)."""
+    return np.random.default_rng(9).standard_normal((80, 256)).astype(np.float32)[32, 96:128]
+
+
+def test_q8_1_sum_term_rounds_twice():
+    """quant.cpp:268: blk.s = fp32_to_fp16(float(sum) * d) - the product rounded to float, then to fp16."""
+    from fractions import Fraction
+    x = tie_block()
+    blk = oracle.quantize(1, x)
+    d = np.float32(np.max(np.abs(x))) / np.float32(127)
+    total = int(blk[4:].view(np.int8).astype(np.int64).sum())
+    prod = np.float32(total) * d
+    assert Fraction(float(prod)) * 128 == Fraction(2717, 2)  # the float product is the tie
+    assert Fraction(total) * Fraction(float(d)) * 128 > Fraction(2717, 2)  # the exact one lies above it
+    assert blk[2:4].view(np.float16)[0] == np.float16(1358 / 128)
+
+
 RAND_FILLS = {Q.Q4_0: G.fill_q4_0, Q.Q5_0: G.fill_q5_0, Q.Q5_1: G.fill_q5_1, Q.Q8_0: G.fill_q8_0, Q.Q4_K: G.fill_q4_k,
               Q.Q5_K: G.fill_q5_k, Q.Q6_K: G.fill_q6_k}
 ACT_FILLS = {0: G.fill_q8_0, 1: G.fill_q8_1, 2: G.fill_q8_k}
