@@ -383,17 +383,23 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
   const bool fuse = n <= 4 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && in % 4 == 0;
   int done_act = -1;
   for (const int t : types) {
-    if (!fuse && nbh_quant::act_of(t) != done_act) {
+    // prefill chunks: the tiled kernels (all but Q6_K), whose K-type activations are in residue-major order
+    const bool tiled = n > kGemvMaxRows && t != nbh_quant::kQ6_K;
+    const bool rm = tiled && nbh_quant::is_k(t);
+    const int act_key = 2 * nbh_quant::act_of(t) + (rm ? 1 : 0);
+    if (!fuse && act_key != done_act) {
       const int64_t ab = nbhs_quant_act_bytes(t, n, in);
       if (ab < 0) throw Error("matmul: invalid quantized shape");
       ensure(acts_buf_, acts_buf_bytes_, size_t(ab));
-      check(nbhs_quantize_acts(t, x, n, in, acts_buf_, stream_), "matmul (activation quantization)");
-      done_act = nbh_quant::act_of(t);
+      check(rm ? nbhs_quantize_acts_rm(t, x, n, in, acts_buf_, stream_)
+               : nbhs_quantize_acts(t, x, n, in, acts_buf_, stream_),
+            "matmul (activation quantization)");
+      done_act = act_key;
     }
     std::vector<size_t> idx;
     for (size_t i = 0; i < dw.size(); ++i)
       if (int(dw[i].type) == t) idx.push_back(i);
-    if (n > kGemvMaxRows && !nbh_quant::is_k(t)) {  // prefill chunks: the tiled kernel, up to 8 weights a launch
+    if (tiled) {  // up to 8 weights a launch
       for (size_t b = 0; b < idx.size(); b += kGemvMaxWeights) {
         const size_t cnt = std::min(idx.size() - b, kGemvMaxWeights);
         const void* wp[kGemvMaxWeights];

@@ -114,6 +114,10 @@ __device__ __forceinline__ int nearest_int(float f) {
 
 // One wave per 256-element super-block; lane l = 8k + w holds elements 32k + w + 8i (i < 4) of sub-block k: the four
 // elements of residue word w, which it stores as word w of the sub-block (residue order, quant_layout.h).
+// RM: the super-block's quants in residue-major order instead (byte 32 w + 4 k + i = element 32 k + w + 8 i), so
+// that residue w's 32 quants - the ones that feed the reference's integer lane w - are contiguous (the order
+// qgemm_k_kernel reads).
+template <bool RM>
 __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restrict__ x, int64_t in,
                                                           int8_t* __restrict__ qs, float* __restrict__ dq,
                                                           int16_t* __restrict__ bsums) {
@@ -154,7 +158,7 @@ __global__ __launch_bounds__(64) void quantize_q8k_kernel(const float* __restric
   }
 #pragma unroll
   for (int m = 1; m < 8; m <<= 1) b0 += __shfl_xor(b0, m, 64), b1 += __shfl_xor(b1, m, 64);
-  reinterpret_cast<uint32_t*>(qs + i * 256)[lane] = word;
+  reinterpret_cast<uint32_t*>(qs + i * 256)[RM ? 8 * w + k : lane] = word;
   if (w == 0) bsums[i * 16 + 2 * k] = int16_t(b0), bsums[i * 16 + 2 * k + 1] = int16_t(b1);
   if (lane == 0) dq[i] = nan ? __builtin_nanf("") : d;
 }
@@ -724,6 +728,135 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
     }
 }
 
+// qgemm_k_kernel: the tiled matmul for Q4_K and Q5_K on the int8 matrix cores (v_mfma_i32_16x16x32_i8).
+// The reference's integer lane w of a super-block is aux[w] = sum over sub-blocks k of s_k * (the dot of the four
+// quants of residue word w of sub-block k with the activation's) - a dot product over the 32 elements of residue
+// w, with the 6-bit sub-block scale s_k varying along it. Split into slices small enough that slice * quant fits
+// int8 (Q4_K: s = 8 s1 + s0, s0, s1 < 8, quants < 16; Q5_K: s = 16 s2 + 4 s1 + s0, slices < 4, quants < 32), each
+// slice is one exact integer MFMA over the residue (K = 32), and aux[w] = sum_i 2^(bits i) C_i, exactly. The float
+// arithmetic that follows is the reference's per output and block: d = fp16(d_w) * d_a, sums[w] += d * aux[w],
+// acc -= (fp16(dmin_w) * d_a) * sumi, result acc + sums[0] + ... + sums[7] - the same operations in the same order
+// as qgemv_kernel, so the same bits.
+// A workgroup (4 waves) takes 16 weight rows and 64 activation rows (16 per wave). Per super-block its threads
+// expand the 16 rows into slice * quant bytes in LDS (residue-major, 40-byte rows: conflict-free 8-byte reads);
+// each wave then runs 8 residues x slices MFMAs of 16 x 16 x 32, its activation operands read straight from the
+// residue-major Q8_K planes (quantize_q8k_kernel<true>). The accumulator layout gives lane l activation row
+// t0 + l % 16 and weight rows 4 (l / 16) + v, v < 4: 4 outputs and their 9 float accumulators per lane.
+constexpr int kKTileRows = 16;
+template <int T>
+constexpr int k_slices() { return T == kQ4_K ? 2 : 3; }
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+template <int T>
+__global__ __launch_bounds__(256) void qgemm_k_kernel(QGemmBatch B, QA A, int64_t n) {
+  static_assert(T == kQ4_K || T == kQ5_K, "Q4_K and Q5_K");
+  constexpr int NS = k_slices<T>();
+  constexpr int RW = 10;  // words per expanded (slice, residue, row) entry: 8 and 2 of padding
+  __shared__ __align__(16) uint32_t ew[NS][8][kKTileRows][RW];
+  __shared__ int mins[kKTileRows][8];
+  __shared__ float wdm[kKTileRows][2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int wi = 0;
+  for (int i = 1; i < B.n_w; ++i)
+    if (int(blockIdx.x) >= B.tile0[i]) wi = i;
+  const QW W = B.w[wi];
+  float* __restrict__ y = B.y[wi];
+  const int64_t row0 = int64_t(int(blockIdx.x) - B.tile0[wi]) * kKTileRows;
+  const int tl = lane & 15, g = lane >> 4;
+  const int64_t t = int64_t(blockIdx.y) * 64 + 16 * wave + tl, tc = t < n ? t : n - 1;
+  // expansion share: row er, residue rr, sub-blocks 4 hh .. 4 hh + 3
+  const int er = tid >> 4, rr = (tid >> 1) & 7, hh = tid & 1;
+  const int64_t erow = row0 + er < W.rows ? row0 + er : W.rows - 1;
+  float sums[8][4], acc[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    acc[v] = 0.f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) sums[w][v] = 0.f;
+  }
+  for (int64_t sb = 0; sb < W.nb; ++sb) {
+    {
+      const int64_t wb = erow * W.nb + sb;
+      const uint8_t* sc = W.s + wb * 16;
+      const uint32_t* qw = reinterpret_cast<const uint32_t*>(W.q + wb * 128);
+      const uint32_t raw[2] = {qw[8 * (2 * hh) + rr], qw[8 * (2 * hh + 1) + rr]};
+      uint32_t hraw = 0;
+      if constexpr (T == kQ5_K) hraw = reinterpret_cast<const uint32_t*>(W.h + wb * 32)[rr];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int k = 4 * hh + kk;
+        int sk, mk;
+        scale_min_k4(k, sc, sk, mk);
+        uint32_t q = (raw[kk >> 1] >> (4 * (kk & 1))) & 0x0F0F0F0Fu;
+        if constexpr (T == kQ5_K) {
+          q |= ((hraw >> k) & 0x01010101u) << 4;
+          ew[0][rr][er][k] = q * uint32_t(sk & 3);
+          ew[1][rr][er][k] = q * uint32_t((sk >> 2) & 3);
+          ew[2][rr][er][k] = q * uint32_t(sk >> 4);
+        } else {
+          ew[0][rr][er][k] = q * uint32_t(sk & 7);
+          ew[1][rr][er][k] = q * uint32_t(sk >> 3);
+        }
+        if (rr == 0) mins[er][k] = mk;
+      }
+      if (rr == 0 && hh == 0) {
+        wdm[er][0] = h2f(W.d[wb]);
+        wdm[er][1] = h2f(W.m[wb]);
+      }
+    }
+    __syncthreads();
+    const int64_t ab = tc * A.nb + sb;
+    const uint8_t* aq = reinterpret_cast<const uint8_t*>(A.qs) + ab * 256;
+    const float da = A.d[ab];
+    const int16_t* bsp = A.bsums + ab * 16;
+    int bsk[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) bsk[k] = int(bsp[2 * k]) + int(bsp[2 * k + 1]);
+    float dv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) dv[v] = __fmul_rn(wdm[4 * g + v][0], da);
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const uint2 bw = *reinterpret_cast<const uint2*>(aq + 32 * w + 8 * g);
+      const long bop = (long(bw.y) << 32) | long(bw.x);
+      i32x4_t c[NS];
+#pragma unroll
+      for (int sl = 0; sl < NS; ++sl) {
+        const uint2 aw = *reinterpret_cast<const uint2*>(&ew[sl][w][tl][2 * g]);
+        const long aop = (long(aw.y) << 32) | long(aw.x);
+        c[sl] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        int aux;
+        if constexpr (T == kQ5_K)
+          aux = c[0][v] + 4 * c[1][v] + 16 * c[2][v];
+        else
+          aux = c[0][v] + 8 * c[1][v];
+        sums[w][v] = __fadd_rn(sums[w][v], __fmul_rn(dv[v], float(aux)));
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int rv = 4 * g + v;
+      int sumi = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) sumi += bsk[k] * mins[rv][k];
+      acc[v] = __fsub_rn(acc[v], __fmul_rn(__fmul_rn(wdm[rv][1], da), float(sumi)));
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    float o = acc[v];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) o = __fadd_rn(o, sums[w][v]);
+    const int64_t r = row0 + 4 * g + v;
+    if (r < W.rows && t < n) y[t * W.rows + r] = o;
+  }
+}
+
 // ---- dequantization (quant.cpp:157-242), one thread per block of one output row ----
 
 template <int T>
@@ -848,8 +981,8 @@ int nbhs_quantize_acts(int type, const float* x, int64_t n, int64_t in, void* ac
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (act == kActQ8_K) {
     if (blocks >= (int64_t(1) << 31)) return NBHS_EINVAL;
-    return nbhs_timing::launch(NBHS_K_QUANTIZE, quantize_q8k_kernel, dim3(unsigned(blocks)), dim3(64), s, x, in, qs, d,
-                               reinterpret_cast<int16_t*>(base + l.bsums_off));
+    return nbhs_timing::launch(NBHS_K_QUANTIZE, quantize_q8k_kernel<false>, dim3(unsigned(blocks)), dim3(64), s, x, in,
+                               qs, d, reinterpret_cast<int16_t*>(base + l.bsums_off));
   }
   const dim3 grid{unsigned((blocks + 255) / 256), 1, 1};
   if (act == kActQ8_1)
@@ -857,6 +990,17 @@ int nbhs_quantize_acts(int type, const float* x, int64_t n, int64_t in, void* ac
                                reinterpret_cast<float*>(base + l.s_off));
   return nbhs_timing::launch(NBHS_K_QUANTIZE, quantize_q8_kernel<false>, grid, dim3(256), s, x, in, n, qs, d,
                              static_cast<float*>(nullptr));
+}
+
+int nbhs_quantize_acts_rm(int type, const float* x, int64_t n, int64_t in, void* acts, nbhs_stream stream) {
+  if (!is_k(type) || !x || !acts || n <= 0 || in <= 0 || in % 256) return NBHS_EINVAL;
+  const int64_t nb = in / 256, blocks = n * nb;
+  if (blocks >= (int64_t(1) << 31)) return NBHS_EINVAL;
+  const ActLayout l = act_layout(kActQ8_K, n, nb);
+  uint8_t* base = static_cast<uint8_t*>(acts);
+  return nbhs_timing::launch(NBHS_K_QUANTIZE, quantize_q8k_kernel<true>, dim3(unsigned(blocks)), dim3(64),
+                             reinterpret_cast<hipStream_t>(stream), x, in, reinterpret_cast<int8_t*>(base + l.qs_off),
+                             reinterpret_cast<float*>(base + l.d_off), reinterpret_cast<int16_t*>(base + l.bsums_off));
 }
 
 int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* rows, float* const* y, int64_t in,
@@ -902,9 +1046,10 @@ int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* row
 
 int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* rows, float* const* y, int64_t in,
                      const void* acts, int64_t n, nbhs_stream stream) {
-  if (!is_quant(type) || is_k(type) || n_w <= 0 || n_w > kMaxQWeights || !w || !rows || !y || !acts || in <= 0 ||
-      in % block_elems(type) || n <= 0 || (n + 63) / 64 > 65535)
+  if (!is_quant(type) || type == kQ6_K || n_w <= 0 || n_w > kMaxQWeights || !w || !rows || !y || !acts ||
+      in <= 0 || in % block_elems(type) || n <= 0 || (n + 63) / 64 > 65535)
     return NBHS_EINVAL;
+  const int64_t tile_rows = is_k(type) ? kKTileRows : 64;
   QGemmBatch B{};
   int64_t tiles = 0;
   for (int i = 0; i < n_w; ++i) {
@@ -912,7 +1057,7 @@ int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* row
     B.w[i] = weight_of(type, w[i], rows[i], in);
     B.y[i] = y[i];
     B.tile0[i] = int(tiles);
-    tiles += (rows[i] + 63) / 64;
+    tiles += (rows[i] + tile_rows - 1) / tile_rows;
     if (tiles >= (int64_t(1) << 31)) return NBHS_EINVAL;
   }
   B.n_w = n_w;
@@ -920,10 +1065,13 @@ int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* row
   const ActLayout l = act_layout(act, n, B.w[0].nb);
   const uint8_t* base = static_cast<const uint8_t*>(acts);
   const QA A{reinterpret_cast<const int8_t*>(base + l.qs_off), reinterpret_cast<const float*>(base + l.d_off),
-             act == kActQ8_1 ? reinterpret_cast<const float*>(base + l.s_off) : nullptr, nullptr, B.w[0].nb};
+             act == kActQ8_1 ? reinterpret_cast<const float*>(base + l.s_off) : nullptr,
+             act == kActQ8_K ? reinterpret_cast<const int16_t*>(base + l.bsums_off) : nullptr, B.w[0].nb};
   const dim3 grid{unsigned(tiles), unsigned((n + 63) / 64), 1}, block{256, 1, 1};
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (type) {
+    case kQ4_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ4_K>, grid, block, s, B, A, n);
+    case kQ5_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ5_K>, grid, block, s, B, A, n);
     case kQ4_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ4_0>, grid, block, s, B, A, n);
     case kQ5_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_0>, grid, block, s, B, A, n);
     case kQ5_1: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_1>, grid, block, s, B, A, n);

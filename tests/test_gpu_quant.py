@@ -130,6 +130,28 @@ def test_quant_tiled_many_weights_one_type(backend, t):
     backend.release_weights()
 
 
+@pytest.mark.parametrize("n", [17, 80, 130])
+def test_quant_tiled_k_types_mixed(backend, n):
+    """Prefill-sized calls over K-type weights: Q4_K and Q5_K run the int8 matrix-core kernel on residue-major
+    activations, Q6_K the row-chunked kernel on the standard layout, all in one call (the activations quantized
+    once per layout, in the order the types come); row counts that end inside a 16-row tile, three super-blocks
+    per row, activation rows that end inside a 64-row tile. Every output bit-exact."""
+    in_ = 768
+    spec = [(oracle.Q4_K, 70), (oracle.Q6_K, 33), (oracle.Q5_K, 16), (oracle.Q4_K, 1), (oracle.Q5_K, 45)]
+    ws = [U.random_qmat(t, r, in_, seed=300 + i) for i, (t, r) in enumerate(spec)]
+    x = (np.random.default_rng(n).standard_normal((n, in_)) * 2).astype(np.float32)
+    with Buffers(backend) as B:
+        dx = B.upload(x)
+        ys = [B.alloc(n * r) for _, r in spec]
+        backend.matmul_multi(ws, dx, ys, n)
+        got = [backend.download(y, (n, r)) for y, (_, r) in zip(ys, spec)]
+    for i, (g, w) in enumerate(zip(got, ws)):
+        ref = oracle.matmul_q(w.t, w.raw, in_, w.rows, x)
+        diff = int(np.sum(bits(g) != bits(ref)))
+        assert diff == 0, (U.NAMES[w.t], i, diff)
+    backend.release_weights()
+
+
 @pytest.mark.parametrize("n", [1, 5, 20])
 def test_quant_q8_1_sum_term_tie(backend, n):
     """Q5_1 against activations holding a block whose Q8_1 sum term float(sum) * d is an exact fp16 tie (the
