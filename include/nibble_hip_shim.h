@@ -193,11 +193,11 @@ int nbhs_quantize_acts(int type, const float* x, int64_t n, int64_t in, void* ac
 int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* rows, float* const* y, int64_t in,
                      const float* x, const void* acts, int64_t n_acts, int64_t t0, int64_t n, nbhs_stream s);
 /* nbhs_quantize_acts for the K types with each super-block's quants in residue-major order (byte 32 w + 4 k + i
- * holds element 32 k + w + 8 i), the layout nbhs_qgemm_multi reads for Q4_K and Q5_K. */
+ * holds element 32 k + w + 8 i), the layout nbhs_qgemm_multi reads for the K types. */
 int nbhs_quantize_acts_rm(int type, const float* x, int64_t n, int64_t in, void* acts, nbhs_stream s);
 /* The same products for any n (prefill chunks), tiled, in one launch for up to NBHS_GEMV_MAX_WEIGHTS weights of
  * one type: y[i][t * rows[i] + r] for t < n over all n quantized activation rows in acts; Q4_0, Q5_0, Q5_1, Q8_0
- * (acts from nbhs_quantize_acts) and Q4_K, Q5_K (acts from nbhs_quantize_acts_rm, int8 matrix cores). Same bits
+ * (acts from nbhs_quantize_acts) and Q4_K, Q5_K, Q6_K (acts from nbhs_quantize_acts_rm, int8 matrix cores). Same bits
  * as nbhs_qgemv_multi. */
 int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* rows, float* const* y, int64_t in,
                      const void* acts, int64_t n, nbhs_stream s);

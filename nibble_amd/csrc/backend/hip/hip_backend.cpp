@@ -383,8 +383,8 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
   const bool fuse = n <= 4 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && in % 4 == 0;
   int done_act = -1;
   for (const int t : types) {
-    // prefill chunks: the tiled kernels (all but Q6_K), whose K-type activations are in residue-major order
-    const bool tiled = n > kGemvMaxRows && t != nbh_quant::kQ6_K;
+    // prefill chunks: the tiled kernels, whose K-type activations are in residue-major order
+    const bool tiled = n > kGemvMaxRows;
     const bool rm = tiled && nbh_quant::is_k(t);
     const int act_key = 2 * nbh_quant::act_of(t) + (rm ? 1 : 0);
     if (!fuse && act_key != done_act) {

@@ -728,15 +728,18 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
     }
 }
 
-// qgemm_k_kernel: the tiled matmul for Q4_K and Q5_K on the int8 matrix cores (v_mfma_i32_16x16x32_i8).
-// The reference's integer lane w of a super-block is aux[w] = sum over sub-blocks k of s_k * (the dot of the four
-// quants of residue word w of sub-block k with the activation's) - a dot product over the 32 elements of residue
-// w, with the 6-bit sub-block scale s_k varying along it. Split into slices small enough that slice * quant fits
-// int8 (Q4_K: s = 8 s1 + s0, s0, s1 < 8, quants < 16; Q5_K: s = 16 s2 + 4 s1 + s0, slices < 4, quants < 32), each
-// slice is one exact integer MFMA over the residue (K = 32), and aux[w] = sum_i 2^(bits i) C_i, exactly. The float
-// arithmetic that follows is the reference's per output and block: d = fp16(d_w) * d_a, sums[w] += d * aux[w],
-// acc -= (fp16(dmin_w) * d_a) * sumi, result acc + sums[0] + ... + sums[7] - the same operations in the same order
-// as qgemv_kernel, so the same bits.
+// qgemm_k_kernel: the tiled matmul for the K types on the int8 matrix cores (v_mfma_i32_16x16x32_i8).
+// The reference's integer lane w of a super-block is aux[w] = sum over the 32 elements e of residue w (four per
+// sub-block) of s(e) * q(e) * a(e), with the sub-block scale s varying along it. s * q is split into slices small
+// enough that each slice's per-element product fits int8, each slice is one exact integer MFMA over the residue
+// (K = 32), and aux[w] = sum_i c_i C_i, exactly:
+//   Q4_K: s = 8 s1 + s0 (s0, s1 < 8), q < 16                        -> s0 q, s1 q            (c = 1, 8)
+//   Q5_K: s = 16 s2 + 4 s1 + s0 (each < 4), q < 32                   -> s0 q, s1 q, s2 q      (c = 1, 4, 16)
+//   Q6_K: s signed 8-bit per 16 elements = 16 s1 + s0 (s0 < 16, -8 <= s1 < 8), q - 32 = 8 u1 + u0 (u0 < 8,
+//         -4 <= u1 < 4)                                              -> s1 u1, s1 u0, s0 u1, s0 u0 (c = 128, 16, 8, 1)
+// The float arithmetic that follows is the reference's per output and block: d = fp16(d_w) * d_a, sums[w] +=
+// d * aux[w], for Q4_K / Q5_K acc -= (fp16(dmin_w) * d_a) * sumi, result acc + sums[0] + ... + sums[7] - the same
+// operations in the same order as qgemv_kernel, so the same bits.
 // A workgroup (4 waves) takes 16 weight rows and 64 activation rows (16 per wave). Per super-block its threads
 // expand the 16 rows into slice * quant bytes in LDS (residue-major, 40-byte rows: conflict-free 8-byte reads);
 // each wave then runs 8 residues x slices MFMAs of 16 x 16 x 32, its activation operands read straight from the
@@ -744,13 +747,22 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
 // t0 + l % 16 and weight rows 4 (l / 16) + v, v < 4: 4 outputs and their 9 float accumulators per lane.
 constexpr int kKTileRows = 16;
 template <int T>
-constexpr int k_slices() { return T == kQ4_K ? 2 : 3; }
+constexpr int k_slices() { return T == kQ4_K ? 2 : T == kQ5_K ? 3 : 4; }
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+
+// Bytes b of the result hold lo16(x_b * y_b) & 0xFF for the four bytes of a word, with x_b, y_b small signed
+// values given as 16-bit lanes: ex / ox the even / odd bytes' x, sy the y of bytes 0 and 1 (lane 0) and of bytes 2
+// and 3 (lane 1). Every product here fits int8, so its low byte is its two's complement.
+__device__ __forceinline__ uint32_t byte_products(u16x2_t ex, u16x2_t ox, u16x2_t sy) {
+  const u16x2_t pe = ex * sy, po = ox * sy;
+  return (__builtin_bit_cast(uint32_t, pe) & 0x00FF00FFu) | ((__builtin_bit_cast(uint32_t, po) & 0x00FF00FFu) << 8);
+}
 
 template <int T>
 __global__ __launch_bounds__(256) void qgemm_k_kernel(QGemmBatch B, QA A, int64_t n) {
-  static_assert(T == kQ4_K || T == kQ5_K, "Q4_K and Q5_K");
+  static_assert(T == kQ4_K || T == kQ5_K || T == kQ6_K, "K types");
   constexpr int NS = k_slices<T>();
   constexpr int RW = 10;  // words per expanded (slice, residue, row) entry: 8 and 2 of padding
   __shared__ __align__(16) uint32_t ew[NS][8][kKTileRows][RW];
@@ -780,11 +792,36 @@ __global__ __launch_bounds__(256) void qgemm_k_kernel(QGemmBatch B, QA A, int64_
       const int64_t wb = erow * W.nb + sb;
       const uint8_t* sc = W.s + wb * 16;
       const uint32_t* qw = reinterpret_cast<const uint32_t*>(W.q + wb * 128);
+      // Q4_K / Q5_K: qs groups 2 hh, 2 hh + 1 (low nibbles: sub-block 2c, high: 2c + 1); Q6_K: the ql groups of
+      // half hh (low nibbles: sub-blocks 4 hh + lg, high: 4 hh + lg + 2)
       const uint32_t raw[2] = {qw[8 * (2 * hh) + rr], qw[8 * (2 * hh + 1) + rr]};
       uint32_t hraw = 0;
       if constexpr (T == kQ5_K) hraw = reinterpret_cast<const uint32_t*>(W.h + wb * 32)[rr];
+      if constexpr (T == kQ6_K) hraw = reinterpret_cast<const uint32_t*>(W.h + wb * 64 + 32 * hh)[rr];
+      if constexpr (T == kQ6_K) {
+        const int8_t* scl = reinterpret_cast<const int8_t*>(sc);
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
+        for (int gg = 0; gg < 4; ++gg) {
+          const int k = 4 * hh + gg;
+          const uint32_t v = ((raw[gg & 1] >> (4 * (gg >> 1))) & 0x0F0F0F0Fu) | (((hraw >> (2 * gg)) & 0x03030303u) << 4);
+          // 16-bit lanes: even bytes (0, 2) and odd bytes (1, 3) of u0 = v & 7 and u1 = (v >> 3) - 4
+          const u16x2_t u0e = __builtin_bit_cast(u16x2_t, v & 0x00070007u);
+          const u16x2_t u0o = __builtin_bit_cast(u16x2_t, (v >> 8) & 0x00070007u);
+          const u16x2_t four = {4, 4};
+          const u16x2_t u1e = __builtin_bit_cast(u16x2_t, (v >> 3) & 0x00070007u) - four;
+          const u16x2_t u1o = __builtin_bit_cast(u16x2_t, (v >> 11) & 0x00070007u) - four;
+          const int slo = scl[2 * k], shi = scl[2 * k + 1];  // bytes 0, 1 / bytes 2, 3 of the residue word
+          const u16x2_t s0 = {uint16_t(slo & 15), uint16_t(shi & 15)};
+          const u16x2_t s1 = {uint16_t(slo >> 4), uint16_t(shi >> 4)};
+          ew[0][rr][er][k] = byte_products(u1e, u1o, s1);
+          ew[1][rr][er][k] = byte_products(u0e, u0o, s1);
+          ew[2][rr][er][k] = byte_products(u1e, u1o, s0);
+          ew[3][rr][er][k] = byte_products(u0e, u0o, s0);
+        }
+        if (rr == 0 && hh == 0) wdm[er][0] = h2f(W.d[wb]);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4 && T != kQ6_K; ++kk) {
         const int k = 4 * hh + kk;
         int sk, mk;
         scale_min_k4(k, sc, sk, mk);
@@ -800,7 +837,7 @@ __global__ __launch_bounds__(256) void qgemm_k_kernel(QGemmBatch B, QA A, int64_
         }
         if (rr == 0) mins[er][k] = mk;
       }
-      if (rr == 0 && hh == 0) {
+      if (T != kQ6_K && rr == 0 && hh == 0) {
         wdm[er][0] = h2f(W.d[wb]);
         wdm[er][1] = h2f(W.m[wb]);
       }
@@ -812,7 +849,7 @@ __global__ __launch_bounds__(256) void qgemm_k_kernel(QGemmBatch B, QA A, int64_
     const int16_t* bsp = A.bsums + ab * 16;
     int bsk[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) bsk[k] = int(bsp[2 * k]) + int(bsp[2 * k + 1]);
+    for (int k = 0; k < 8; ++k) bsk[k] = T == kQ6_K ? 0 : int(bsp[2 * k]) + int(bsp[2 * k + 1]);
     float dv[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) dv[v] = __fmul_rn(wdm[4 * g + v][0], da);
@@ -830,7 +867,9 @@ __global__ __launch_bounds__(256) void qgemm_k_kernel(QGemmBatch B, QA A, int64_
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         int aux;
-        if constexpr (T == kQ5_K)
+        if constexpr (T == kQ6_K)
+          aux = 128 * c[0][v] + 16 * c[1][v] + 8 * c[2][v] + c[3][v];
+        else if constexpr (T == kQ5_K)
           aux = c[0][v] + 4 * c[1][v] + 16 * c[2][v];
         else
           aux = c[0][v] + 8 * c[1][v];
@@ -838,7 +877,7 @@ __global__ __launch_bounds__(256) void qgemm_k_kernel(QGemmBatch B, QA A, int64_
       }
     }
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < 4 && T != kQ6_K; ++v) {
       const int rv = 4 * g + v;
       int sumi = 0;
 #pragma unroll
@@ -1046,7 +1085,7 @@ int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* row
 
 int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* rows, float* const* y, int64_t in,
                      const void* acts, int64_t n, nbhs_stream stream) {
-  if (!is_quant(type) || type == kQ6_K || n_w <= 0 || n_w > kMaxQWeights || !w || !rows || !y || !acts ||
+  if (!is_quant(type) || n_w <= 0 || n_w > kMaxQWeights || !w || !rows || !y || !acts ||
       in <= 0 || in % block_elems(type) || n <= 0 || (n + 63) / 64 > 65535)
     return NBHS_EINVAL;
   const int64_t tile_rows = is_k(type) ? kKTileRows : 64;
@@ -1072,6 +1111,7 @@ int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* row
   switch (type) {
     case kQ4_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ4_K>, grid, block, s, B, A, n);
     case kQ5_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ5_K>, grid, block, s, B, A, n);
+    case kQ6_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ6_K>, grid, block, s, B, A, n);
     case kQ4_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ4_0>, grid, block, s, B, A, n);
     case kQ5_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_0>, grid, block, s, B, A, n);
     case kQ5_1: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_1>, grid, block, s, B, A, n);

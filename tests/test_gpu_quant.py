@@ -132,12 +132,13 @@ def test_quant_tiled_many_weights_one_type(backend, t):
 
 @pytest.mark.parametrize("n", [17, 80, 130])
 def test_quant_tiled_k_types_mixed(backend, n):
-    """Prefill-sized calls over K-type weights: Q4_K and Q5_K run the int8 matrix-core kernel on residue-major
-    activations, Q6_K the row-chunked kernel on the standard layout, all in one call (the activations quantized
-    once per layout, in the order the types come); row counts that end inside a 16-row tile, three super-blocks
-    per row, activation rows that end inside a 64-row tile. Every output bit-exact."""
+    """Prefill-sized calls over K-type weights, which run the int8 matrix-core kernel on residue-major Q8_K
+    activations, mixed in one call with a Q8_0 weight (the legacy tiled kernel on Q8_0 activations): the
+    activations are quantized once per layout, in the order the types come. Row counts that end inside a 16-row
+    tile, three super-blocks per row, activation rows that end inside a 64-row tile. Every output bit-exact."""
     in_ = 768
-    spec = [(oracle.Q4_K, 70), (oracle.Q6_K, 33), (oracle.Q5_K, 16), (oracle.Q4_K, 1), (oracle.Q5_K, 45)]
+    spec = [(oracle.Q4_K, 70), (oracle.Q6_K, 33), (oracle.Q8_0, 20), (oracle.Q5_K, 16), (oracle.Q4_K, 1),
+            (oracle.Q5_K, 45), (oracle.Q6_K, 130)]
     ws = [U.random_qmat(t, r, in_, seed=300 + i) for i, (t, r) in enumerate(spec)]
     x = (np.random.default_rng(n).standard_normal((n, in_)) * 2).astype(np.float32)
     with Buffers(backend) as B:
