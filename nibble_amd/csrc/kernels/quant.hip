@@ -741,7 +741,8 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
 // d * aux[w], for Q4_K / Q5_K acc -= (fp16(dmin_w) * d_a) * sumi, result acc + sums[0] + ... + sums[7] - the same
 // operations in the same order as qgemv_kernel, so the same bits.
 // A workgroup (4 waves) takes 16 weight rows and 64 activation rows (16 per wave). Per super-block its threads
-// expand the 16 rows into slice * quant bytes in LDS (residue-major, 40-byte rows: conflict-free 8-byte reads);
+// expand the 16 rows into slice * quant bytes in LDS (residue-major, 40-byte rows: conflict-free 8-byte reads),
+// two super-blocks per stage;
 // each wave then runs 8 residues x slices MFMAs of 16 x 16 x 32, its activation operands read straight from the
 // residue-major Q8_K planes (quantize_q8k_kernel<true>). The accumulator layout gives lane l activation row
 // t0 + l % 16 and weight rows 4 (l / 16) + v, v < 4: 4 outputs and their 9 float accumulators per lane.
@@ -764,10 +765,11 @@ template <int T>
 __global__ __launch_bounds__(256) void qgemm_k_kernel(QGemmBatch B, QA A, int64_t n) {
   static_assert(T == kQ4_K || T == kQ5_K || T == kQ6_K, "K types");
   constexpr int NS = k_slices<T>();
-  constexpr int RW = 10;  // words per expanded (slice, residue, row) entry: 8 and 2 of padding
-  __shared__ __align__(16) uint32_t ew[NS][8][kKTileRows][RW];
-  __shared__ int mins[kKTileRows][8];
-  __shared__ float wdm[kKTileRows][2];
+  constexpr int RW = 10;   // words per expanded (slice, residue, row) entry: 8 and 2 of padding
+  constexpr int SBS = 2;   // super-blocks staged per barrier pair: one global round trip for both
+  __shared__ __align__(16) uint32_t ew[SBS][NS][8][kKTileRows][RW];
+  __shared__ int mins[SBS][kKTileRows][8];
+  __shared__ float wdm[SBS][kKTileRows][2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int wi = 0;
   for (int i = 1; i < B.n_w; ++i)
@@ -787,80 +789,103 @@ __global__ __launch_bounds__(256) void qgemm_k_kernel(QGemmBatch B, QA A, int64_
 #pragma unroll
     for (int w = 0; w < 8; ++w) sums[w][v] = 0.f;
   }
-  for (int64_t sb = 0; sb < W.nb; ++sb) {
-    {
-      const int64_t wb = erow * W.nb + sb;
-      const uint8_t* sc = W.s + wb * 16;
-      const uint32_t* qw = reinterpret_cast<const uint32_t*>(W.q + wb * 128);
-      // Q4_K / Q5_K: qs groups 2 hh, 2 hh + 1 (low nibbles: sub-block 2c, high: 2c + 1); Q6_K: the ql groups of
-      // half hh (low nibbles: sub-blocks 4 hh + lg, high: 4 hh + lg + 2)
-      const uint32_t raw[2] = {qw[8 * (2 * hh) + rr], qw[8 * (2 * hh + 1) + rr]};
-      uint32_t hraw = 0;
-      if constexpr (T == kQ5_K) hraw = reinterpret_cast<const uint32_t*>(W.h + wb * 32)[rr];
-      if constexpr (T == kQ6_K) hraw = reinterpret_cast<const uint32_t*>(W.h + wb * 64 + 32 * hh)[rr];
-      if constexpr (T == kQ6_K) {
-        const int8_t* scl = reinterpret_cast<const int8_t*>(sc);
+  // Raw words of this thread's expansion share: Q4_K / Q5_K qs groups 2 hh, 2 hh + 1 (low nibbles: sub-block 2c,
+  // high: 2c + 1); Q6_K the ql groups of half hh (low nibbles: sub-blocks 4 hh + lg, high: 4 hh + lg + 2); the high
+  // bits; the 16 scale bytes; d and dmin.
+  struct Raw {
+    uint32_t q[2], h;
+    uint4 sc;
+    uint16_t d, m;
+  };
+  auto load_raw = [&](int64_t sb, Raw& r) {
+    const int64_t wb = erow * W.nb + sb;
+    const uint32_t* qw = reinterpret_cast<const uint32_t*>(W.q + wb * 128);
+    r.q[0] = qw[8 * (2 * hh) + rr];
+    r.q[1] = qw[8 * (2 * hh + 1) + rr];
+    r.h = 0;
+    if constexpr (T == kQ5_K) r.h = reinterpret_cast<const uint32_t*>(W.h + wb * 32)[rr];
+    if constexpr (T == kQ6_K) r.h = reinterpret_cast<const uint32_t*>(W.h + wb * 64 + 32 * hh)[rr];
+    r.sc = *reinterpret_cast<const uint4*>(W.s + wb * 16);
+    r.d = W.d[wb];
+    r.m = T == kQ6_K ? uint16_t(0) : W.m[wb];
+  };
+  auto expand = [&](const Raw& raw, int j) {
+    // scale bytes by compile-time index (a register array indexed by hh would go to scratch)
+    const uint32_t scw[4] = {raw.sc.x, raw.sc.y, raw.sc.z, raw.sc.w};
+    auto sbyte = [&](int i) { return int((scw[i >> 2] >> (8 * (i & 3))) & 0xFFu); };
+    if constexpr (T == kQ6_K) {
 #pragma unroll
-        for (int gg = 0; gg < 4; ++gg) {
-          const int k = 4 * hh + gg;
-          const uint32_t v = ((raw[gg & 1] >> (4 * (gg >> 1))) & 0x0F0F0F0Fu) | (((hraw >> (2 * gg)) & 0x03030303u) << 4);
-          // 16-bit lanes: even bytes (0, 2) and odd bytes (1, 3) of u0 = v & 7 and u1 = (v >> 3) - 4
-          const u16x2_t u0e = __builtin_bit_cast(u16x2_t, v & 0x00070007u);
-          const u16x2_t u0o = __builtin_bit_cast(u16x2_t, (v >> 8) & 0x00070007u);
-          const u16x2_t four = {4, 4};
-          const u16x2_t u1e = __builtin_bit_cast(u16x2_t, (v >> 3) & 0x00070007u) - four;
-          const u16x2_t u1o = __builtin_bit_cast(u16x2_t, (v >> 11) & 0x00070007u) - four;
-          const int slo = scl[2 * k], shi = scl[2 * k + 1];  // bytes 0, 1 / bytes 2, 3 of the residue word
-          const u16x2_t s0 = {uint16_t(slo & 15), uint16_t(shi & 15)};
-          const u16x2_t s1 = {uint16_t(slo >> 4), uint16_t(shi >> 4)};
-          ew[0][rr][er][k] = byte_products(u1e, u1o, s1);
-          ew[1][rr][er][k] = byte_products(u0e, u0o, s1);
-          ew[2][rr][er][k] = byte_products(u1e, u1o, s0);
-          ew[3][rr][er][k] = byte_products(u0e, u0o, s0);
-        }
-        if (rr == 0 && hh == 0) wdm[er][0] = h2f(W.d[wb]);
+      for (int gg = 0; gg < 4; ++gg) {
+        const int k = 4 * hh + gg;
+        const uint32_t v =
+            ((raw.q[gg & 1] >> (4 * (gg >> 1))) & 0x0F0F0F0Fu) | (((raw.h >> (2 * gg)) & 0x03030303u) << 4);
+        // 16-bit lanes: even bytes (0, 2) and odd bytes (1, 3) of u0 = v & 7 and u1 = (v >> 3) - 4
+        const u16x2_t u0e = __builtin_bit_cast(u16x2_t, v & 0x00070007u);
+        const u16x2_t u0o = __builtin_bit_cast(u16x2_t, (v >> 8) & 0x00070007u);
+        const u16x2_t four = {4, 4};
+        const u16x2_t u1e = __builtin_bit_cast(u16x2_t, (v >> 3) & 0x00070007u) - four;
+        const u16x2_t u1o = __builtin_bit_cast(u16x2_t, (v >> 11) & 0x00070007u) - four;
+        // the signed scales of bytes 0, 1 and of bytes 2, 3 of the residue word: scale bytes 2k, 2k + 1
+        const int slo = int(int8_t(hh ? sbyte(8 + 2 * gg) : sbyte(2 * gg)));
+        const int shi = int(int8_t(hh ? sbyte(9 + 2 * gg) : sbyte(2 * gg + 1)));
+        const u16x2_t s0 = {uint16_t(slo & 15), uint16_t(shi & 15)};
+        const u16x2_t s1 = {uint16_t(slo >> 4), uint16_t(shi >> 4)};
+        ew[j][0][rr][er][k] = byte_products(u1e, u1o, s1);
+        ew[j][1][rr][er][k] = byte_products(u0e, u0o, s1);
+        ew[j][2][rr][er][k] = byte_products(u1e, u1o, s0);
+        ew[j][3][rr][er][k] = byte_products(u0e, u0o, s0);
       }
+    } else {
 #pragma unroll
-      for (int kk = 0; kk < 4 && T != kQ6_K; ++kk) {
+      for (int kk = 0; kk < 4; ++kk) {
         const int k = 4 * hh + kk;
-        int sk, mk;
-        scale_min_k4(k, sc, sk, mk);
-        uint32_t q = (raw[kk >> 1] >> (4 * (kk & 1))) & 0x0F0F0F0Fu;
+        // scale_min_k4 (quant.cpp:55-64) on the register copy of the packed scales, k = 4 hh + kk
+        const int sk = hh ? (sbyte(8 + kk) & 0xF) | ((sbyte(kk) >> 6) << 4) : sbyte(kk) & 63;
+        const int mk = hh ? (sbyte(8 + kk) >> 4) | ((sbyte(4 + kk) >> 6) << 4) : sbyte(kk + 4) & 63;
+        uint32_t q = (raw.q[kk >> 1] >> (4 * (kk & 1))) & 0x0F0F0F0Fu;
         if constexpr (T == kQ5_K) {
-          q |= ((hraw >> k) & 0x01010101u) << 4;
-          ew[0][rr][er][k] = q * uint32_t(sk & 3);
-          ew[1][rr][er][k] = q * uint32_t((sk >> 2) & 3);
-          ew[2][rr][er][k] = q * uint32_t(sk >> 4);
+          q |= ((raw.h >> k) & 0x01010101u) << 4;
+          ew[j][0][rr][er][k] = q * uint32_t(sk & 3);
+          ew[j][1][rr][er][k] = q * uint32_t((sk >> 2) & 3);
+          ew[j][2][rr][er][k] = q * uint32_t(sk >> 4);
         } else {
-          ew[0][rr][er][k] = q * uint32_t(sk & 7);
-          ew[1][rr][er][k] = q * uint32_t(sk >> 3);
+          ew[j][0][rr][er][k] = q * uint32_t(sk & 7);
+          ew[j][1][rr][er][k] = q * uint32_t(sk >> 3);
         }
-        if (rr == 0) mins[er][k] = mk;
-      }
-      if (T != kQ6_K && rr == 0 && hh == 0) {
-        wdm[er][0] = h2f(W.d[wb]);
-        wdm[er][1] = h2f(W.m[wb]);
+        if (rr == 0) mins[j][er][k] = mk;
       }
     }
-    __syncthreads();
+    if (rr == 0 && hh == 0) {
+      wdm[j][er][0] = h2f(raw.d);
+      wdm[j][er][1] = h2f(raw.m);
+    }
+  };
+  // one super-block of this lane's outputs from stage j
+  auto compute = [&](int64_t sb, int j) {
     const int64_t ab = tc * A.nb + sb;
     const uint8_t* aq = reinterpret_cast<const uint8_t*>(A.qs) + ab * 256;
+    uint2 bw[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) bw[w] = *reinterpret_cast<const uint2*>(aq + 32 * w + 8 * g);
     const float da = A.d[ab];
-    const int16_t* bsp = A.bsums + ab * 16;
     int bsk[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) bsk[k] = T == kQ6_K ? 0 : int(bsp[2 * k]) + int(bsp[2 * k + 1]);
+    for (int k = 0; k < 8; ++k) bsk[k] = 0;
+    if constexpr (T != kQ6_K) {
+      const int16_t* bsp = A.bsums + ab * 16;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) bsk[k] = int(bsp[2 * k]) + int(bsp[2 * k + 1]);
+    }
     float dv[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) dv[v] = __fmul_rn(wdm[4 * g + v][0], da);
+    for (int v = 0; v < 4; ++v) dv[v] = __fmul_rn(wdm[j][4 * g + v][0], da);
 #pragma unroll
     for (int w = 0; w < 8; ++w) {
-      const uint2 bw = *reinterpret_cast<const uint2*>(aq + 32 * w + 8 * g);
-      const long bop = (long(bw.y) << 32) | long(bw.x);
+      const long bop = (long(bw[w].y) << 32) | long(bw[w].x);
       i32x4_t c[NS];
 #pragma unroll
       for (int sl = 0; sl < NS; ++sl) {
-        const uint2 aw = *reinterpret_cast<const uint2*>(&ew[sl][w][tl][2 * g]);
+        const uint2 aw = *reinterpret_cast<const uint2*>(&ew[j][sl][w][tl][2 * g]);
         const long aop = (long(aw.y) << 32) | long(aw.x);
         c[sl] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, i32x4_t{0, 0, 0, 0}, 0, 0, 0);
       }
@@ -876,14 +901,27 @@ __global__ __launch_bounds__(256) void qgemm_k_kernel(QGemmBatch B, QA A, int64_
         sums[w][v] = __fadd_rn(sums[w][v], __fmul_rn(dv[v], float(aux)));
       }
     }
+    if constexpr (T != kQ6_K) {
 #pragma unroll
-    for (int v = 0; v < 4 && T != kQ6_K; ++v) {
-      const int rv = 4 * g + v;
-      int sumi = 0;
+      for (int v = 0; v < 4; ++v) {
+        const int rv = 4 * g + v;
+        int sumi = 0;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) sumi += bsk[k] * mins[rv][k];
-      acc[v] = __fsub_rn(acc[v], __fmul_rn(__fmul_rn(wdm[rv][1], da), float(sumi)));
+        for (int k = 0; k < 8; ++k) sumi += bsk[k] * mins[j][rv][k];
+        acc[v] = __fsub_rn(acc[v], __fmul_rn(__fmul_rn(wdm[j][rv][1], da), float(sumi)));
+      }
     }
+  };
+  for (int64_t sb = 0; sb < W.nb; sb += SBS) {
+    const bool two = sb + 1 < W.nb;
+    Raw r0, r1;
+    load_raw(sb, r0);
+    if (two) load_raw(sb + 1, r1);
+    expand(r0, 0);
+    if (two) expand(r1, 1);
+    __syncthreads();
+    compute(sb, 0);  // block order: sb, then sb + 1
+    if (two) compute(sb + 1, 1);
     __syncthreads();
   }
 #pragma unroll
