@@ -78,21 +78,24 @@ def test_quant_embed_bit_exact(backend, t):
     backend.release_weights()
 
 
-def test_quant_non_finite_activations(backend):
+@pytest.mark.parametrize("n", [2, 20])
+def test_quant_non_finite_activations(backend, n):
     """A NaN in an activation block makes its scale NaN (quant.cpp:37-49, 273-303): every output that reads the
-    block is NaN, as in the reference; rows without it stay finite and exact."""
-    for t in (oracle.Q8_0, oracle.Q4_K):
+    block is NaN, as in the reference; rows without it stay finite and exact. n = 2 runs the row-chunked kernel,
+    n = 20 the tiled ones."""
+    for t in (oracle.Q8_0, oracle.Q4_K, oracle.Q6_K):
         in_ = 512
         w = U.random_qmat(t, 8, in_, seed=5)
-        x = np.random.default_rng(0).standard_normal((2, in_)).astype(np.float32)
+        x = np.random.default_rng(0).standard_normal((n, in_)).astype(np.float32)
         x[1, 300] = np.nan
         with Buffers(backend) as B:
-            dx, dy = B.upload(x), B.alloc(2 * 8)
-            backend.matmul(w, dx, dy, 2)
-            got = backend.download(dy, (2, 8))
+            dx, dy = B.upload(x), B.alloc(n * 8)
+            backend.matmul(w, dx, dy, n)
+            got = backend.download(dy, (n, 8))
         ref = oracle.matmul_q(t, w.raw, in_, 8, x)
         assert np.all(np.isnan(got[1])) and np.all(np.isnan(ref[1]))
-        assert np.array_equal(bits(got[0]), bits(ref[0]))
+        keep = [i for i in range(n) if i != 1]
+        assert np.array_equal(bits(got[keep]), bits(ref[keep])), U.NAMES[t]
     backend.release_weights()
 
 
