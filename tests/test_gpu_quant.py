@@ -18,9 +18,10 @@ TYPES = list(U.NAMES)
 
 
 @pytest.mark.parametrize("t", TYPES, ids=[U.NAMES[t] for t in TYPES])
-@pytest.mark.parametrize("n", [1, 3, 16, 17, 40])
+@pytest.mark.parametrize("n", [1, 3, 16, 17, 40, 96])
 def test_quant_matmul_bit_exact(backend, t, n):
-    """Activation quantization and the block dots, every activation-row chunking (n <= 16 and beyond)."""
+    """Activation quantization and the block dots, every activation-row chunking: n <= 16 (one row-chunked
+    launch), 17 and 40 (row-chunked launches for the legacy types, tiled for the K types), 96 (tiled)."""
     be_ = oracle.block_elems(t)
     in_ = 2 * 256 if be_ == 256 else 7 * 32 + 32 * 64  # two super-blocks / 71 legacy blocks (a partial chunk)
     rows = 37  # not a multiple of the 4 rows per wave
@@ -78,11 +79,11 @@ def test_quant_embed_bit_exact(backend, t):
     backend.release_weights()
 
 
-@pytest.mark.parametrize("n", [2, 20])
+@pytest.mark.parametrize("n", [2, 100])
 def test_quant_non_finite_activations(backend, n):
     """A NaN in an activation block makes its scale NaN (quant.cpp:37-49, 273-303): every output that reads the
     block is NaN, as in the reference; rows without it stay finite and exact. n = 2 runs the row-chunked kernel,
-    n = 20 the tiled ones."""
+    n = 100 the tiled ones."""
     for t in (oracle.Q8_0, oracle.Q4_K, oracle.Q6_K):
         in_ = 512
         w = U.random_qmat(t, 8, in_, seed=5)
@@ -119,7 +120,7 @@ def test_quant_tiled_many_weights_one_type(backend, t):
     """Prefill-sized calls (n > 16) over nine weights of one legacy type: a tiled launch takes up to eight weights,
     its grid runs over the row tiles of all of them (row counts that end inside a tile), and the ninth weight goes
     to a second launch. Every output bit-exact."""
-    in_, n = 256, 80
+    in_, n = 256, 100
     rows = [70, 33, 130, 64, 1, 65, 7, 128, 40]
     ws = [U.random_qmat(t, r, in_, seed=50 + i) for i, r in enumerate(rows)]
     x = np.random.default_rng(9).standard_normal((n, in_)).astype(np.float32)
@@ -156,11 +157,11 @@ def test_quant_tiled_k_types_mixed(backend, n):
     backend.release_weights()
 
 
-@pytest.mark.parametrize("n", [1, 5, 20])
+@pytest.mark.parametrize("n", [1, 5, 100])
 def test_quant_q8_1_sum_term_tie(backend, n):
     """Q5_1 against activations holding a block whose Q8_1 sum term float(sum) * d is an exact fp16 tie (the
     reference rounds the product to float, then to fp16: down to the even neighbour here). Every activation path:
-    quantized inside the launch (n = 1), by the quantizer launch (n = 5) and under the tiled kernel (n = 20)."""
+    quantized inside the launch (n = 1), by the quantizer launch (n = 5) and under the tiled kernel (n = 100)."""
     from tests.test_quant_oracle import tie_block
     in_, rows = 256, 24
     x = np.random.default_rng(3).standard_normal((n, in_)).astype(np.float32)
