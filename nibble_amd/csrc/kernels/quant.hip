@@ -392,9 +392,12 @@ __device__ __forceinline__ void load32(const uint8_t* p, uint32_t (&w)[8]) {
 // The integer lanes of super-block sb of row rr against an activation super-block whose sub-block k words are
 // act(k, w) (residue order) and 16-sums bsum(g): aux[w] = sum over the block's elements e with e % 8 == w of
 // scale(e) * (a_e * q_e) (quant.cpp:118-144, 394-416), and for Q4_K / Q5_K sumi = sum_k (bsums) * m_k.
-template <int T, class ActW, class BSum>
+// SPL > 1: this lane takes part `part` of SPL equal shares of the sub-blocks (the same code for every part, only
+// the data offsets differ, so lanes of different parts do not diverge); the integer results of the parts add up
+// to the whole block's (exactly: integer sums).
+template <int T, int SPL = 1, class ActW, class BSum>
 __device__ __forceinline__ void k_lanes(const QW& W, int64_t rr, int64_t sb, ActW act, BSum bsum, int (&aux)[8],
-                                        int& sumi) {
+                                        int& sumi, int part = 0) {
   const int64_t wb = rr * W.nb + sb;
 #pragma unroll
   for (int w = 0; w < 8; ++w) aux[w] = 0;
@@ -404,7 +407,8 @@ __device__ __forceinline__ void k_lanes(const QW& W, int64_t rr, int64_t sb, Act
     uint32_t hw[8];
     if constexpr (T == kQ5_K) load32(W.h + wb * 32, hw);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int cc = 0; cc < 4 / SPL; ++cc) {
+      const int c = cc + (4 / SPL) * part;
       uint32_t qw[8];
       load32(W.q + wb * 128 + 32 * c, qw);
 #pragma unroll
@@ -424,7 +428,8 @@ __device__ __forceinline__ void k_lanes(const QW& W, int64_t rr, int64_t sb, Act
   } else {  // Q6_K: sub-block k = 4h + g of the 128-element half h; values 0..63 less 32 (quant.cpp:84-96)
     const int8_t* scl = reinterpret_cast<const int8_t*>(sc);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int hh = 0; hh < 2 / SPL; ++hh) {
+      const int h = hh + (2 / SPL) * part;
       uint32_t hw[8];
       load32(W.h + wb * 64 + 32 * h, hw);
 #pragma unroll
@@ -464,7 +469,13 @@ struct QBatch {  // weights of one type sharing one input; wave0: first wave of 
 // (in = 2048: 8), so K waves take twice the rows; with 16 activation rows a wave's outputs are capped at 64. A
 // single-row launch over many rows (an FFN's 16384) takes 16 rows per wave: the activation row each wave quantizes
 // is then shared by more weight rows, and there are still a thousand or more waves.
-constexpr int rows_per_wave(bool k, int NT, bool wide) { return NT > 4 ? 4 : k ? 8 : wide && NT == 1 ? 16 : 4; }
+constexpr int rows_per_wave(bool k, int NT, bool wide) {
+  return NT > 4 ? 4 : k ? (NT == 1 && !wide ? 4 : 8) : wide && NT == 1 ? 16 : 4;
+}
+// K types with one activation row in a launch of QKV size: each (row, super-block) pair is split over two adjacent
+// lanes (half the sub-blocks each), which halves the serial integer chain per lane and doubles the waves. Wide
+// launches (an FFN's 16384 rows) have waves enough and lose more to the activation quantization each wave repeats.
+constexpr int k_split(bool k, int NT, bool wide) { return k && NT == 1 && !wide ? 2 : 1; }
 constexpr int64_t kWideRows = 16384;  // total rows of a launch from which single-row launches go wide
 
 // A K activation super-block staged in LDS on the fused path: 256 quants in residue order, d, the 16-sums.
@@ -538,8 +549,11 @@ __global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* 
         }
       }
     } else {
-      for (int p = lane; p < RW * nc; p += 64) {
-        const int r = p / nc, bl = p % nc;
+      constexpr int SPL = k_split(K, NT, WIDE);
+      // RW * nc * SPL <= 64 (nc <= 8), so the two lanes of a split pair are always in the same pass
+      for (int p = lane; p < RW * nc * SPL; p += 64) {
+        const int pair = p / SPL, part = p % SPL;
+        const int r = pair / nc, bl = pair % nc;
         const int64_t rr = r0 + (r < nr ? r : nr - 1), b = c0 + bl;
         for (int t = 0; t < NT; ++t) {
           if (t >= n) break;
@@ -547,16 +561,22 @@ __global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* 
           float da;
           if constexpr (FUSED) {
             const LdsActK& s = acts[t][bl];
-            k_lanes<T>(W, rr, b, [&](int k, int w) { return s.a[8 * k + w]; }, [&](int g) { return s.bs[g]; }, aux,
-                       sumi);
+            k_lanes<T, SPL>(W, rr, b, [&](int k, int w) { return s.a[8 * k + w]; }, [&](int g) { return s.bs[g]; },
+                            aux, sumi, part);
             da = s.d;
           } else {
             const int64_t ab = int64_t(t) * A.nb + b;
             const uint32_t* aq = reinterpret_cast<const uint32_t*>(A.qs + ab * 256);
             const int16_t* bs = A.bsums + ab * 16;
-            k_lanes<T>(W, rr, b, [&](int k, int w) { return aq[8 * k + w]; }, [&](int g) { return int(bs[g]); },
-                       aux, sumi);
+            k_lanes<T, SPL>(W, rr, b, [&](int k, int w) { return aq[8 * k + w]; }, [&](int g) { return int(bs[g]); },
+                            aux, sumi, part);
             da = A.d[ab];
+          }
+          if constexpr (SPL == 2) {  // the partner lane (p ^ 1) holds the other half
+#pragma unroll
+            for (int l = 0; l < 8; ++l) aux[l] += __shfl_xor(aux[l], 1, 64);
+            sumi += __shfl_xor(sumi, 1, 64);
+            if (part != 0) continue;
           }
           const int64_t wb = rr * W.nb + b;
           const float d = __fmul_rn(h2f(W.d[wb]), da);
