@@ -105,6 +105,20 @@ int nbh_backend_append_rope_attention(nbh_backend* be, const float* q, float* k_
                                       int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float freq_base, int neox,
                                       const float* freq_factors);
 
+/* fp16 KV caches - an extension: the reference's cache is fp32 and its design defers an F16 KV cache
+ * (docs/superpowers/specs/2026-10-17-nibble-design.md:181). k16, v16: layer bases of _Float16 [rows, n_kv_heads,
+ * head_dim] caches in buffers from nbh_backend_alloc (a buffer of f floats holds 2f halves); head_dim 64 or 128.
+ * nbh_backend_attention_f16kv is nbh_backend_attention over the cached values widened exactly (q already
+ * rotated); nbh_backend_append_rope_attention_f16kv first writes rows pos0.. as fp16(rope(k_new)) and fp16(v_new)
+ * (the fp32 rotation, then rounding to nearest even) and reads q unrotated, as nbh_backend_append_rope_attention.
+ * Every row runs on the split-context decode kernel. */
+int nbh_backend_attention_f16kv(nbh_backend* be, const float* q, const void* k16, const void* v16, float* out,
+                                int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim);
+int nbh_backend_append_rope_attention_f16kv(nbh_backend* be, const float* q, void* k16, void* v16,
+                                            const float* k_new, const float* v_new, float* out, int64_t n,
+                                            int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                            float freq_base, int neox, const float* freq_factors);
+
 /* Ragged batch of single-token decodes. No counterpart in the reference, whose Backend serves one sequence: each
  * sequence i is Backend::attention (backend.h:68-69) with n = 1 - query row q[i] [n_heads, head_dim] at position
  * pos0[i] over its own layer caches k_cache[i], v_cache[i] - and equals that call within rounding. q, k_cache,

@@ -94,6 +94,26 @@ int nbhs_append_attn_decode_f32(const float* q, float* k_cache, float* v_cache, 
                                 int64_t head_dim, float* workspace, int64_t workspace_floats, int cu_count,
                                 const float* rope_cs, int64_t rope_rows, int neox, nbhs_stream s);
 
+/* fp16 KV caches (an extension: the reference's cache is fp32, and its design defers an F16 KV cache,
+ * docs/superpowers/specs/2026-10-17-nibble-design.md:181). k16, v16 hold _Float16 [rows, n_kv_heads, head_dim]; the
+ * attention is the fp32 attention over the cached values widened exactly, head_dim 64 or 128 only, with the same
+ * workspace as nbhs_attn_decode_f32. */
+int nbhs_attn_decode_f16kv(const float* q, const void* k16, const void* v16, float* out, int64_t n, int64_t pos0,
+                           int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float* workspace,
+                           int64_t workspace_floats, int cu_count, const float* q_rope_cs, int64_t q_rope_rows,
+                           int q_rope_neox, nbhs_stream s);
+/* nbhs_append_attn_decode_f32 over fp16 caches: cache row pos0 receives fp16(rope(k_new)) and fp16(v_new) (rotated
+ * in fp32 as the fp32 append does, then rounded to nearest even), and the attention uses the row as stored. */
+int nbhs_append_attn_decode_f16kv(const float* q, void* k16, void* v16, const float* k_new, const float* v_new,
+                                  float* out, int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                  float* workspace, int64_t workspace_floats, int cu_count, const float* rope_cs,
+                                  int64_t rope_rows, int neox, nbhs_stream s);
+/* n fp32 rows k_new, v_new [n, n_kv_heads, head_dim] into fp16 cache rows pos0..pos0+n-1: K rotated by the table
+ * (as nbhs_append_rope_f32), both rounded to fp16. */
+int nbhs_append_rope_f16kv(void* k16, void* v16, const float* k_new, const float* v_new, int64_t n, int64_t pos0,
+                           int64_t n_kv_heads, int64_t head_dim, const float* cs_table, int64_t table_rows, int neox,
+                           nbhs_stream s);
+
 /* Ragged batch of single-row decodes (one launch pair for all sequences; an extension the reference's single-session
  * Backend has no counterpart for - each sequence i is exactly Backend::attention with n = 1, backend.h:68-69):
  * query row q[i] [n_heads, head_dim] at position pos0[i] attends to rows 0..pos0[i] of its own caches k[i], v[i]

@@ -46,6 +46,9 @@ _SIGNATURES = {
                                         _I, c_float, c_int, c_void_p]),
     "nbh_backend_append_rope_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                                   c_void_p, _I, _I, _I, _I, _I, c_float, c_int, c_void_p]),
+    "nbh_backend_attention_f16kv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, _I, _I, _I, _I, _I]),
+    "nbh_backend_append_rope_attention_f16kv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                                        c_void_p, _I, _I, _I, _I, _I, c_float, c_int, c_void_p]),
     "nbh_backend_attention_batch": (c_int, [c_void_p, _I, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, _I, _I,
                                             _I]),
     "nbh_backend_append_rope_attention_batch": (c_int, [c_void_p, _I, c_void_p, c_void_p, c_void_p, c_void_p,
@@ -220,6 +223,21 @@ class HipBackend:
         ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
         _check(lib().nbh_backend_append_rope_attention(
             self._h, c_void_p(int(q)), c_void_p(int(k_cache)), c_void_p(int(v_cache)), c_void_p(int(k_new)),
+            c_void_p(int(v_new)), c_void_p(int(out)), n, pos0, n_heads, n_kv_heads, head_dim, freq_base,
+            int(bool(neox)), None if ff is None else _host_ptr(ff)))
+
+    def attention_f16kv(self, q, k16, v16, out, n, pos0, n_heads, n_kv_heads, head_dim):
+        """attention over fp16 caches k16, v16 (_Float16 [rows, n_kv_heads, head_dim] in buffers from alloc; a
+        buffer of f floats holds 2f halves), q already rotated. head_dim 64 or 128."""
+        _check(lib().nbh_backend_attention_f16kv(self._h, c_void_p(int(q)), c_void_p(int(k16)), c_void_p(int(v16)),
+                                                 c_void_p(int(out)), n, pos0, n_heads, n_kv_heads, head_dim))
+
+    def append_rope_attention_f16kv(self, q, k16, v16, k_new, v_new, out, n, pos0, n_heads, n_kv_heads, head_dim,
+                                    freq_base, neox, freq_factors=None):
+        """append_rope_attention over fp16 caches: rows pos0.. receive fp16(rope(k_new)) and fp16(v_new)."""
+        ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
+        _check(lib().nbh_backend_append_rope_attention_f16kv(
+            self._h, c_void_p(int(q)), c_void_p(int(k16)), c_void_p(int(v16)), c_void_p(int(k_new)),
             c_void_p(int(v_new)), c_void_p(int(out)), n, pos0, n_heads, n_kv_heads, head_dim, freq_base,
             int(bool(neox)), None if ff is None else _host_ptr(ff)))
 

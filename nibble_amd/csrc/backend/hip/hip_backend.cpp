@@ -674,6 +674,67 @@ void HipBackend::append_rope_attention(const float* q, float* k_cache, float* v_
   run_attention(q, k_cache, v_cache, out, n, pos0, n_heads, n_kv_heads, head_dim, table, rows, p.neox, &app, &p);
 }
 
+void HipBackend::run_decode_f16kv(const float* q, const void* k16, const void* v16, float* out, int64_t n,
+                                  int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                  const float* rope_table, int64_t rope_rows, bool neox, const char* op) {
+  // rows in groups the decode kernel's workspace bound covers, q rotated on load when a table is given
+  for (int64_t t0 = 0; t0 < n; t0 += kDecodeMaxRows) {
+    const int64_t rows = std::min<int64_t>(kDecodeMaxRows, n - t0);
+    const int64_t ws = nbhs_attn_decode_workspace(rows, pos0 + t0, n_heads, n_kv_heads, head_dim, cu_count_);
+    if (ws < 0) throw Error(std::string(op) + ": invalid decode shape");
+    ensure(decode_ws_, decode_ws_bytes_, size_t(ws) * sizeof(float));
+    check(nbhs_attn_decode_f16kv(q + t0 * n_heads * head_dim, k16, v16, out + t0 * n_heads * head_dim, rows,
+                                 pos0 + t0, n_heads, n_kv_heads, head_dim, decode_ws_,
+                                 int64_t(decode_ws_bytes_ / sizeof(float)), cu_count_, rope_table, rope_rows,
+                                 neox ? 1 : 0, stream_),
+          op);
+  }
+}
+
+void HipBackend::attention_f16kv(const float* q, const void* k16, const void* v16, float* out, int64_t n,
+                                 int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim) {
+  if (head_dim != 64 && head_dim != 128)
+    throw Error("attention_f16kv: head_dim must be 64 or 128, got " + str(head_dim));
+  // the fp16 caches span half the floats of fp32 ones: checked as float counts rounded up
+  check_attention_args(q, static_cast<const float*>(k16), static_cast<const float*>(v16), out, n, pos0, n_heads,
+                       n_kv_heads, head_dim / 2, "attention_f16kv");
+  check_range(q, n * n_heads * head_dim, "attention_f16kv", "q");
+  check_range(out, n * n_heads * head_dim, "attention_f16kv", "out");
+  run_decode_f16kv(q, k16, v16, out, n, pos0, n_heads, n_kv_heads, head_dim, nullptr, 0, false, "attention_f16kv");
+}
+
+void HipBackend::append_rope_attention_f16kv(const float* q, void* k16, void* v16, const float* k_new,
+                                             const float* v_new, float* out, int64_t n, int64_t pos0,
+                                             int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                             const RopeParams& p) {
+  const char* op = "append_rope_attention_f16kv";
+  if (head_dim != 64 && head_dim != 128) throw Error(std::string(op) + ": head_dim must be 64 or 128, got " + str(head_dim));
+  check_attention_args(q, static_cast<const float*>(k16), static_cast<const float*>(v16), out, n, pos0, n_heads,
+                       n_kv_heads, head_dim / 2, op);
+  check_range(q, n * n_heads * head_dim, op, "q");
+  check_range(out, n * n_heads * head_dim, op, "out");
+  int64_t kvf;
+  if (overflow_mul(n * n_kv_heads, head_dim, &kvf)) throw Error(std::string(op) + ": size overflows");
+  check_range(k_new, kvf, op, "k_new");
+  check_range(v_new, kvf, op, "v_new");
+  int64_t rows;
+  const float* table = rope_table(head_dim, pos0 + n, p, &rows);
+  if (n == 1) {  // decode step: the append rides in the attention launch
+    const int64_t ws = nbhs_attn_decode_workspace(1, pos0, n_heads, n_kv_heads, head_dim, cu_count_);
+    if (ws < 0) throw Error(std::string(op) + ": invalid decode shape");
+    ensure(decode_ws_, decode_ws_bytes_, size_t(ws) * sizeof(float));
+    check(nbhs_append_attn_decode_f16kv(q, k16, v16, k_new, v_new, out, pos0, n_heads, n_kv_heads, head_dim,
+                                        decode_ws_, int64_t(decode_ws_bytes_ / sizeof(float)), cu_count_, table, rows,
+                                        p.neox ? 1 : 0, stream_),
+          op);
+    return;
+  }
+  check(nbhs_append_rope_f16kv(k16, v16, k_new, v_new, n, pos0, n_kv_heads, head_dim, table, rows, p.neox ? 1 : 0,
+                               stream_),
+        op);
+  run_decode_f16kv(q, k16, v16, out, n, pos0, n_heads, n_kv_heads, head_dim, table, rows, p.neox, op);
+}
+
 void HipBackend::attention_batch(int64_t n_seq, const float* const* q, const float* const* k_cache,
                                  const float* const* v_cache, float* const* out, const int64_t* pos0, int64_t n_heads,
                                  int64_t n_kv_heads, int64_t head_dim) {

@@ -79,6 +79,15 @@ class HipBackend final : public Backend {
   void append_rope_attention(const float* q, float* k_cache, float* v_cache, const float* k_new, const float* v_new,
                              float* out, int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads,
                              int64_t head_dim, const RopeParams& p);
+  // fp16 KV caches (an extension; the reference's cache is fp32): k16 / v16 hold _Float16 [rows, n_kv_heads,
+  // head_dim], head_dim 64 or 128. attention_f16kv is attention over the cached values widened exactly (q rotated
+  // already); append_rope_attention_f16kv writes fp16(rope(k_new)) and fp16(v_new) into rows pos0.. first and
+  // reads q unrotated. Every row runs on the split-context decode kernel (one launch with the append when n = 1).
+  void attention_f16kv(const float* q, const void* k16, const void* v16, float* out, int64_t n, int64_t pos0,
+                       int64_t n_heads, int64_t n_kv_heads, int64_t head_dim);
+  void append_rope_attention_f16kv(const float* q, void* k16, void* v16, const float* k_new, const float* v_new,
+                                   float* out, int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads,
+                                   int64_t head_dim, const RopeParams& p);
   // Ragged batch of single-token decodes - an extension with no counterpart in the reference, whose Backend serves
   // one sequence: host arrays of n_seq device pointers and positions, sequence i being attention(q[i], k_cache[i],
   // v_cache[i], out[i], 1, pos0[i], ...) over its own caches (equal within rounding: the context split differs).
@@ -132,6 +141,9 @@ class HipBackend final : public Backend {
     const float* k_new;
     const float* v_new;
   };
+  void run_decode_f16kv(const float* q, const void* k16, const void* v16, float* out, int64_t n, int64_t pos0,
+                        int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const float* rope_table,
+                        int64_t rope_rows, bool neox, const char* op);
   void check_attention_args(const float* q, const float* k, const float* v, const float* out, int64_t n,
                             int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const char* op) const;
   void run_attention(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,

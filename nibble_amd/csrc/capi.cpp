@@ -188,6 +188,21 @@ int nbh_backend_append_rope_attention(nbh_backend* be, const float* q, float* k_
   });
 }
 
+int nbh_backend_attention_f16kv(nbh_backend* be, const float* q, const void* k16, const void* v16, float* out,
+                                int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim) {
+  return guarded([&] { B(be).attention_f16kv(q, k16, v16, out, n, pos0, n_heads, n_kv_heads, head_dim); });
+}
+
+int nbh_backend_append_rope_attention_f16kv(nbh_backend* be, const float* q, void* k16, void* v16,
+                                            const float* k_new, const float* v_new, float* out, int64_t n,
+                                            int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                            float freq_base, int neox, const float* freq_factors) {
+  return guarded([&] {
+    B(be).append_rope_attention_f16kv(q, k16, v16, k_new, v_new, out, n, pos0, n_heads, n_kv_heads, head_dim,
+                                      RopeParams{freq_base, neox != 0, freq_factors});
+  });
+}
+
 int nbh_backend_attention_batch(nbh_backend* be, int64_t n_seq, const float* const* q, const float* const* k_cache,
                                 const float* const* v_cache, float* const* out, const int64_t* pos0, int64_t n_heads,
                                 int64_t n_kv_heads, int64_t head_dim) {

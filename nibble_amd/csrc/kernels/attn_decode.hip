@@ -15,14 +15,14 @@ namespace {
 
 using namespace nbh_decode;
 
-template <int HD, int GB>
+template <int HD, int GB, typename KV>
 __global__ __launch_bounds__(kDecodeThreads) void attn_decode_partial(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ out,
+    const float* __restrict__ q, const KV* __restrict__ k, const KV* __restrict__ v, float* __restrict__ out,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, int64_t pos0, int n_heads, int n_kv, int group, int n_sub,
     int n_chunks, int64_t groups_per_chunk, int64_t extra_groups, float qscale, const float2* __restrict__ q_rope,
-    int q_rope_neox, const float* __restrict__ k_new, const float* __restrict__ v_new, float* __restrict__ k_dst,
-    float* __restrict__ v_dst) {
-  partial_block<HD, GB>(q, k, v, out, ws_o, ws_ml, pos0, n_heads, n_kv, group, n_sub, n_chunks, groups_per_chunk,
+    int q_rope_neox, const float* __restrict__ k_new, const float* __restrict__ v_new, KV* __restrict__ k_dst,
+    KV* __restrict__ v_dst) {
+  partial_block<HD, GB, KV>(q, k, v, out, ws_o, ws_ml, pos0, n_heads, n_kv, group, n_sub, n_chunks, groups_per_chunk,
                         extra_groups, qscale, q_rope, q_rope_neox, k_new, v_new, k_dst, v_dst, blockIdx.x, blockIdx.y,
                         blockIdx.z);
 }
@@ -146,7 +146,7 @@ template <int HD, int GB>
 int resident_per_cu() {
   static const int n = [] {
     int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, attn_decode_partial<HD, GB>, kDecodeThreads, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, attn_decode_partial<HD, GB, float>, kDecodeThreads, 0) !=
             hipSuccess ||
         b < 1)
       b = 1;
@@ -191,25 +191,27 @@ Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t h
   return p;
 }
 
-// Appended row of a single-row call: new K/V rows in, cache rows out (all null when nothing is appended).
+// Appended row of a single-row call: new K/V rows in (fp32), cache rows out (all null when nothing is appended).
+template <typename KVT>
 struct Append {
   const float* k_new = nullptr;
   const float* v_new = nullptr;
-  float* k_dst = nullptr;
-  float* v_dst = nullptr;
+  KVT* k_dst = nullptr;
+  KVT* v_dst = nullptr;
 };
 
-template <int HD>
-int launch_decode(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0, int64_t H,
+template <int HD, typename KVT>
+int launch_decode(const float* q, const KVT* k, const KVT* v, float* out, int64_t n, int64_t pos0, int64_t H,
                   int64_t KV, float* ws, const Plan& p, float qscale, const float2* q_rope, int q_rope_neox,
-                  const Append& app, hipStream_t s) {
+                  const Append<KVT>& app, hipStream_t s) {
   float* ws_o = ws;
   float* ws_ml = ws ? ws + n * H * p.n_chunks * HD : nullptr;
   const int group = int(H / KV);
   const dim3 grid(p.n_chunks, unsigned(KV * p.n_sub), unsigned(n));
   hipError_t e;
 #define NBH_DECODE(GB)                                                                                             \
-  e = nbhs_timing::launch(NBHS_K_DECODE_PARTIAL, attn_decode_partial<HD, GB>, grid, dim3(kDecodeThreads), s, q, k, \
+  e = nbhs_timing::launch(NBHS_K_DECODE_PARTIAL, attn_decode_partial<HD, GB, KVT>, grid, dim3(kDecodeThreads), s, q, \
+                          k,                                                                                        \
                           v, out, ws_o, ws_ml, pos0, int(H), int(KV), group, p.n_sub, p.n_chunks,                   \
                           p.groups_per_chunk, p.extra_groups, qscale, q_rope, q_rope_neox, app.k_new, app.v_new,  \
                           app.k_dst, app.v_dst)
@@ -225,11 +227,33 @@ int launch_decode(const float* q, const float* k, const float* v, float* out, in
                              dim3(kDecodeThreads), s, ws_o, ws_ml, out, p.n_chunks);
 }
 
+// n appended rows into fp16 caches: K rotated exactly as the fp32 append does (rope_rotate in fp32, the table of
+// the RoPE kernel), then both K and V rounded to fp16. One thread per rotation pair (and the matching V pair).
+__global__ __launch_bounds__(256) void append_rope_f16_kernel(_Float16* __restrict__ k16, _Float16* __restrict__ v16,
+                                                              const float* __restrict__ kn,
+                                                              const float* __restrict__ vn, int64_t n, int64_t pos0,
+                                                              int64_t n_kv, int64_t hd,
+                                                              const float2* __restrict__ cs, int neox) {
+  const int64_t h2 = hd / 2, pairs = n * n_kv * h2;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < pairs; i += int64_t(gridDim.x) * 256) {
+    const int64_t row = i / (n_kv * h2), rem = i % (n_kv * h2), g = rem / h2, j = rem % h2;
+    const int64_t a = neox ? j : 2 * j, b = neox ? j + h2 : 2 * j + 1;  // the pair's two dimensions
+    const int64_t src = (row * n_kv + g) * hd, dst = ((pos0 + row) * n_kv + g) * hd;
+    float x = kn[src + a], y = kn[src + b];
+    rope_rotate(x, y, cs[(pos0 + row) * h2 + j]);
+    k16[dst + a] = _Float16(x);
+    k16[dst + b] = _Float16(y);
+    v16[dst + a] = _Float16(vn[src + a]);
+    v16[dst + b] = _Float16(vn[src + b]);
+  }
+}
+
 bool tiled_head_dim(int64_t hd) { return hd == 64 || hd == 128; }
 
-int decode(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0, int64_t n_heads,
+template <typename KVT>
+int decode(const float* q, const KVT* k, const KVT* v, float* out, int64_t n, int64_t pos0, int64_t n_heads,
            int64_t n_kv_heads, int64_t head_dim, float* workspace, int64_t workspace_floats, int cu_count,
-           const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, const Append& app, hipStream_t s) {
+           const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, const Append<KVT>& app, hipStream_t s) {
   if (!q || !k || !v || !out || n <= 0 || n > 65535 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 ||
       n_heads % n_kv_heads != 0 || head_dim <= 0 || head_dim > 256 || n_heads > 65535)
     return NBHS_EINVAL;
@@ -238,8 +262,12 @@ int decode(const float* q, const float* k, const float* v, float* out, int64_t n
   const float2* q_rope = reinterpret_cast<const float2*>(q_rope_cs);
   const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
   if (!tiled_head_dim(head_dim)) {
-    return nbhs_timing::launch(NBHS_K_GENERIC, attn_generic, dim3(unsigned(n_heads), unsigned(n)), dim3(64), s, q, k,
-                               v, out, pos0, int(n_heads), int(n_kv_heads), int(head_dim), qscale);
+    if constexpr (sizeof(KVT) != 4) {
+      return NBHS_EINVAL;  // fp16 caches: the tiled head sizes only
+    } else {
+      return nbhs_timing::launch(NBHS_K_GENERIC, attn_generic, dim3(unsigned(n_heads), unsigned(n)), dim3(64), s, q,
+                                 k, v, out, pos0, int(n_heads), int(n_kv_heads), int(head_dim), qscale);
+    }
   }
   const Plan p = make_plan(n, pos0, n_heads, n_kv_heads, head_dim, cu_count);
   const int64_t need = p.n_chunks == 1 ? 0 : n * n_heads * p.n_chunks * (head_dim + 2);
@@ -426,7 +454,16 @@ int nbhs_attn_decode_f32(const float* q, const float* k, const float* v, float* 
                          int64_t workspace_floats, int cu_count, const float* q_rope_cs, int64_t q_rope_rows,
                          int q_rope_neox, nbhs_stream stream) {
   return decode(q, k, v, out, n, pos0, n_heads, n_kv_heads, head_dim, workspace, workspace_floats, cu_count,
-                q_rope_cs, q_rope_rows, q_rope_neox, Append{}, reinterpret_cast<hipStream_t>(stream));
+                q_rope_cs, q_rope_rows, q_rope_neox, Append<float>{}, reinterpret_cast<hipStream_t>(stream));
+}
+
+int nbhs_attn_decode_f16kv(const float* q, const void* k16, const void* v16, float* out, int64_t n, int64_t pos0,
+                           int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float* workspace,
+                           int64_t workspace_floats, int cu_count, const float* q_rope_cs, int64_t q_rope_rows,
+                           int q_rope_neox, nbhs_stream stream) {
+  return decode(q, static_cast<const _Float16*>(k16), static_cast<const _Float16*>(v16), out, n, pos0, n_heads,
+                n_kv_heads, head_dim, workspace, workspace_floats, cu_count, q_rope_cs, q_rope_rows, q_rope_neox,
+                Append<_Float16>{}, reinterpret_cast<hipStream_t>(stream));
 }
 
 int nbhs_append_attn_decode_f32(const float* q, float* k_cache, float* v_cache, const float* k_new,
@@ -435,13 +472,42 @@ int nbhs_append_attn_decode_f32(const float* q, float* k_cache, float* v_cache, 
                                 const float* rope_cs, int64_t rope_rows, int neox, nbhs_stream stream) {
   // One query row, tiled head sizes, RoPE table required (it rotates q and the new K row alike).
   if (!k_new || !v_new || !rope_cs || !tiled_head_dim(head_dim)) return NBHS_EINVAL;
-  Append app;
+  Append<float> app;
   app.k_new = k_new;
   app.v_new = v_new;
   app.k_dst = k_cache;
   app.v_dst = v_cache;
   return decode(q, k_cache, v_cache, out, 1, pos0, n_heads, n_kv_heads, head_dim, workspace, workspace_floats,
                 cu_count, rope_cs, rope_rows, neox, app, reinterpret_cast<hipStream_t>(stream));
+}
+
+int nbhs_append_attn_decode_f16kv(const float* q, void* k16, void* v16, const float* k_new, const float* v_new,
+                                  float* out, int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                  float* workspace, int64_t workspace_floats, int cu_count, const float* rope_cs,
+                                  int64_t rope_rows, int neox, nbhs_stream stream) {
+  if (!k_new || !v_new || !rope_cs || !tiled_head_dim(head_dim)) return NBHS_EINVAL;
+  Append<_Float16> app;
+  app.k_new = k_new;
+  app.v_new = v_new;
+  app.k_dst = static_cast<_Float16*>(k16);
+  app.v_dst = static_cast<_Float16*>(v16);
+  return decode(q, static_cast<const _Float16*>(k16), static_cast<const _Float16*>(v16), out, 1, pos0, n_heads,
+                n_kv_heads, head_dim, workspace, workspace_floats, cu_count, rope_cs, rope_rows, neox, app,
+                reinterpret_cast<hipStream_t>(stream));
+}
+
+int nbhs_append_rope_f16kv(void* k16, void* v16, const float* k_new, const float* v_new, int64_t n, int64_t pos0,
+                           int64_t n_kv_heads, int64_t head_dim, const float* cs_table, int64_t table_rows, int neox,
+                           nbhs_stream stream) {
+  if (!k16 || !v16 || !k_new || !v_new || !cs_table || n <= 0 || pos0 < 0 || n_kv_heads <= 0 || head_dim <= 0 ||
+      head_dim % 2 != 0 || pos0 + n > table_rows)
+    return NBHS_EINVAL;
+  const int64_t pairs = n * n_kv_heads * (head_dim / 2);
+  const int64_t blocks = (pairs + 255) / 256;
+  return nbhs_timing::launch(NBHS_K_ROPE, append_rope_f16_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)),
+                             dim3(256), reinterpret_cast<hipStream_t>(stream), static_cast<_Float16*>(k16),
+                             static_cast<_Float16*>(v16), k_new, v_new, n, pos0, n_kv_heads, head_dim,
+                             reinterpret_cast<const float2*>(cs_table), neox);
 }
 
 }  // extern "C"

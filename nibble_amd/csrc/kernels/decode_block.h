@@ -102,6 +102,38 @@ __device__ __forceinline__ f32x4 load4(const float* p) {
 #endif
 }
 
+// Four consecutive cache elements as floats: fp32 caches (the reference's) or fp16 caches (8-byte loads, exact
+// widening).
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+template <typename KV>
+__device__ __forceinline__ f32x4 load_kv4(const KV* p) {
+  if constexpr (sizeof(KV) == 4) {
+    return load4(reinterpret_cast<const float*>(p));
+  } else {
+#if NBH_DECODE_NT
+    const f16x4 h = __builtin_nontemporal_load(reinterpret_cast<const f16x4*>(p));
+#else
+    const f16x4 h = *reinterpret_cast<const f16x4*>(p);
+#endif
+    return f32x4{float(h[0]), float(h[1]), float(h[2]), float(h[3])};
+  }
+}
+template <typename KV>
+__device__ __forceinline__ void store_kv4(KV* p, f32x4 x) {
+  if constexpr (sizeof(KV) == 4)
+    *reinterpret_cast<f32x4*>(p) = x;
+  else
+    *reinterpret_cast<f16x4*>(p) = f16x4{_Float16(x[0]), _Float16(x[1]), _Float16(x[2]), _Float16(x[3])};
+}
+// x as the cache will hold it (fp16 caches: rounded to nearest even).
+template <typename KV>
+__device__ __forceinline__ f32x4 as_stored(f32x4 x) {
+  if constexpr (sizeof(KV) == 4)
+    return x;
+  else
+    return f32x4{float(_Float16(x[0])), float(_Float16(x[1])), float(_Float16(x[2])), float(_Float16(x[3]))};
+}
+
 // Online-softmax state of one query head over some rows, as held by one lane: running max m (log2 domain), sum of
 // weights l, weighted V slice o (VPL float4 of the lane's dimensions).
 template <int VPL>
@@ -124,14 +156,14 @@ __device__ __forceinline__ void merge(State<VPL>& a, float bm, float bl, const f
 
 // One workgroup of the split-context kernel: chunk `chunk` of query row t for KV head x head subgroup `by`
 // (by / n_sub, by % n_sub). HD: head_dim (64 or 128). GB: query heads per workgroup (the GQA group, or a slice of
-// it). Needs kDecodeThreads threads.
-template <int HD, int GB>
+// it). KV: the cache element type (float, or _Float16 for an fp16 cache). Needs kDecodeThreads threads.
+template <int HD, int GB, typename KV = float>
 __device__ __forceinline__ void partial_block(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ out,
+    const float* __restrict__ q, const KV* __restrict__ k, const KV* __restrict__ v, float* __restrict__ out,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, int64_t pos0, int n_heads, int n_kv, int group, int n_sub,
     int n_chunks, int64_t groups_per_chunk, int64_t extra_groups, float qscale, const float2* __restrict__ q_rope,
-    int q_rope_neox, const float* __restrict__ k_new, const float* __restrict__ v_new, float* __restrict__ k_dst,
-    float* __restrict__ v_dst, int chunk, int by, int64_t t) {
+    int q_rope_neox, const float* __restrict__ k_new, const float* __restrict__ v_new, KV* __restrict__ k_dst,
+    KV* __restrict__ v_dst, int chunk, int by, int64_t t) {
   constexpr int VPL = 2;                            // float4 per lane per row
   constexpr int LPR = HD / (4 * VPL);               // lanes per K/V row: 8 (hd 64) or 16 (hd 128)
   constexpr int RPS = 64 / LPR;                     // rows per wave load
@@ -161,15 +193,15 @@ __device__ __forceinline__ void partial_block(
 #endif
 
   const int64_t row_stride = int64_t(n_kv) * HD;
-  const float* kb = k + int64_t(g) * HD + 4 * dl;  // float4 column dl + LPR * i of the row
-  const float* vb = v + int64_t(g) * HD + 4 * dl;
+  const KV* kb = k + int64_t(g) * HD + 4 * dl;  // float4 column dl + LPR * i of the row
+  const KV* vb = v + int64_t(g) * HD + 4 * dl;
 
   // Single-row append: the workgroup whose last row group holds row pos0 (= len - 1, n is 1) owns the new row.
   const bool append = k_new != nullptr;
   const int64_t new_grp = pos0 / kStep;
   const bool owner = append && gcnt > 0 && g0 + (gcnt - 1) * gstride == new_grp;
-  const float* knb = append ? k_new + int64_t(g) * HD + 4 * dl : kb;  // the new row's lane slice
-  const float* vnb = append ? v_new + int64_t(g) * HD + 4 * dl : vb;
+  const float* knb = append ? k_new + int64_t(g) * HD + 4 * dl : nullptr;  // the new row's lane slice
+  const float* vnb = append ? v_new + int64_t(g) * HD + 4 * dl : nullptr;
 
   // One iteration's rows: kUnroll row slots, VPL float4 of K and of V each. Rows past the causal window are
   // clamped to the last valid row (never read out of range) and masked in the partial iteration. When appending,
@@ -184,12 +216,22 @@ __device__ __forceinline__ void partial_block(
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t j = min(row_of(grp, u), len - 1);
       const bool fresh = append && j >= pos0;
-      const float* kr = fresh ? knb : kb + j * row_stride;
-      const float* vr = fresh ? vnb : vb + j * row_stride;
+      if constexpr (sizeof(KV) == 4) {
+        const float* kr = fresh ? knb : reinterpret_cast<const float*>(kb) + j * row_stride;
+        const float* vr = fresh ? vnb : reinterpret_cast<const float*>(vb) + j * row_stride;
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        r.k[u][i] = load4(kr + 4 * LPR * i);
-        r.v[u][i] = load4(vr + 4 * LPR * i);
+        for (int i = 0; i < VPL; ++i) {
+          r.k[u][i] = load4(kr + 4 * LPR * i);
+          r.v[u][i] = load4(vr + 4 * LPR * i);
+        }
+      } else {  // the appended row's lanes read cache row 0 instead (their values are replaced in compute)
+        const KV* kr = kb + (fresh ? 0 : j) * row_stride;
+        const KV* vr = vb + (fresh ? 0 : j) * row_stride;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+          r.k[u][i] = load_kv4(kr + 4 * LPR * i);
+          r.v[u][i] = load_kv4(vr + 4 * LPR * i);
+        }
       }
     }
   };
@@ -238,6 +280,12 @@ __device__ __forceinline__ void partial_block(
       nv[i] = *reinterpret_cast<const f32x4*>(vnb + 4 * LPR * i);
     }
     rotate(nk, pos0);
+    // attend to the row as the cache will hold it
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      nk[i] = as_stored<KV>(nk[i]);
+      nv[i] = as_stored<KV>(nv[i]);
+    }
   }
 
   f32x4 qv[GB][VPL];
@@ -325,12 +373,12 @@ __device__ __forceinline__ void partial_block(
 
   // The appended row goes into its cache row once per KV head (head subgroup 0 of the owner).
   if (owner && sg == 0 && wave == 0 && lane < LPR) {
-    float* kd = k_dst + pos0 * row_stride + int64_t(g) * HD + 4 * dl;
-    float* vd = v_dst + pos0 * row_stride + int64_t(g) * HD + 4 * dl;
+    KV* kd = k_dst + pos0 * row_stride + int64_t(g) * HD + 4 * dl;
+    KV* vd = v_dst + pos0 * row_stride + int64_t(g) * HD + 4 * dl;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      *reinterpret_cast<f32x4*>(kd + 4 * LPR * i) = nk[i];
-      *reinterpret_cast<f32x4*>(vd + 4 * LPR * i) = nv[i];
+      store_kv4(kd + 4 * LPR * i, nk[i]);
+      store_kv4(vd + 4 * LPR * i, nv[i]);
     }
   }
 
