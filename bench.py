@@ -193,6 +193,64 @@ def ragged_decode(be, steps, warmup):
 FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 (MFMA)
 
 
+def f16kv_decode(be, steps, warmup):
+    """Decode steps over fp16 KV caches (an extension: the reference's cache is fp32), at the config-4 shape: 16
+    layers at 32k context, one append_rope_attention_f16kv per layer (the new row rides in the attention launch).
+    HBM GB/s of the fp16 K and V rows each step reads."""
+    shape, NL, ctx = configs.LLAMA32_1B, 16, 32768
+    H, KV, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
+    rows = ctx + steps + warmup + 1
+    halves = rows * KV * D
+    rng = np.random.default_rng(5)
+    host = rng.standard_normal(halves).astype(np.float16).view(np.float32)
+    ck, cv = [], []
+    for l in range(NL):
+        k, v = be.alloc(halves // 2), be.alloc(halves // 2)
+        if l == 0:
+            be.write(k, host)
+            be.write(v, host[::-1].copy())
+        else:
+            be.copy(k, ck[0], halves // 2)
+            be.copy(v, cv[0], halves // 2)
+        ck.append(k)
+        cv.append(v)
+    q, kd, vd, out = be.alloc(H * D), be.alloc(KV * D), be.alloc(KV * D), be.alloc(H * D)
+    for p_, n_ in ((q, H * D), (kd, KV * D), (vd, KV * D)):
+        be.fill_normal(p_, n_, seed=n_)
+    base, neox, ff = shape.rope_base, shape.neox, shape.freq_factors()
+
+    def step(s):
+        for l in range(NL):
+            be.append_rope_attention_f16kv(q, ck[l], cv[l], kd, vd, out, 1, ctx + s, H, KV, D, base, neox, ff)
+
+    for s in range(warmup):
+        step(s)
+    be.sync()
+    e0, e1 = be.event(), be.event()
+    e0.record()
+    for s in range(warmup, warmup + steps):
+        step(s)
+    e1.record()
+    ms = e0.elapsed_ms(e1) / steps
+    byts = sum(NL * 4 * KV * D * (ctx + s + 1) for s in range(warmup, warmup + steps)) / steps
+    KernelTiming.enable(True, only=KernelTiming.DECODE_PARTIAL)
+    step(warmup + steps)
+    be.sync()
+    pm, pn = KernelTiming.read(KernelTiming.DECODE_PARTIAL)
+    KernelTiming.enable(False)
+    for p_ in ck + cv + [q, kd, vd, out]:
+        be.free(p_)
+    gbs = byts / (ms * 1e-3) / 1e9
+    part_us = pm / pn * 1e3
+    part_gbs = 4 * KV * D * (ctx + warmup + steps + 1) / (part_us * 1e-6) / 1e9
+    log(f"fp16 KV decode: {ms:.4f} ms/step over {NL} layers -> {gbs:.0f} GB/s of fp16 rows ({gbs / HBM_PEAK_GBS:.1%}); "
+        f"partial kernel {part_us:.2f} us -> {part_gbs:.0f} GB/s")
+    return {"metric": "decode attn over fp16 KV caches (extension), HBM GB/s of the fp16 rows read",
+            "value": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "ms_per_step": round(ms, 4),
+            "layers": NL, "ctx": ctx, "steps": steps,
+            "partial_kernel": {"avg_launch_us": round(part_us, 3), "value": round(part_gbs, 1), "unit": "GB/s"}}
+
+
 def qkv_projection(be, steps, warmup, chunk=512, chunk_reps=3):
     """The QKV projection feeding the attention path (transformer.cpp:171-194) at the Llama-3.2-1B shape: F16
     weights wq [2048, 2048], wk and wv [512, 2048] per layer, 16 layers, one matmul_multi per layer writing q and the
@@ -682,6 +740,8 @@ def main():
     }
     if args.cfg5_steps > 0:
         result["config5"] = ragged_decode(be, args.cfg5_steps, 2)
+    if args.cfg5_steps > 0:
+        result["decode_f16kv"] = f16kv_decode(be, 32, 4)
     if args.qkv_steps > 0:
         result["qkv_projection"] = qkv_projection(be, args.qkv_steps, 4)
         result["quant_projection"] = quant_projection(be, args.qkv_steps, 4)

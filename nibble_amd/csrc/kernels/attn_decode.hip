@@ -167,14 +167,15 @@ int resident_per_cu(int64_t head_dim, int gb) {
 // evenly over min(slots, groups) chunks; the remainder goes one group each to the first chunks, which load that
 // group together with their first one (see attn_decode_partial), so a context one row past a round size costs no
 // workgroup an extra HBM round trip and no workgroup waits for a free slot.
-Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t head_dim, int cu_count) {
+Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t head_dim, int cu_count,
+               int unroll = kUnroll) {
   Plan p;
   const int64_t group = n_heads / n_kv;
   p.gb = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8;
   p.n_sub = int((group + p.gb - 1) / p.gb);
   const int64_t max_len = pos0 + n;
   const int64_t lpr = head_dim / 8;
-  const int64_t step = (64 / lpr) * kUnroll * (kDecodeThreads / 64);  // rows a workgroup covers per iteration
+  const int64_t step = (64 / lpr) * unroll * (kDecodeThreads / 64);  // rows a workgroup covers per iteration
   const int64_t units = (max_len + step - 1) / step;
   const int64_t cus = cu_count > 0 ? cu_count : 256;
   const int64_t streams = n * n_kv * p.n_sub;  // workgroups per chunk index
@@ -269,7 +270,8 @@ int decode(const float* q, const KVT* k, const KVT* v, float* out, int64_t n, in
                                  k, v, out, pos0, int(n_heads), int(n_kv_heads), int(head_dim), qscale);
     }
   }
-  const Plan p = make_plan(n, pos0, n_heads, n_kv_heads, head_dim, cu_count);
+  // (an fp16 plan has at most the chunks of the fp32 one: nbhs_attn_decode_workspace covers both)
+  const Plan p = make_plan(n, pos0, n_heads, n_kv_heads, head_dim, cu_count, unroll_for(int(sizeof(KVT))));
   const int64_t need = p.n_chunks == 1 ? 0 : n * n_heads * p.n_chunks * (head_dim + 2);
   if (need > 0 && (!workspace || workspace_floats < need)) return NBHS_EINVAL;
   if (n_kv_heads * p.n_sub > 65535) return NBHS_EINVAL;

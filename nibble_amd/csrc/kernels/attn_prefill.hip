@@ -196,8 +196,8 @@ void attn_prefill_kernel(
     const int streams = n_kv * fp32_n_sub;
     const int64_t p0 = pos0 - fp32_rows;
     constexpr int64_t kStepRows = (nbh_decode::kDecodeThreads / 64) * (64 / (HD / 8)) * nbh_decode::kUnroll;
-    nbh_decode::partial_block<HD, 4, float>(q - fp32_rows * n_heads * HD, kc, vc, out - fp32_rows * n_heads * HD, nullptr,
-                                     nullptr, p0, n_heads, n_kv, group, fp32_n_sub, 1,
+    nbh_decode::partial_block<HD, 4, float>(q - fp32_rows * n_heads * HD, kc, vc, out - fp32_rows * n_heads * HD,
+                                     nullptr, nullptr, p0, n_heads, n_kv, group, fp32_n_sub, 1,
                                      (p0 + fp32_rows + kStepRows - 1) / kStepRows, 0, qscale, q_rope, q_rope_neox,
                                      nullptr, nullptr, nullptr, nullptr, 0, int(e % streams),
                                      fp32_rows - 1 - e / streams);  // longest rows first

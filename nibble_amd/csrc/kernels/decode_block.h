@@ -61,6 +61,9 @@ constexpr int64_t kLongGroups = 12;
 #define NBH_DECODE_INTERLEAVE 1
 #endif
 constexpr int kUnroll = NBH_DECODE_UNROLL;
+// Row slots per lane per iteration for a cache element of `bytes` bytes: fp16 caches take twice the rows, so that
+// an iteration moves as many bytes as with fp32 (the kernel is bound by iterations, one memory round trip each).
+constexpr int unroll_for(int bytes) { return bytes == 4 ? kUnroll : 2 * kUnroll; }
 constexpr int kMaxChunks = 4096;  // partials per (row, head); bounds the combine kernel's LDS table
 constexpr float kLazy = 8.0f;     // allowed growth of scores over the running max before a rescale
 
@@ -167,7 +170,8 @@ __device__ __forceinline__ void partial_block(
   constexpr int VPL = 2;                            // float4 per lane per row
   constexpr int LPR = HD / (4 * VPL);               // lanes per K/V row: 8 (hd 64) or 16 (hd 128)
   constexpr int RPS = 64 / LPR;                     // rows per wave load
-  constexpr int WAVE_ROWS = RPS * kUnroll;          // rows per wave iteration
+  constexpr int KU = unroll_for(int(sizeof(KV)));   // row slots per lane per iteration
+  constexpr int WAVE_ROWS = RPS * KU;               // rows per wave iteration
   constexpr int NW = kDecodeThreads / 64;           // waves per workgroup
   constexpr int64_t kStep = NW * WAVE_ROWS;         // rows the workgroup covers per iteration
   __shared__ float sm_m[NW][GB], sm_l[NW][GB];
@@ -203,17 +207,17 @@ __device__ __forceinline__ void partial_block(
   const float* knb = append ? k_new + int64_t(g) * HD + 4 * dl : nullptr;  // the new row's lane slice
   const float* vnb = append ? v_new + int64_t(g) * HD + 4 * dl : nullptr;
 
-  // One iteration's rows: kUnroll row slots, VPL float4 of K and of V each. Rows past the causal window are
+  // One iteration's rows: KU row slots, VPL float4 of K and of V each. Rows past the causal window are
   // clamped to the last valid row (never read out of range) and masked in the partial iteration. When appending,
   // lanes on row pos0 (and those clamped to it) read k_new / v_new instead of the cache row, which this kernel
   // writes; compute() replaces those values with the rotated row.
   struct Rows {
-    f32x4 k[kUnroll][VPL], v[kUnroll][VPL];
+    f32x4 k[KU][VPL], v[KU][VPL];
   };
   auto row_of = [&](int64_t grp, int u) { return grp * kStep + wave * WAVE_ROWS + u * RPS + sub; };
   auto load = [&](int64_t grp, Rows& r) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < KU; ++u) {
       const int64_t j = min(row_of(grp, u), len - 1);
       const bool fresh = append && j >= pos0;
       if constexpr (sizeof(KV) == 4) {
@@ -311,7 +315,7 @@ __device__ __forceinline__ void partial_block(
     // Wave-uniform: does it hold the appended row? Then its lanes take the rotated row from registers.
     if (owner && grp_idx == new_grp && grp_idx * kStep + wave * WAVE_ROWS + WAVE_ROWS > pos0) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < KU; ++u) {
         const bool fresh = row_of(grp_idx, u) >= pos0;
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
@@ -323,10 +327,10 @@ __device__ __forceinline__ void partial_block(
 #pragma unroll
     for (int h = 0; h < GB; ++h) {
       if (h >= gcount) continue;
-      float sc[kUnroll];
+      float sc[KU];
       float mloc = -INFINITY;
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < KU; ++u) {
         f32x4 prod = qv[h][0] * r.k[u][0];
 #pragma unroll
         for (int i = 1; i < VPL; ++i) prod += qv[h][i] * r.k[u][i];
@@ -350,7 +354,7 @@ __device__ __forceinline__ void partial_block(
       }
       const float ms = st[h].m == -INFINITY ? 0.0f : st[h].m;
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < KU; ++u) {
         const float p = exp2_raw(sc[u] - ms);
         st[h].l += p;
 #pragma unroll
