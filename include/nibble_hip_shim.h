@@ -156,6 +156,9 @@ int nbhs_attn_decode_batch_f32(int64_t n_seq, const float* const* q, const float
  * the prefill kernel's work list: staging empties it for the prefill launch that follows. */
 int64_t nbhs_prefill_staging_halves(int64_t rows, int64_t n_kv_heads, int64_t head_dim); /* per tensor */
 int64_t nbhs_prefill_aux_words(int64_t n, int64_t n_heads, int64_t n_kv_heads);
+/* The largest nbhs_prefill_aux_words(m, n_heads, kv) over m <= max_rows and every kv dividing n_heads: the work list
+ * that serves any prefill call of up to max_rows rows with n_heads query heads (what reserve() allocates). */
+int64_t nbhs_prefill_aux_words_bound(int64_t max_rows, int64_t n_heads);
 int nbhs_stage_kv_f16(const float* k, const float* v, void* k16, void* vt16, int64_t rows, int64_t n_kv_heads,
                       int64_t head_dim, uint32_t* aux, int64_t aux_words, nbhs_stream s);
 /* KV append fused with the staging: cache rows pos0..pos0+n-1 receive rope(k_new) and v_new (as

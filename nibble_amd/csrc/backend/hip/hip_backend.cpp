@@ -183,8 +183,8 @@ void HipBackend::reserve(const ReserveParams& rp) {
     throw Error("reserve: RoPE table for n_ctx=" + str(rp.n_ctx) + " is too large");
   int64_t ids_bytes;
   if (overflow_mul(rp.max_rows, int64_t(sizeof(int32_t)), &ids_bytes)) throw Error("reserve: max_rows too large");
-  // the prefill work list of a call of up to max_rows rows (one word per (row tile, KV head), n_kv <= n_heads)
-  const int64_t aux_words = rp.max_rows > 0 && rp.n_heads > 0 ? nbhs_prefill_aux_words(rp.max_rows, rp.n_heads, 1) : 0;
+  // the prefill work list of a call of up to max_rows rows (one word per (row tile, KV head)), for any KV head count
+  const int64_t aux_words = rp.max_rows > 0 && rp.n_heads > 0 ? nbhs_prefill_aux_words_bound(rp.max_rows, rp.n_heads) : 0;
   reserved_ = rp;
   ensure(decode_ws_, decode_ws_bytes_, size_t(ws_floats) * sizeof(float));
   ensure(acts_buf_, acts_buf_bytes_, size_t(acts));
@@ -690,6 +690,7 @@ const float* HipBackend::rope_table(int64_t head_dim, int64_t rows_needed, const
   const size_t tbytes = size_t(entries) * sizeof(float);
   const bool slab_free =
       std::none_of(rope_tables_.begin(), rope_tables_.end(), [&](const RopeTable& t) { return t.dev == rope_slab_; });
+  bool was_slab = false;  // a growing table that held the slab may keep it
   if (it == rope_tables_.end()) {
     rope_tables_.push_back(RopeTable{});
     it = rope_tables_.end() - 1;
@@ -698,11 +699,12 @@ const float* HipBackend::rope_table(int64_t head_dim, int64_t rows_needed, const
     if (ff) it->factors.assign(ff, ff + half);
   } else {
     check(nbhs_stream_sync(stream_), "sync before rope table growth");  // queued work may still read it
-    if (it->dev != rope_slab_) check(nbhs_free(it->dev), "free rope table");
+    was_slab = rope_slab_ && it->dev == rope_slab_;
+    if (!was_slab) check(nbhs_free(it->dev), "free rope table");
     it->dev = nullptr;
     it->rows = 0;
   }
-  if (rope_slab_ && tbytes <= rope_slab_bytes_ && (slab_free || it->dev == rope_slab_)) {
+  if (rope_slab_ && tbytes <= rope_slab_bytes_ && (slab_free || was_slab)) {
     it->dev = rope_slab_;
   } else {
     void* d = nullptr;

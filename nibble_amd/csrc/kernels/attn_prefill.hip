@@ -1,12 +1,13 @@
 // Causal GQA prefill attention on gfx950 MFMA: Backend::attention (backend.h:68-69) for many query rows,
 // semantics of ref_ops.cpp:188-214 (row t attends to cache rows 0..pos0+t; head h reads KV head h/(H/KV)).
 //
-// Numerics: Q is scaled by log2(e)/sqrt(d) and rounded to fp16, K and V come from fp16 copies of the fp32 cache
-// (stage_kv), QK^T and PV run on v_mfma_f32_32x32x16_f16 with fp32 accumulation, and the online softmax (shift,
+// Numerics: Q is scaled by log2(e)/sqrt(d) and split into fp16 high and low parts (a rounding of the query would
+// be shared by every key of its row), K and V come from fp16 copies of the fp32 cache (stage_kv), QK^T (K times
+// both query parts) and PV run on v_mfma_f32_32x32x16_f16 with fp32 accumulation, and the online softmax (shift,
 // exp2, running sums, rescaling) is fp32. The softmax shift is not the running max: it is set from the first tile
 // and raised only when a tile's weights outgrow it (checked through their sum, see kPSumMax), so the per-tile
 // max, the subtraction (folded into the MFMA accumulator init) and the O rescale all leave the common path; the
-// result is the same normalised softmax, since any shift cancels. The host routes rows with fewer than 256
+// result is the same normalised softmax, since any shift cancels. The host routes rows with fewer than 128
 // visible keys to the fp32 decode kernel, where fp16 rounding of a few V rows is not averaged away.
 //
 // Layout (per wave, 32 query rows):
@@ -69,29 +70,45 @@ constexpr float kPSumMax = 4096.0f;
 // it, then the list itself, then one arrival counter per list entry (zeroed by the staging launch).
 constexpr int kAuxHead = 16;
 // Per key split of a prefill row tile, the record beside its partial output: shift, sum, sum of squared weights,
-// the error estimate's score coefficient (est_c1 * |q|^2/d * largest |k|^2) and the largest |v|^2.
+// the error estimate's score coefficient (est_c1 * |y|^2/d * largest |k|^2), the largest |v|^2 and the query
+// residual's coefficient (est_c3 * |r| * sqrt(largest |k|^2)).
 constexpr int kSplitRec = 6;
 
-// Rounding-error estimate of a row computed with fp16 operands (Q * log2(e)/sqrt(d), K, V and the weights P
-// rounded to nearest, relative error at most u = 2^-11, modelled as independent with variance u^2/3 each; fp32
-// accumulation). To first order the output error of dimension d is
-//   sum_j w_j [ln2 (e_j - e_mean)(v_jd - o_d) + eps_v,jd v_jd + (eps_p,j - eps_p,mean)(v_jd - o_d)],
-// w_j = p_j / l, with e_j the score error (log2 units) of key j: variance about (2u^2/3) |q|^2/d |k_j|^2 for
-// query and key rounding. Bounding |k_j|^2 by the largest row norm K, |v_jd| by the largest element V and
+// Rounding-error estimate of a row computed with fp16 operands. The scaled query y = Q * log2(e)/sqrt(d) enters
+// the scores as two fp16 parts, y = hi + lo + r (hi = fp16(y), lo = fp16(y - hi), |r| ~ 2^-22 |y|), so its
+// rounding is not a per-row error shared by every key: K, V and the weights P are rounded to nearest (relative
+// error at most u = 2^-11), and those roundings, one per key, are modelled as independent with variance u^2/3
+// each; accumulation is fp32. To first order the output error of dimension d is
+//   sum_j w_j [ln2 (e_j - e_mean)(v_jd - o_d) + eps_v,jd v_jd + (eps_p,j - eps_p,mean)(v_jd - o_d)] + c_d,
+// w_j = p_j / l, with e_j the score error (log2 units) of key j from rounding k_j: variance about
+// (u^2/3) |y|^2/d |k_j|^2. Bounding |k_j|^2 by the largest row norm K, |v_jd| by the largest element V and
 // (v - o)^2 by 2 (V^2 + O^2), O the row's largest output:
-//   var <= (sum_j p_j^2 / l^2) [2 ln2^2 (2u^2/3) (|q|^2/d) K (V^2 + O^2) + (u^2/3) (3 V^2 + 2 O^2)].
-// The row is accepted when kEstZ * sqrt(var) <= kEstBudget (the 1e-3 parity bar). Checked against an exact
-// emulation of this kernel's rounding over N(0,1) data at score scales 0.5-30, keys with 1 % outlier rows x8,
-// outlier V rows, a query aligned with one key, low-rank keys, a large common key or value component, 65-8192
-// keys, head_dim 64 and 128 (7168 rows, two seeds): the emulated error was at most 0.79 sqrt(var), so an accepted
-// row errs by at most 0.79 / 1.5 of the bar; the worst accepted row erred by 4.0e-4 (tests/test_error_estimate.py
-// keeps a subset of these cases).
+//   var <= (sum_j p_j^2 / l^2) [2 ln2^2 (u^2/3) (|y|^2/d) K (V^2 + O^2) + (u^2/3) (3 V^2 + 2 O^2)].
+// The query's residual r is common to every key of the row, so its term c_d = ln2 sum_j w_j (r.k_j)(v_jd - o_d)
+// does not average out; it is bounded outright, |c_d| <= ln2 |r| sqrt(K) (V + O), with |r| computed exactly per row.
+// The row is accepted when kEstZ * sqrt(var) + ln2 |r| sqrt(K) (V + O) <= kEstBudget (the 1e-3 parity bar).
+// Checked against an exact emulation of this kernel's rounding over N(0,1) data at score scales 0.5-30, keys with
+// 1 % outlier rows x8, outlier V rows, a query aligned with one key, low-rank keys, a large common key or value
+// component, and q, K and V projected from shared low-rank hidden states (K and V correlated: the case where an
+// unsplit query's rounding adds up coherently over the keys), 65-8192 keys, head_dim 64 and 128: the emulated error
+// stayed within 0.71 sqrt(var) (tests/test_error_estimate.py), so an accepted row errs by at most 0.71 / 1.5 of the
+// bar.
 constexpr float kEstZ = 1.5f;
 constexpr float kEstBudget = 1e-3f;
 constexpr double kEstU = 1.0 / 2048.0;
 constexpr double kLn2 = 0.6931471805599453;
 
 __device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }  // v_exp_f32; -inf -> 0
+
+// (hi, lo) of x: hi = fp16(x), lo = fp16(x - hi). Both must start from the same x: a product passed in is pinned to
+// its fp32 rounding first (the empty asm), or the compiler fuses the multiply into hi's conversion (v_fma_mixlo_f16,
+// one rounding of the exact product) while lo subtracts a hi rounded from the fp32 product - at an fp16 tie the two
+// disagree and hi + lo misses x by one fp16 ulp. x - hi is exact in fp32 (hi is x's nearest fp16).
+__device__ __forceinline__ half2_t split_f16(float x) {
+  asm("" : "+v"(x));
+  const _Float16 hi = (_Float16)x;
+  return half2_t{hi, (_Float16)(x - (float)hi)};
+}
 
 // Chunk swizzle of LDS tile rows with CPR 16-byte chunks: rows 0..7 (and 0..15) map a given chunk to distinct
 // chunks, and for 8-chunk (128-byte) rows also the rows of equal parity among 16 consecutive ones (64-bank LDS
@@ -272,7 +289,8 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(KVT* ck, KVT* cv, const f
 // architectural VGPRs (-amdgpu-mfma-vgpr-form, see the Makefile), so the S^T and O^T accumulators both stay
 // resident with no per-tile copies through accumulation registers. head_dim 64 is held to 3 waves per SIMD
 // (<= 168 registers, measured fastest: 2 waves with more registers per wave lose more latency hiding than they
-// gain); head_dim 128 needs more registers and runs at what fits.
+// gain); head_dim 128 is held to 2 (256 registers: its query's high and low parts alone take 64), where two
+// values live across the key loop go to scratch outside it.
 #ifndef NBH_PREFILL_WAVES_PER_EU
 #define NBH_PREFILL_WAVES_PER_EU 3
 #endif
@@ -281,14 +299,14 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(KVT* ck, KVT* cv, const f
 #endif
 template <int HD, typename KVT>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(
-    HD == 64 ? NBH_PREFILL_MIN_WAVES_PER_EU : 1, NBH_PREFILL_WAVES_PER_EU)))
+    HD == 64 ? NBH_PREFILL_MIN_WAVES_PER_EU : 2, NBH_PREFILL_WAVES_PER_EU)))
 void attn_prefill_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ k16, const _Float16* __restrict__ vt16,
     float* __restrict__ out, int64_t n, int64_t pos0, int n_heads, int n_kv, int group, int64_t rows_pad,
     int n_tiles, float qscale, const float2* __restrict__ q_rope, int q_rope_neox, const KVT* __restrict__ kc,
     const KVT* __restrict__ vc, int64_t fp32_rows, int fp32_n_sub, int n_split, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, const float2* __restrict__ kstats, uint32_t* __restrict__ aux, int aux_cap,
-    float est_c1, float est_c2) {
+    float est_c1, float est_c2, float est_c3) {
   // Workgroups past the MFMA tiles: query row t < fp32_rows of the call (q and out start fp32_rows rows before
   // this launch's MFMA rows) for KV head x head subgroup `by`, in fp32 over its whole causal window.
   static_assert(kWaves * 64 == nbh_decode::kDecodeThreads, "the fp32 rows' body runs on the MFMA workgroup size");
@@ -360,8 +378,10 @@ void attn_prefill_kernel(
   // position-major (cos, sin) table) is rotated here, exactly as the RoPE kernel would have in memory: the lane
   // holds both members of every pair it needs - adjacent pairs within its 8 dimensions, NeoX pairs (j, j + HD/2)
   // in chunks c and c + DC/2.
-  half8_t qf[kQB][DC];
-  float qn2[kQB];
+  // qf / qlo: the scaled query's fp16 high and low parts (both multiply each K fragment, see split_f16); qr2: the
+  // squared norm of what the two leave out, for the error estimate's query term.
+  half8_t qf[kQB][DC], qlo[kQB][DC];
+  float qn2[kQB], qr2[kQB];
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
     const float* qrow = q + (t[qb] * n_heads + head[qb]) * HD;
@@ -390,16 +410,22 @@ void attn_prefill_kernel(
           for (int e = 0; e < 8; e += 2) rope_rotate(x[c][e], x[c][e + 1], cs[(16 * c + 8 * hf + e) / 2]);
       }
     }
-    float ss = 0.f;
+    float ss = 0.f, rr = 0.f;
 #pragma unroll
     for (int c = 0; c < DC; ++c)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float y = x[c][e] * qscale;
+        float y = x[c][e] * qscale;
+        asm("" : "+v"(y));  // hi, lo and the norms all from y's fp32 rounding (see split_f16)
         ss += y * y;
-        qf[qb][c][e] = (_Float16)y;
+        const half2_t hl = split_f16(y);
+        qf[qb][c][e] = hl[0];
+        qlo[qb][c][e] = hl[1];
+        const float r = (y - float(hl[0])) - float(hl[1]);  // both differences exact in fp32
+        rr += r * r;
       }
     qn2[qb] = (ss + __shfl_xor(ss, 32, 64)) * (1.0f / HD);  // mean square of the scaled query
+    qr2[qb] = rr + __shfl_xor(rr, 32, 64);
   }
 
   floatx16 oacc[kQB][DT];
@@ -505,32 +531,36 @@ void attn_prefill_kernel(
       const float2 tst = kstats[int64_t(g) * (rows_pad / kBN) + kt];  // the tile's statistics (stage_kv_kernel)
       kmx = fmaxf(kmx, tst.x);
       vmx = fmaxf(vmx, tst.y);
-      // S^T for the tile's two 32-key halves and every query block; each K fragment read from LDS serves all
-      // blocks, and the chains are interleaved so consecutive MFMAs do not wait on each other's results. The
-      // raised wave priority keeps the MFMA pipe fed while other waves of the SIMD run their softmax VALU work.
+      // S^T for the tile's two 32-key halves and every query block, K times the query's high and then its low
+      // part in one accumulator; each K fragment read from LDS serves both parts and all blocks, and the chains
+      // are interleaved so consecutive MFMAs do not wait on each other's results. The raised wave priority keeps
+      // the MFMA pipe fed while other waves of the SIMD run their softmax VALU work.
       floatx16 s[kQB][2];
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int c = 0; c < DC; ++c)
+      for (int c = 0; c < DC; ++c) {
+        const half8_t a[2] = {k_frag(cur, 0, c), k_frag(cur, 1, c)};
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const half8_t a = k_frag(cur, kk, c);
+        for (int part = 0; part < 2; ++part)
 #pragma unroll
-          for (int qb = 0; qb < kQB; ++qb) {
-            floatx16 c0;
-            if (c == 0) {
-              if constexpr (kFold) {
-                c0 = mneg;
+          for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+              floatx16 c0;
+              if (c == 0 && part == 0) {
+                if constexpr (kFold) {
+                  c0 = mneg;
+                } else {
+#pragma unroll
+                  for (int r = 0; r < 16; ++r) c0[r] = 0.f;
+                }
               } else {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) c0[r] = 0.f;
+                c0 = s[qb][kk];
               }
-            } else {
-              c0 = s[qb][kk];
+              s[qb][kk] =
+                  __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk], part == 0 ? qf[qb][c] : qlo[qb][c], c0, 0, 0, 0);
             }
-            s[qb][kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[qb][c], c0, 0, 0, 0);
-          }
-        }
+      }
       __builtin_amdgcn_s_setprio(0);
       // Causal mask (and inactive rows) only where some key of the tile lies past the wave's first row.
       if (int64_t(kt) * kBN + kBN > wave_kfull) {
@@ -656,13 +686,15 @@ void attn_prefill_kernel(
     const float om2 = om * om, vg2 = vmx * vmx;
     const float est =
         l2_tot / (l_tot * l_tot) * (est_c1 * qn2[qb] * kmx * (vg2 + om2) + est_c2 * (3.f * vg2 + 2.f * om2));
-    flag = flag || (n_split == 1 && active[qb] && l_tot > 0.f && !(est <= 1.0f));
+    const float rk = est_c3 * sqrtf(qr2[qb] * kmx);  // the query residual's bound, per unit of (V + O)
+    flag = flag || (n_split == 1 && active[qb] && l_tot > 0.f && !(sqrtf(est) + rk * (vmx + om) <= 1.0f));
     if (n_split > 1 && active[qb] && hf == 0) {
       // a key split judges nothing alone (few keys look sharp): its terms go to the merge, which estimates the row
       float* rec = ws_ml + ((t[qb] * n_heads + head[qb]) * n_split + split) * kSplitRec;
       rec[2] = l2_tot;
       rec[3] = est_c1 * qn2[qb] * kmx;
       rec[4] = vg2;
+      rec[5] = rk;
     }
   }
   if (__syncthreads_or(flag) && threadIdx.x == 0) {
@@ -756,15 +788,6 @@ __global__ __launch_bounds__(kWaves * 64) void attn_prefill_precise_kernel(
   const int max_key_tiles = int((pos0 + n + kBN - 1) / kBN);
   const int ps = precise_ranges(count, ws_floats, HD, max_key_tiles);
   uint32_t* const arrivals = aux + kAuxHead + 2 * aux_cap;
-  // (hi, lo) of x: hi = fp16(x), lo = fp16(x - hi). Both must start from the same x: a product passed in is pinned
-  // to its fp32 rounding first (the empty asm), or the compiler fuses the multiply into hi's conversion
-  // (v_fma_mixlo_f16, one rounding of the exact product) while lo subtracts a hi rounded from the fp32 product -
-  // at an fp16 tie the two disagree and hi + lo misses x by one fp16 ulp.
-  auto split = [](float x) {
-    asm("" : "+v"(x));
-    const _Float16 hi = (_Float16)x;
-    return half2_t{hi, (_Float16)(x - (float)hi)};
-  };
   for (int64_t u = blockIdx.x; u < int64_t(count) * ps; u += gridDim.x) {
     const uint32_t it = uint32_t(u % count);
     const int range = int(u / count);
@@ -821,7 +844,7 @@ __global__ __launch_bounds__(kWaves * 64) void attn_prefill_precise_kernel(
       for (int c = 0; c < DC; ++c)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const half2_t hl = split(x[c][e] * qscale);
+          const half2_t hl = split_f16(x[c][e] * qscale);
           qh[c][e] = hl[0];
           qlw[c][e] = hl[1];
         }
@@ -869,7 +892,7 @@ __global__ __launch_bounds__(kWaves * 64) void attn_prefill_precise_kernel(
 #pragma unroll
       for (int i = 0; i < K_F4; ++i) {
         const int f = threadIdx.x + THREADS * i, r = f / (HD / 4), c4 = f % (HD / 4);
-        const half2_t sx = split(kr[i].x), sy = split(kr[i].y), sz = split(kr[i].z), sw = split(kr[i].w);
+        const half2_t sx = split_f16(kr[i].x), sy = split_f16(kr[i].y), sz = split_f16(kr[i].z), sw = split_f16(kr[i].w);
         const int at = r * HD + 8 * ((c4 >> 1) ^ swz<KCPR>(r)) + 4 * (c4 & 1);
         *reinterpret_cast<half4_t*>(&khi[at]) = half4_t{sx[0], sy[0], sz[0], sw[0]};
         *reinterpret_cast<half4_t*>(&klo[at]) = half4_t{sx[1], sy[1], sz[1], sw[1]};
@@ -885,7 +908,7 @@ __global__ __launch_bounds__(kWaves * 64) void attn_prefill_precise_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int d = 8 * db + e;
-          const half2_t sa = split(a8[e]), sb = split(b8[e]);
+          const half2_t sa = split_f16(a8[e]), sb = split_f16(b8[e]);
           const int at = d * kBN + 8 * ((pos >> 3) ^ swz<VCPR>(d)) + (pos & 7);
           *reinterpret_cast<half2_t*>(&vhi[at]) = half2_t{sa[0], sb[0]};
           *reinterpret_cast<half2_t*>(&vlo[at]) = half2_t{sa[1], sb[1]};
@@ -965,7 +988,7 @@ __global__ __launch_bounds__(kWaves * 64) void attn_prefill_precise_kernel(
         half8_t ph, pl;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const half2_t hl = split(sacc[kc >> 1][8 * (kc & 1) + e]);
+          const half2_t hl = split_f16(sacc[kc >> 1][8 * (kc & 1) + e]);
           ph[e] = hl[0];
           pl[e] = hl[1];
         }
@@ -1103,19 +1126,19 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
   const float* ml = ws_ml + rh * n_split * kSplitRec;
   const float4* po = reinterpret_cast<const float4*>(ws_o + rh * n_split * HD) + c4;
   float2 ml01[SPM], ml23[SPM];  // (shift, sum), (sum of squared weights, score coefficient)
-  float vg[SPM];                // largest |v|^2
+  float2 ml45[SPM];             // (largest |v|^2, query residual coefficient)
   float4 o[SPM];
 #pragma unroll
   for (int sp = 0; sp < SPM; ++sp) {
     ml01[sp] = make_float2(-INFINITY, 0.f);
     ml23[sp] = make_float2(0.f, 0.f);
-    vg[sp] = 0.f;
+    ml45[sp] = make_float2(0.f, 0.f);
     o[sp] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (sp < n_split) {
       const float* rec = ml + kSplitRec * sp;
       ml01[sp] = *reinterpret_cast<const float2*>(rec);
       ml23[sp] = *reinterpret_cast<const float2*>(rec + 2);
-      vg[sp] = rec[4];
+      ml45[sp] = *reinterpret_cast<const float2*>(rec + 4);
       o[sp] = po[int64_t(sp) * V4];
     }
   }
@@ -1124,7 +1147,7 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
   for (int sp = 0; sp < SPM; ++sp) mx = fmaxf(mx, ml01[sp].x);
   const float ms = mx == -INFINITY ? 0.0f : mx;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  float l = 0.f, l2 = 0.f, a = 0.f, b = 0.f;
+  float l = 0.f, l2 = 0.f, a = 0.f, b = 0.f, rk = 0.f;
 #pragma unroll
   for (int sp = 0; sp < SPM; ++sp) {
     const float w = sp < n_split ? exp2_raw(ml01[sp].x - ms) : 0.f;  // the missing splits' partials are zeros
@@ -1136,7 +1159,8 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
     if (ml01[sp].y > 0.f) {  // splits that saw keys (the others' records are not written)
       l2 += ml23[sp].x * w * w;
       a = fmaxf(a, ml23[sp].y);
-      b = fmaxf(b, vg[sp]);
+      b = fmaxf(b, ml45[sp].x);
+      rk = fmaxf(rk, ml45[sp].y);
     }
   }
   const float inv = 1.0f / l;
@@ -1147,7 +1171,7 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
   for (int m = 1; m < V4; m <<= 1) om = fmaxf(om, __shfl_xor(om, m, 64));  // over the row's V4 lanes
   const float om2 = om * om;
   const float est = l2 * inv * inv * (a * (b + om2) + est_c2 * (3.f * b + 2.f * om2));
-  if (c4 == 0 && l > 0.f && !(est <= 1.0f)) {
+  if (c4 == 0 && l > 0.f && !(sqrtf(est) + rk * (sqrtf(b) + om) <= 1.0f)) {
     const int64_t t = rh / n_heads;
     const int head = int(rh % n_heads), g = head / group;
     const int64_t p = t * group + head % group;
@@ -1197,6 +1221,16 @@ int64_t nbhs_prefill_aux_words(int64_t n, int64_t n_heads, int64_t n_kv_heads) {
   if (n <= 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0) return -1;
   const int64_t tiles = (n * (n_heads / n_kv_heads) + kRowsPerBlock - 1) / kRowsPerBlock;
   return kAuxHead + 3 * tiles * n_kv_heads;
+}
+
+int64_t nbhs_prefill_aux_words_bound(int64_t max_rows, int64_t n_heads) {
+  if (max_rows <= 0 || n_heads <= 0) return -1;
+  // n_kv ceil(m G / 128) tiles, G = n_heads / n_kv: not monotone in n_kv (the rounding), so every divisor is tried;
+  // it is monotone in m
+  int64_t words = 0;
+  for (int64_t kv = 1; kv <= n_heads; ++kv)
+    if (n_heads % kv == 0) words = std::max(words, nbhs_prefill_aux_words(max_rows, n_heads, kv));
+  return words;
 }
 
 namespace {
@@ -1329,9 +1363,11 @@ int prefill_impl(const float* q, const void* k16, const void* vt16, float* out, 
   const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
   const int64_t off = fp32_rows * n_heads * head_dim;  // the MFMA rows start fp32_rows rows in
   const float2* kstats = stats_of(const_cast<void*>(vt16), staged_rows_pad, n_kv_heads, head_dim);
-  // error-estimate coefficients, with the acceptance test folded in: flag when var * Z^2 / budget^2 > 1
+  // error-estimate coefficients, with the acceptance test folded in: flag when
+  // sqrt(var * Z^2 / budget^2) + (ln2 / budget) |r| sqrt(K) (V + O) > 1
   const double u2 = kEstU * kEstU, zb = double(kEstZ) * kEstZ / (double(kEstBudget) * kEstBudget);
-  const float est_c1 = float(2.0 * kLn2 * kLn2 * (2.0 * u2 / 3.0) * zb), est_c2 = float(u2 / 3.0 * zb);
+  const float est_c1 = float(2.0 * kLn2 * kLn2 * (u2 / 3.0) * zb), est_c2 = float(u2 / 3.0 * zb);
+  const float est_c3 = float(kLn2 / kEstBudget);
   const float2* q_rope = reinterpret_cast<const float2*>(q_rope_cs);
   hipError_t e = nbhs_timing::launch(
       NBHS_K_PREFILL_MFMA, head_dim == 64 ? attn_prefill_kernel<64, KVT> : attn_prefill_kernel<128, KVT>,
@@ -1339,7 +1375,7 @@ int prefill_impl(const float* q, const void* k16, const void* vt16, float* out, 
       dim3(kWaves * 64), s, q + off, static_cast<const _Float16*>(k16), static_cast<const _Float16*>(vt16), out + off,
       n_mfma, pos0 + fp32_rows, int(n_heads), int(n_kv_heads), int(group), staged_rows_pad, int(tiles), qscale,
       q_rope, q_rope_neox, k_cache, v_cache, fp32_rows, int(fp32_sub), sp, ws_o, ws_ml, kstats, aux, int(aux_cap),
-      est_c1, est_c2);
+      est_c1, est_c2, est_c3);
   if (e != hipSuccess) return e;
   if (sp > 1) {
     const int64_t threads = n_mfma * n_heads * (head_dim / 4);

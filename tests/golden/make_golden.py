@@ -41,16 +41,29 @@ ATTN_CASES = [
     ("qwen_chunk", 40, 300, 14, 2, 64, 1.0),         # chunked prefill (pos0 > 0)
     ("tinyllama_decode", 1, 1792, 32, 4, 64, 1.0),   # config 3 first step
     ("llama_decode_2k", 1, 2047, 32, 8, 64, 1.0),    # config 4/5 shape, reduced context
-    ("llama_prefill_300", 300, 0, 32, 8, 64, 1.0),   # crosses the fp32/MFMA prefill split at 256
+    ("llama_prefill_300", 300, 0, 32, 8, 64, 1.0),   # crosses the fp32/MFMA prefill split at 128
     ("d128_prefill", 64, 200, 8, 2, 128, 1.0),
     # Large attention scores at prefill shapes (the reference's own large-q case, tests/test_ops.cpp:196-216, scales
-    # q by 30): rows on both sides of the 256-row fp32 prefix, a chunk deep into a long cache, head_dim 128, and a
+    # q by 30): rows on both sides of the 128-row fp32 prefix, a chunk deep into a long cache, head_dim 128, and a
     # short chunk whose keys the MFMA route splits over several workgroups.
     ("prefill_qscale30", 320, 0, 4, 2, 64, 30.0),
     ("prefill_qscale5_pos4096", 512, 4096, 32, 8, 64, 5.0),
     ("prefill_d128_qscale30", 300, 100, 8, 2, 128, 30.0),
     ("prefill_qscale2", 600, 0, 14, 2, 64, 2.0),
     ("chunk_qscale30_pos1024", 64, 1024, 32, 8, 64, 30.0),
+]
+
+# (name, n, pos0, H, KV, D, qscale, rank, vmix): K and V projected from shared low-rank hidden states, as in a
+# transformer (K = h Wk, V = h (vmix Wk + (1 - vmix) R), h of rank `rank` plus 10 % noise), with a random query per
+# row and head. K and V correlate, so an error in the query that every key of a row shares does not average out over
+# the keys. Chunks deep into a 4k cache (the MFMA route, key splits), Qwen and head_dim 128 shapes; "q05" keeps every
+# row tile on the MFMA route, "r1_q1" sends every tile to the split-operand recomputation.
+CORR_CASES = [
+    ("prefill_corr_r2_q05", 256, 3840, 32, 8, 64, 0.5, 2, 0.8),
+    ("prefill_corr_r8_q1", 256, 3840, 32, 8, 64, 1.0, 8, 0.6),
+    ("prefill_corr_r1_q1", 256, 3840, 32, 8, 64, 1.0, 1, 1.0),
+    ("prefill_corr_r2_qwen", 384, 1664, 14, 2, 64, 0.7, 2, 0.8),
+    ("prefill_corr_d128", 192, 1856, 8, 2, 128, 0.7, 2, 0.8),
 ]
 
 # (name, n, heads, hd, pos0, base, neox, llama3)
@@ -94,6 +107,26 @@ def attn_inputs(i, n, pos0, H, KV, D, qscale):
     return q.astype(np.float32), k, v
 
 
+def corr_inputs(i, n, pos0, H, KV, D, qscale, rank, vmix):
+    """q [n, H, D], k, v [pos0 + n, KV, D] of a CORR_CASES entry. The projections are exact int64 products of
+    quantised normals (hidden states x 256, weights x 4096 / sqrt(4 D)), scaled by a power of two and rounded once to
+    float32, so every machine regenerates the same bits whatever its BLAS."""
+    ctx, dm = pos0 + n, 4 * D
+
+    def ints(shape, tensor, scale):
+        return np.rint(synth.normal_array(shape, 902, i, tensor).astype(np.float64) * scale).astype(np.int64)
+
+    h = ints((ctx, rank), 1, 16) @ ints((rank, dm), 2, 16 / np.sqrt(rank)) + ints((ctx, dm), 3, 25.6)
+    ws = 4096 / np.sqrt(dm)
+    wk, r = ints((dm, KV * D), 4, ws), ints((dm, KV * D), 5, ws)
+    wv = np.rint(vmix * wk + (1 - vmix) * r).astype(np.int64)
+    sc = 1.0 / (256 * 4096)
+    k = ((h @ wk) * sc).astype(np.float32).reshape(ctx, KV, D)
+    v = ((h @ wv) * sc).astype(np.float32).reshape(ctx, KV, D)
+    q = (synth.normal_array((n, H, D), 902, i, 7).astype(np.float64) * qscale).astype(np.float32)
+    return q, k, v
+
+
 def rope_input(i, n, heads, hd):
     return synth.normal_array((n, heads, hd), 901, i, 1)
 
@@ -112,6 +145,13 @@ def main():
         if simd is None:
             sys.exit("the reference's SIMD tier is unavailable on this host; golden vectors need AVX2")
         put_output(out, f"attn/{name}/simd", simd)
+    for i, (name, n, pos0, H, KV, D, qs, rank, vmix) in enumerate(CORR_CASES):
+        q, k, v = corr_inputs(i, n, pos0, H, KV, D, qs, rank, vmix)
+        out[f"attn/{name}/shape"] = np.array([i, n, pos0, H, KV, D], np.int64)
+        out[f"attn/{name}/qscale"] = np.array([qs], np.float32)
+        out[f"attn/{name}/input_sha256"] = sha(q, k, v)
+        put_output(out, f"attn/{name}/scalar", oracle.ref_attention_scalar(q, k, v, pos0, KV))
+        put_output(out, f"attn/{name}/simd", oracle.ref_attention_simd(q, k, v, pos0, KV))
     for i, (name, n, heads, hd, pos0, base, neox, l3) in enumerate(ROPE_CASES):
         x = rope_input(i, n, heads, hd)
         ff = synth.llama3_freq_factors(hd, base) if l3 else None

@@ -90,7 +90,7 @@ def test_f16kv_rows_and_append(backend, n, pos0):
                          ids=["n300-pos0-0", "chunk512-pos0-4096", "n1024-qscale5", "n700-pos0-77"])
 def test_f16kv_prefill_mfma_route(backend, n, pos0, qscale):
     """Prefill over fp16 caches: calls of more than 16 rows take the MFMA route - fp16 cache rows staged unchanged,
-    rows below position 256 in fp32 from the fp16 cache, the error estimate and the split-operand recomputation (q
+    rows below position 128 in fp32 from the fp16 cache, the error estimate and the split-operand recomputation (q
     scaled by 5 makes the scores large enough to list row tiles). First attention_f16kv over given caches (q
     rotated) against the oracle over the fp16 values; then the same rows through append_rope_attention_f16kv (the
     append fused with the staging, q unrotated): appended rows bit-exact (fp16 of the reference's fp32 RoPE), rows

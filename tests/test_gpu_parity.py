@@ -141,6 +141,67 @@ def test_large_scores_through_fused_append(backend, case):
         assert recomputed > 0
 
 
+def corr_golden(case):
+    """Inputs of a correlated golden case, with the oracle's output checked against the reference's vector."""
+    name, n, pos0, H, KV, D, qs, rank, vmix = case
+    i = int(GOLD[f"attn/{name}/shape"][0])
+    q, k, v = make_golden.corr_inputs(i, n, pos0, H, KV, D, qs, rank, vmix)
+    assert np.array_equal(make_golden.sha(q, k, v), GOLD[f"attn/{name}/input_sha256"]), "inputs regenerated differ"
+    ref = oracle.attention_scalar(q, k, v, pos0, KV)
+    key = f"attn/{name}/scalar"
+    if key in GOLD.files:
+        assert np.array_equal(bits(ref), bits(GOLD[key]))
+    else:
+        assert np.array_equal(make_golden.sha(ref), GOLD[key + "_sha256"])
+    return q, k, v, ref
+
+
+# On prefill_corr_r2_q05 every row tile stays on the MFMA route. An exact CPU emulation of the kernel's rounding puts
+# its largest error at 8.6e-5 with the query split into fp16 high and low parts, and at 5.3e-4 with the query rounded
+# to fp16 once (K and V correlate, so that rounding, shared by the row's 4096 keys, adds up): the bound below tells
+# the two apart.
+CORR_MAX_ABS = {"prefill_corr_r2_q05": 2.5e-4}
+
+
+@pytest.mark.parametrize("case", make_golden.CORR_CASES, ids=[c[0] for c in make_golden.CORR_CASES])
+def test_attention_golden_correlated(backend, case):
+    """K and V projected from shared low-rank hidden states (reference vectors from the compiled reference), through
+    Backend::attention on the default route: within the parity tolerance, and on the all-MFMA case within the split
+    query's error level."""
+    name = case[0]
+    q, k, v, ref = corr_golden(case)
+    got = gpu_attention(backend, q, k, v, case[2], case[4])
+    p = assert_parity(got, ref, name)
+    if name in CORR_MAX_ABS:
+        assert p["max_abs"] <= CORR_MAX_ABS[name], p
+    if name.startswith("prefill_corr_r1"):
+        assert backend.prefill_recomputed() > 0
+
+
+@pytest.mark.parametrize("case", make_golden.CORR_CASES, ids=[c[0] for c in make_golden.CORR_CASES])
+def test_attention_golden_correlated_through_fused_append(backend, case):
+    """The correlated cases through append_rope_attention: the call's rows arrive as k_new / v_new and are rotated
+    (Llama-3 RoPE) into the cache, q is rotated on load; appended rows bit-exact, outputs within the parity tolerance
+    of the reference's attention over the rotated rows."""
+    name, n, pos0, H, KV, D = case[:6]
+    q, k, v, _ = corr_golden(case)
+    base, ff = 5e5, synth.llama3_freq_factors(D, 5e5)
+    kn, vn = np.ascontiguousarray(k[pos0:]), np.ascontiguousarray(v[pos0:])
+    ck0, cv0 = k.copy(), v.copy()
+    ck0[pos0:] = 0
+    cv0[pos0:] = 0
+    with Buffers(backend) as B:
+        dq, dkn, dvn = B.upload(q), B.upload(kn), B.upload(vn)
+        dk, dv, do = B.upload(ck0), B.upload(cv0), B.alloc(q.size)
+        backend.append_rope_attention(dq, dk, dv, dkn, dvn, do, n, pos0, H, KV, D, base, False, ff)
+        got = backend.download(do, q.shape)
+        gk, gv = backend.download(dk, k.shape), backend.download(dv, v.shape)
+    assert np.array_equal(bits(gk[pos0:]), bits(oracle.rope(kn.copy(), pos0, base, False, ff))), "appended K rows"
+    assert np.array_equal(bits(gv[pos0:]), bits(vn)), "appended V rows"
+    qr = oracle.rope(q.copy(), pos0, base, False, ff)
+    assert_parity(got, cpu_attention(qr, gk, gv, pos0, KV), f"{name} fused")
+
+
 @pytest.mark.parametrize("D", [2, 8, 13, 16, 24, 64, 128])
 @pytest.mark.parametrize("H,KV", [(4, 4), (6, 3), (8, 2), (14, 2), (32, 4), (16, 1)])
 def test_attention_head_shapes(backend, D, H, KV):
@@ -434,7 +495,7 @@ def test_reserve_covers_every_op_at_its_limits():
         be.copy(big, big.at(3), 2 * (1 << 20))      # moving down
         q, out = be.alloc(max_rows * H * D), be.alloc(max_rows * H * D)
         k, v = be.alloc(n_ctx * KV * D), be.alloc(n_ctx * KV * D)
-        for pos0 in range(0, n_ctx, max_rows):  # chunked prefill, rows >= 256 on the MFMA route
+        for pos0 in range(0, n_ctx, max_rows):  # chunked prefill, rows >= 128 on the MFMA route
             be.rope(q, max_rows, H, D, pos0, 5e5, False, synth.llama3_freq_factors(D, 5e5))
             be.attention(q, k, v, out, max_rows, pos0, H, KV, D)
         be.attention(q, k, v, out, 1, n_ctx - 1, H, KV, D)
@@ -442,6 +503,56 @@ def test_reserve_covers_every_op_at_its_limits():
         assert be.internal_bytes() == cap
         for p in (x, y, w16, big, q, out, k, v):
             be.free(p)
+    finally:
+        be.close()
+
+
+@pytest.mark.parametrize("max_rows,H,KV", [(200, 32, 32), (200, 32, 8), (100, 32, 32), (300, 14, 2), (129, 8, 1)])
+def test_reserve_covers_the_prefill_work_list_for_any_kv_heads(max_rows, H, KV):
+    """The prefill work list reserve() allocates serves calls of up to max_rows rows whatever the KV head count (one
+    word per row tile and KV head: n_kv ceil(n G / 128)); the shapes where one KV head is not the worst case (max_rows
+    * G not a multiple of 128) allocate nothing after reserve()."""
+    import nibble_amd
+
+    be = nibble_amd.HipBackend(0)
+    try:
+        D, n_ctx = 64, 1024
+        be.reserve(n_ctx, H, max_rows, H * D)
+        cap = be.internal_bytes()
+        q, out = be.alloc(max_rows * H * D), be.alloc(max_rows * H * D)
+        k, v = be.alloc(n_ctx * KV * D), be.alloc(n_ctx * KV * D)
+        be.fill_normal(q, max_rows * H * D, 3, 1.0)
+        be.fill_normal(k, n_ctx * KV * D, 4, 1.0)
+        be.fill_normal(v, n_ctx * KV * D, 5, 1.0)
+        for n, pos0 in [(max_rows, 128), (max_rows, n_ctx - max_rows), (max_rows // 2 + 17, 300)]:
+            be.attention(q, k, v, out, n, pos0, H, KV, D)
+        be.sync()
+        assert be.internal_bytes() == cap
+        for p_ in (q, out, k, v):
+            be.free(p_)
+    finally:
+        be.close()
+
+
+def test_rope_table_growing_within_the_slab_keeps_it():
+    """A RoPE table living in the slab reserve() sized (n_ctx x max_width / n_heads floats) that grows past n_ctx
+    but still fits the slab stays in it: no allocation, and the rotation at the new positions is bit-exact."""
+    import nibble_amd
+
+    be = nibble_amd.HipBackend(0)
+    try:
+        H, D, n_ctx = 8, 64, 1024
+        be.reserve(n_ctx, H, 64, 4 * H * D)  # the slab holds 4 n_ctx rows of a head_dim-64 table
+        cap = be.internal_bytes()
+        x = synth.normal_array((2, H, D), 7, 1)
+        with Buffers(be) as B:
+            for pos0 in (100, 1500, 3000):  # 1500 and 3000 grow the table, to 2048 and then 4096 rows
+                dx = B.upload(x)
+                be.rope(dx, 2, H, D, pos0, 1e4, False, None)
+                y = be.download(dx, x.shape)
+                assert np.array_equal(bits(y), bits(oracle.rope(x.copy(), pos0, 1e4, False, None))), pos0
+                be.sync()
+                assert be.internal_bytes() == cap, pos0
     finally:
         be.close()
 

@@ -61,6 +61,18 @@ def test_attention_restatement_reproduces_reference_vectors(case):
         assert matches_gold(f"attn/{name}/simd", oracle.attention_parallel(q, k, v, pos0, KV, threads=3))
 
 
+@pytest.mark.parametrize("case", make_golden.CORR_CASES, ids=[c[0] for c in make_golden.CORR_CASES])
+def test_attention_restatement_reproduces_reference_vectors_correlated(case):
+    """The correlated-K/V cases (K and V projected from shared low-rank hidden states)."""
+    name, n, pos0, H, KV, D, qs, rank, vmix = case
+    i = int(GOLD[f"attn/{name}/shape"][0])
+    q, k, v = make_golden.corr_inputs(i, n, pos0, H, KV, D, qs, rank, vmix)
+    assert np.array_equal(GOLD[f"attn/{name}/input_sha256"], sha(q, k, v)), "input generator drifted"
+    assert matches_gold(f"attn/{name}/scalar", oracle.attention_scalar(q, k, v, pos0, KV))
+    if oracle.have_avx2():
+        assert matches_gold(f"attn/{name}/simd", oracle.attention_parallel(q, k, v, pos0, KV, threads=8))
+
+
 @pytest.mark.parametrize("case", make_golden.ROPE_CASES, ids=[c[0] for c in make_golden.ROPE_CASES])
 def test_rope_restatement_reproduces_reference_vectors(case):
     name, n, heads, hd, pos0, base, neox, l3 = case

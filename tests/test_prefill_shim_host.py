@@ -1,5 +1,6 @@
 """Host-side argument checks of the MFMA prefill entry point of libnibble_hip.so, on the CPU: each case is rejected
-with NBHS_EINVAL before anything is launched (no GPU call is made here; the pointers are never dereferenced)."""
+with NBHS_EINVAL before anything is launched (no GPU call is made here; the pointers are never dereferenced). Also the
+host-side sizing helpers (work list bound, whole-row decode route)."""
 import ctypes
 
 import pytest
@@ -73,3 +74,23 @@ def test_decode_rows_route_shapes():
           (1, 24, 8, 96), (1, 256, 64, 128), (1, 8, 2, 128), (0, 32, 8, 64), (1, 30, 8, 64)]
     assert all(f(*a) == 1 for a in yes), [a for a in yes if f(*a) != 1]
     assert all(f(*a) == 0 for a in no), [a for a in no if f(*a) != 0]
+
+
+def test_work_list_bound_covers_every_kv_head_count():
+    """reserve() sizes the prefill work list with nbhs_prefill_aux_words_bound(max_rows, n_heads): it must cover
+    every call of up to max_rows rows for every KV head count dividing n_heads. One KV head is not the worst case
+    when max_rows * group is not a multiple of the 128-row tile (max_rows 100 with 32 / 32 heads needs 112 words,
+    one KV head gives 91)."""
+    L = ctypes.CDLL(nibble_amd.LIB_PATH)
+    words, bound = L.nbhs_prefill_aux_words, L.nbhs_prefill_aux_words_bound
+    words.restype = bound.restype = ctypes.c_int64
+    words.argtypes = [ctypes.c_int64] * 3
+    bound.argtypes = [ctypes.c_int64] * 2
+    assert words(100, 32, 1) == 91 and words(100, 32, 32) == 112  # the under-reservation a one-head bound made
+    for max_rows in (1, 17, 100, 127, 128, 129, 200, 300, 512, 1000):
+        for H in (1, 2, 7, 14, 24, 32, 40, 64):
+            b = bound(max_rows, H)
+            need = max(words(m, H, kv) for m in {1, max_rows // 2 + 1, max_rows} for kv in range(1, H + 1)
+                       if H % kv == 0)
+            assert b == need, (max_rows, H, b, need)
+    assert bound(0, 32) == -1 and bound(16, 0) == -1
