@@ -442,8 +442,10 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
   int64_t x_count;
   if (overflow_mul(n, in, &x_count)) throw Error("matmul: n x width overflows");
   check_range(x, x_count, "matmul", "x");
-  std::vector<DeviceWeight> dw;
-  dw.reserve(ws.size());
+  // Per-call lists live in member vectors that only grow: after the first call of a given weight count nothing
+  // here allocates (alloc_tests.cpp:278-337 counts every operator new of a warm matmul).
+  std::vector<DeviceWeight>& dw = mm_dw_;
+  dw.clear();
   const auto xa = reinterpret_cast<uintptr_t>(x);
   for (size_t i = 0; i < ws.size(); ++i) {
     dw.push_back(device_weight(*ws[i], "matmul"));
@@ -457,14 +459,11 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
   // Quantized weights (ref_ops.cpp:109-135): the weights of one type share one launch per chunk of up to 16
   // activation rows. Up to 4 rows are quantized inside that launch; more are quantized once per activation format
   // first, as CpuBackend::matmul_multi quantizes the shared input once (cpu_backend.cpp:146-240).
-  std::vector<size_t> fl;
-  std::vector<int> types;
+  std::vector<int>& types = mm_types_;
+  types.clear();
   for (size_t i = 0; i < dw.size(); ++i) {
     const int t = int(dw[i].type);
-    if (!nbh_quant::is_quant(t))
-      fl.push_back(i);
-    else if (std::find(types.begin(), types.end(), t) == types.end())
-      types.push_back(t);
+    if (nbh_quant::is_quant(t) && std::find(types.begin(), types.end(), t) == types.end()) types.push_back(t);
   }
   const bool fuse = n <= 4 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && in % 4 == 0;
   int done_act = -1;
@@ -483,7 +482,8 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
             "matmul (activation quantization)");
       done_act = act_key;
     }
-    std::vector<size_t> idx;
+    std::vector<size_t>& idx = mm_idx_;
+    idx.clear();
     for (size_t i = 0; i < dw.size(); ++i)
       if (int(dw[i].type) == t) idx.push_back(i);
     if (tiled) {  // up to 8 weights a launch
@@ -520,15 +520,15 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
       }
     }
   }
-  if (fl.size() != dw.size()) {
-    std::vector<DeviceWeight> fw;
-    std::vector<float*> fy;
-    for (size_t i : fl) fw.push_back(dw[i]), fy.push_back(ys[i]);
-    dw.swap(fw);
-    ys_float_.assign(fy.begin(), fy.end());
-  } else {
-    ys_float_.assign(ys.begin(), ys.end());
-  }
+  // the float weights and their outputs, compacted to the front of the lists
+  size_t nf = 0;
+  ys_float_.clear();
+  for (size_t i = 0; i < dw.size(); ++i)
+    if (!nbh_quant::is_quant(int(dw[i].type))) {
+      dw[nf++] = dw[i];
+      ys_float_.push_back(ys[i]);
+    }
+  dw.resize(nf);
   if (dw.empty()) return;
   const std::vector<float*>& yv = ys_float_;
   if (n <= kGemvMaxRows) {

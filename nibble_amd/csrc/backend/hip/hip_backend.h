@@ -205,7 +205,12 @@ class HipBackend final : public Backend {
   size_t ids_buf_bytes_ = 0;
   float* acts_buf_ = nullptr;  // activations quantized for quantized weights
   size_t acts_buf_bytes_ = 0;
-  std::vector<float*> ys_float_;  // outputs of a matmul_multi's float weights
+  // matmul_multi's per-call lists (reused, so a warm call allocates nothing): the call's device weights (then its
+  // float weights, compacted), their quantized types, one type's weight indices, the float weights' outputs
+  std::vector<DeviceWeight> mm_dw_;
+  std::vector<int> mm_types_;
+  std::vector<size_t> mm_idx_;
+  std::vector<float*> ys_float_;
 };
 
 }  // namespace nibble::hip

@@ -124,12 +124,25 @@ int nbh_backend_matmul_multi(nbh_backend* be, int64_t n_w, const nbh_tensor* con
                              float* const* ys, int64_t n) {
   return guarded([&] {
     if (n_w <= 0 || !ws || !ys) throw nibble::Error("matmul_multi: need n_w > 0 weights and outputs");
-    std::vector<nibble::Tensor> t;
-    t.reserve(size_t(n_w));
-    for (int64_t i = 0; i < n_w; ++i) t.push_back(tensor_of(ws[i]));
-    std::vector<const nibble::Tensor*> tp;
-    for (auto& x_ : t) tp.push_back(&x_);
-    B(be).matmul_multi(std::span<const nibble::Tensor* const>(tp), x, std::span<float* const>(ys, size_t(n_w)), n);
+    // The views on the stack for up to kStack weights (a layer's QKV or gate + up: nothing allocated per call).
+    constexpr int64_t kStack = 16;
+    nibble::Tensor ts[kStack];
+    const nibble::Tensor* tps[kStack];
+    std::vector<nibble::Tensor> tv;
+    std::vector<const nibble::Tensor*> tpv;
+    const nibble::Tensor** tp = tps;
+    if (n_w > kStack) {
+      tv.resize(size_t(n_w));
+      tpv.resize(size_t(n_w));
+      tp = tpv.data();
+    }
+    for (int64_t i = 0; i < n_w; ++i) {
+      nibble::Tensor& t = n_w > kStack ? tv[size_t(i)] : ts[i];
+      t = tensor_of(ws[i]);
+      tp[i] = &t;
+    }
+    B(be).matmul_multi(std::span<const nibble::Tensor* const>(tp, size_t(n_w)), x,
+                       std::span<float* const>(ys, size_t(n_w)), n);
   });
 }
 
