@@ -3,6 +3,8 @@ of, nbh_backend_attention on its decode route, through the C ABI. Both run the s
 (the split partials go to the library's static device array instead of the backend's workspace), so outputs must
 be bit-identical; they are also held to the parity tolerance of the oracle. Calls in a row, each with a smaller
 input than the one before, so each runs over the array the previous one left behind."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -51,5 +53,33 @@ def test_noalloc_decode_rejects_shapes_off_the_decode_route():
                 nibble_amd.attention_decode_noalloc(d, d, d, d, 17, 0, 8, 8, 64, be.stream_handle())
             with pytest.raises(nibble_amd.BackendError, match="invalid shape"):
                 nibble_amd.attention_decode_noalloc(d, d, d, d, 1, 0, 6, 4, 64, be.stream_handle())
+    finally:
+        be.close()
+
+
+def test_noalloc_decode_whole_row_shape_beyond_the_array():
+    """Llama-3-8B's decode shape (32 / 8 heads, head_dim 128) at 40000 positions qualifies for the whole-row kernel,
+    but its partials (32 heads x 256 workgroups x 130 floats) exceed the 4 MiB array: the entry point takes the
+    per-head split kernel instead, which nbh_backend_attention does not, so the outputs are held to the oracle's
+    tolerance rather than to bit-identity; nothing is allocated."""
+    n, pos0, H, KV, D = 1, 40000, 32, 8, 128
+    capacity = nibble_amd.lib().nbhs_attn_decode_noalloc_capacity
+    capacity.restype = ctypes.c_int64
+    assert capacity() < H * 256 * (D + 2)
+    be = nibble_amd.HipBackend(0)
+    try:
+        rng = np.random.default_rng(41)
+        q = rng.standard_normal((n, H, D)).astype(np.float32)
+        k = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+        v = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+        with Buffers(be) as B:
+            dq, dk, dv, do = B.upload(q), B.upload(k), B.upload(v), B.alloc(q.size)
+            be.write(do, np.full(q.size, np.nan, np.float32))
+            be.sync()
+            before = be.internal_bytes()
+            nibble_amd.attention_decode_noalloc(dq, dk, dv, do, n, pos0, H, KV, D, be.stream_handle())
+            got = be.download(do, q.shape)
+            assert be.internal_bytes() == before
+        assert_parity(got, cpu_attention(q, k, v, pos0, KV), "noalloc decode beyond the array")
     finally:
         be.close()
