@@ -181,6 +181,15 @@ int nbh_backend_silu_mul(nbh_backend* be, float* gate, const float* up, int64_t 
  * prefill rate (a debugging aid). */
 int nbh_backend_set_attention_fp32(nbh_backend* be, int on);
 
+/* Batch invariance switch. The reference's kernels give a row the same bits however tokens are batched into calls
+ * (its model tests demand it: tests/test_model.cpp:141-151, 253-263); this backend's default routes agree only
+ * within rounding (fp16-operand MFMA prefill, keys split over workgroups by the call's shape, rocBLAS for long float
+ * matmuls). on != 0: every attention row takes the ordered fp32 route (one workgroup per row over its whole window,
+ * keys in position order) and every float-weight matmul the gemv kernel, so batch, token-by-token and chunked
+ * evaluation agree bit for bit, at a much lower prefill rate (and a lower long-context decode rate: a row's keys are
+ * no longer split over workgroups). Quantized matmuls are bit-exact either way. */
+int nbh_backend_set_batch_invariant(nbh_backend* be, int on);
+
 /* Decode attention that allocates nothing. No counterpart in the reference: for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops). It is the decode route of
  * nbh_backend_attention (n <= 16 query rows; q already rotated; results bit-identical to that call, which takes the

@@ -119,6 +119,16 @@ int nbhs_attn_decode_f16kv(const float* q, const void* k16, const void* v16, flo
                            int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, float* workspace,
                            int64_t workspace_floats, int cu_count, const float* q_rope_cs, int64_t q_rope_rows,
                            int q_rope_neox, nbhs_stream s);
+/* The ordered route of nbhs_attn_decode_f32 / nbhs_attn_decode_f16kv: each query row (and head subgroup) in one
+ * workgroup over its whole window, key groups in position order - no split of the keys over workgroups and no
+ * whole-row kernel -, so a row's result depends on its own keys only: bitwise the same whichever call computes it,
+ * however rows are batched into calls. Any head_dim the other routes take; no workspace. */
+int nbhs_attn_decode_ordered_f32(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                                 int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const float* q_rope_cs,
+                                 int64_t q_rope_rows, int q_rope_neox, nbhs_stream s);
+int nbhs_attn_decode_ordered_f16kv(const float* q, const void* k16, const void* v16, float* out, int64_t n,
+                                   int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                   const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, nbhs_stream s);
 /* nbhs_append_attn_decode_f32 over fp16 caches: cache row pos0 receives fp16(rope(k_new)) and fp16(v_new) (rotated
  * in fp32 as the fp32 append does, then rounded to nearest even), and the attention uses the row as stored. */
 int nbhs_append_attn_decode_f16kv(const float* q, void* k16, void* v16, const float* k_new, const float* v_new,

@@ -59,6 +59,7 @@ _SIGNATURES = {
     "nbh_backend_add_bias": (c_int, [c_void_p, c_void_p, POINTER(NbhTensor), _I]),
     "nbh_backend_release_weights": (c_int, [c_void_p]),
     "nbh_backend_set_attention_fp32": (c_int, [c_void_p, c_int]),
+    "nbh_backend_set_batch_invariant": (c_int, [c_void_p, c_int]),
     "nbh_backend_prefill_recomputed": (c_int, [c_void_p, POINTER(c_int64)]),
     "nbh_backend_stream": (c_int, [c_void_p, POINTER(c_void_p)]),
     "nbh_attention_decode_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, _I, _I, _I, _I, _I, c_void_p]),
@@ -302,6 +303,11 @@ class HipBackend:
     def set_attention_fp32(self, on: bool):
         """Every attention row on the fp32 kernels (on) or the default fp16-operand MFMA prefill (off)."""
         _check(lib().nbh_backend_set_attention_fp32(self._h, int(bool(on))))
+
+    def set_batch_invariant(self, on: bool):
+        """Results bitwise independent of how rows are batched into calls (on): the ordered fp32 attention route and
+        the gemv kernel for every float matmul; off (default): the faster routes, equal within rounding."""
+        _check(lib().nbh_backend_set_batch_invariant(self._h, int(bool(on))))
 
     def stream_handle(self) -> int:
         """The hipStream_t (as an integer) the backend's ops run on."""

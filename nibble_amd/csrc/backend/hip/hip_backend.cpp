@@ -15,6 +15,8 @@ namespace {
 
 // Calls with at most this many query rows take the fp32 split-context kernel (decode, short appends).
 constexpr int64_t kDecodeMaxRows = NBHS_DECODE_MAX_ROWS;
+// Rows per launch of the ordered route (its grid holds one z index per row; a row's result is the same in any launch).
+constexpr int64_t kOrderedMaxRows = 32768;
 // Prefill rows at positions below this see so few keys that fp16 rounding of single V rows does not average out:
 // nearly all of them would be listed for recomputation, so they take the fp32 kernel in the MFMA launch. Rows from
 // here on take the MFMA kernel, whose rounding-error estimate lists the row tiles that need recomputing (at 128
@@ -550,10 +552,12 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
     return;
   }
   for (size_t i = 0; i < dw.size(); ++i) {
-    if (dw[i].type == DType::F16 && !dw[i].key) {
+    if ((dw[i].type == DType::F16 && !dw[i].key) || batch_invariant_) {
       // An F16 weight in a caller's buffer: its bytes may change between calls, so no fp32 widening is kept; the
-      // gemv kernel reads it as F16 in 16-row slices of x (no scratch, nothing allocated).
-      const int f16 = 1;
+      // gemv kernel reads it as F16 in 16-row slices of x (no scratch, nothing allocated). With batch invariance
+      // every float weight takes this route: the gemv computes each output from its own x row with one summation
+      // order whatever the rows per launch, so batching cannot change its bits.
+      const int f16 = dw[i].type == DType::F16 ? 1 : 0;
       const void* wp = dw[i].dev;
       const int64_t rows = dw[i].rows;
       for (int64_t t0 = 0; t0 < n; t0 += kGemvMaxRows) {
@@ -787,6 +791,15 @@ void HipBackend::append_rope_attention(const float* q, float* k_cache, float* v_
 void HipBackend::run_decode_f16kv(const float* q, const void* k16, const void* v16, float* out, int64_t n,
                                   int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
                                   const float* rope_table, int64_t rope_rows, bool neox, const char* op) {
+  if (batch_invariant_) {
+    const int64_t qw = n_heads * head_dim;
+    for (int64_t t0 = 0; t0 < n; t0 += kOrderedMaxRows)
+      check(nbhs_attn_decode_ordered_f16kv(q + t0 * qw, k16, v16, out + t0 * qw, std::min(kOrderedMaxRows, n - t0),
+                                           pos0 + t0, n_heads, n_kv_heads, head_dim, rope_table, rope_rows,
+                                           neox ? 1 : 0, stream_),
+            op);
+    return;
+  }
   // rows in groups the decode kernel's workspace bound covers, q rotated on load when a table is given
   for (int64_t t0 = 0; t0 < n; t0 += kDecodeMaxRows) {
     const int64_t rows = std::min<int64_t>(kDecodeMaxRows, n - t0);
@@ -805,8 +818,10 @@ void HipBackend::run_prefill_f16kv(const float* q, void* k16, void* v16, float* 
                                    int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const float* rope_table,
                                    int64_t rope_rows, bool neox, const float* k_new, const float* v_new,
                                    const char* op) {
-  // rows below kFp32PrefixRows (all rows with set_attention_fp32) take the fp32 kernel, as for fp32 caches
-  const int64_t split = attention_fp32_ ? n : std::clamp<int64_t>(kFp32PrefixRows - pos0, 0, n);
+  // rows below kFp32PrefixRows (all rows with set_attention_fp32 or batch invariance) take the fp32 kernel, as for
+  // fp32 caches
+  const int64_t split =
+      attention_fp32_ || batch_invariant_ ? n : std::clamp<int64_t>(kFp32PrefixRows - pos0, 0, n);
   if (split == n) {
     if (k_new)
       check(nbhs_append_rope_f16kv(k16, v16, k_new, v_new, n, pos0, n_kv_heads, head_dim, rope_table, rope_rows,
@@ -864,7 +879,7 @@ void HipBackend::append_rope_attention_f16kv(const float* q, void* k16, void* v1
   check_range(v_new, kvf, op, "v_new");
   int64_t rows;
   const float* table = rope_table(head_dim, pos0 + n, p, &rows);
-  if (n == 1) {  // decode step: the append rides in the attention launch
+  if (n == 1 && !batch_invariant_) {  // decode step: the append rides in the attention launch
     const int64_t ws = nbhs_attn_decode_workspace(1, pos0, n_heads, n_kv_heads, head_dim, cu_count_);
     if (ws < 0) throw Error(std::string(op) + ": invalid decode shape");
     ensure(decode_ws_, decode_ws_bytes_, size_t(ws) * sizeof(float));
@@ -918,7 +933,8 @@ void HipBackend::run_batch(int64_t n_seq, const float* const* q, const float* co
     }
     max_pos = std::max(max_pos, pos0[i]);
   }
-  if (head_dim != 64 && head_dim != 128) {  // no batch kernel for these sizes: one call per sequence
+  // no batch kernel for these sizes, and none on the ordered route: one call per sequence
+  if ((head_dim != 64 && head_dim != 128) || batch_invariant_) {
     for (int64_t i = 0; i < n_seq; ++i) {
       if (p)
         append_rope_attention(q[i], const_cast<float*>(k[i]), const_cast<float*>(v[i]), k_new[i], v_new[i], out[i],
@@ -983,6 +999,16 @@ void HipBackend::run_attention(const float* q, const float* k, const float* v, f
           "attention (append)");
   };
 
+  if (batch_invariant_) {  // every row on the ordered route: its result depends on its own keys only
+    if (app) append_kv();
+    const int64_t qw = n_heads * head_dim;
+    for (int64_t t0 = 0; t0 < n; t0 += kOrderedMaxRows)
+      check(nbhs_attn_decode_ordered_f32(q + t0 * qw, k, v, out + t0 * qw, std::min(kOrderedMaxRows, n - t0),
+                                         pos0 + t0, n_heads, n_kv_heads, head_dim, rope_table, rope_rows,
+                                         neox ? 1 : 0, stream_),
+            "attention (ordered route)");
+    return;
+  }
   const bool mfma_shape = head_dim == 64 || head_dim == 128;
   if (app && mfma_shape && n == 1) {  // decode step: the append rides in the attention launch
     const int64_t ws = nbhs_attn_decode_workspace(1, pos0, n_heads, n_kv_heads, head_dim, cu_count_);

@@ -110,6 +110,15 @@ class HipBackend final : public Backend {
   // split-context kernel, as decode does: the reference's float arithmetic throughout, at a much lower prefill
   // rate. For models whose attention scores are large enough that fp16 rounding of Q and K moves the softmax.
   void set_attention_fp32(bool on) { attention_fp32_ = on; }
+  // Batch invariance: the reference's CPU kernels compute each row with a fixed accumulation order, so how tokens
+  // are batched into calls cannot change a bit (its model tests demand it: test_model.cpp:141-151, 253-263). By
+  // default this backend trades that for speed (prefill rows on fp16-operand MFMA, keys split over workgroups by
+  // the call's shape, rocBLAS for long float matmuls): results agree within rounding. With batch invariance on,
+  // every attention row takes the ordered fp32 route (one workgroup per row over its whole window, keys in position
+  // order) and float-weight matmuls of any row count the gemv kernel (16-row slices), so each row's results are
+  // bitwise the same however rows are batched - at a much lower prefill rate and a lower decode rate.
+  void set_batch_invariant(bool on) { batch_invariant_ = on; }
+  bool batch_invariant() const { return batch_invariant_; }
   // Row tiles (128 packed query rows x one KV head) the last MFMA prefill call recomputed with split fp16 operands
   // because their rounding-error estimate exceeded the budget. Waits for queued work.
   int64_t prefill_recomputed();
@@ -201,6 +210,7 @@ class HipBackend final : public Backend {
   std::map<const void*, DeviceWeight> weights_;  // host weight data -> its device form
   nbhs_blas blas_ = nullptr;
   bool attention_fp32_ = false;
+  bool batch_invariant_ = false;
   float* ids_buf_ = nullptr;  // token ids of the last embed, on the device
   size_t ids_buf_bytes_ = 0;
   float* acts_buf_ = nullptr;  // activations quantized for quantized weights

@@ -173,6 +173,10 @@ int nbh_backend_set_attention_fp32(nbh_backend* be, int on) {
   return guarded([&] { B(be).set_attention_fp32(on != 0); });
 }
 
+int nbh_backend_set_batch_invariant(nbh_backend* be, int on) {
+  return guarded([&] { B(be).set_batch_invariant(on != 0); });
+}
+
 int nbh_attention_decode_noalloc(const float* q, const float* k, const float* v, float* out, int64_t n,
                                  int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, void* stream) {
   return guarded([&] {

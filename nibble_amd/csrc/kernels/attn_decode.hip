@@ -171,8 +171,12 @@ int resident_per_cu(int64_t head_dim, int gb) {
 // evenly over min(slots, groups) chunks; the remainder goes one group each to the first chunks, which load that
 // group together with their first one (see attn_decode_partial), so a context one row past a round size costs no
 // workgroup an extra HBM round trip and no workgroup waits for a free slot.
+//
+// single_chunk: every (row, head subgroup) in one workgroup over its whole window, key groups in position order (the
+// ordered route): a row's summation then depends on its own keys only, not on the call's other rows or its length.
 template <typename KV = float>
-Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t head_dim, int cu_count) {
+Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t head_dim, int cu_count,
+               bool single_chunk = false) {
   const int unroll = unroll_for(int(sizeof(KV)));
   Plan p;
   const int64_t group = n_heads / n_kv;
@@ -188,7 +192,7 @@ Plan make_plan(int64_t n, int64_t pos0, int64_t n_heads, int64_t n_kv, int64_t h
   int64_t slots = cus * resident / streams;
   if (resident > NBH_DECODE_WG_PER_CU && units < kLongGroups * slots)
     slots = cus * NBH_DECODE_WG_PER_CU / streams;  // short context: fewer, longer workgroups
-  if (slots < 1) slots = 1;
+  if (slots < 1 || single_chunk) slots = 1;
   int64_t chunks = units < slots ? units : slots;
   if (chunks > kMaxChunks) chunks = kMaxChunks;
   p.n_chunks = int(chunks);
@@ -315,7 +319,7 @@ template <typename KVT>
 int decode(const float* q, const KVT* k, const KVT* v, float* out, int64_t n, int64_t pos0, int64_t n_heads,
            int64_t n_kv_heads, int64_t head_dim, float* workspace, int64_t workspace_floats, int cu_count,
            const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox, const Append<KVT>& app, hipStream_t s,
-           bool allow_rows = true) {
+           bool allow_rows = true, bool single_chunk = false) {
   if (!q || !k || !v || !out || n <= 0 || n > 65535 || pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 ||
       n_heads % n_kv_heads != 0 || head_dim <= 0 || head_dim > 256 || n_heads > 65535)
     return NBHS_EINVAL;
@@ -331,7 +335,7 @@ int decode(const float* q, const KVT* k, const KVT* v, float* out, int64_t n, in
                                  k, v, out, pos0, int(n_heads), int(n_kv_heads), int(head_dim), qscale);
     }
   }
-  if (allow_rows && rows_route(n, n_heads, n_kv_heads, head_dim) && pos0 < kRowsMaxPos) {
+  if (allow_rows && !single_chunk && rows_route(n, n_heads, n_kv_heads, head_dim) && pos0 < kRowsMaxPos) {
     const int64_t G = rows_grid<KVT>(pos0, n_kv_heads, head_dim, cu_count);
     const int64_t need = G == 1 ? 0 : n_heads * G * (head_dim + 2);
     if (need > 0 && (!workspace || workspace_floats < need)) return NBHS_EINVAL;
@@ -342,7 +346,7 @@ int decode(const float* q, const KVT* k, const KVT* v, float* out, int64_t n, in
                             s);
   }
   // (nbhs_attn_decode_workspace covers the plans of both cache types)
-  const Plan p = make_plan<KVT>(n, pos0, n_heads, n_kv_heads, head_dim, cu_count);
+  const Plan p = make_plan<KVT>(n, pos0, n_heads, n_kv_heads, head_dim, cu_count, single_chunk);
   const int64_t need = p.n_chunks == 1 ? 0 : n * n_heads * p.n_chunks * (head_dim + 2);
   if (need > 0 && (!workspace || workspace_floats < need)) return NBHS_EINVAL;
   if (n_kv_heads * p.n_sub > 65535) return NBHS_EINVAL;
@@ -618,6 +622,22 @@ int nbhs_attn_decode_f16kv(const float* q, const void* k16, const void* v16, flo
   return decode(q, static_cast<const _Float16*>(k16), static_cast<const _Float16*>(v16), out, n, pos0, n_heads,
                 n_kv_heads, head_dim, workspace, workspace_floats, cu_count, q_rope_cs, q_rope_rows, q_rope_neox,
                 Append<_Float16>{}, reinterpret_cast<hipStream_t>(stream));
+}
+
+int nbhs_attn_decode_ordered_f32(const float* q, const float* k, const float* v, float* out, int64_t n, int64_t pos0,
+                                 int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const float* q_rope_cs,
+                                 int64_t q_rope_rows, int q_rope_neox, nbhs_stream stream) {
+  return decode(q, k, v, out, n, pos0, n_heads, n_kv_heads, head_dim, nullptr, 0, 0, q_rope_cs, q_rope_rows,
+                q_rope_neox, Append<float>{}, reinterpret_cast<hipStream_t>(stream), false, true);
+}
+
+int nbhs_attn_decode_ordered_f16kv(const float* q, const void* k16, const void* v16, float* out, int64_t n,
+                                   int64_t pos0, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                   const float* q_rope_cs, int64_t q_rope_rows, int q_rope_neox,
+                                   nbhs_stream stream) {
+  return decode(q, static_cast<const _Float16*>(k16), static_cast<const _Float16*>(v16), out, n, pos0, n_heads,
+                n_kv_heads, head_dim, nullptr, 0, 0, q_rope_cs, q_rope_rows, q_rope_neox, Append<_Float16>{},
+                reinterpret_cast<hipStream_t>(stream), false, true);
 }
 
 int nbhs_append_attn_decode_f32(const float* q, float* k_cache, float* v_cache, const float* k_new,

@@ -10,7 +10,8 @@ there the bar is 1e-3 relative to the logits' largest magnitude, the attention t
 the affected row tiles to the split-operand recomputation, and the forward meets the reference's own float bar.
 
 Chunking: the reference demands bitwise equality of batch, incremental and 2-token-chunk runs
-(test_model.cpp:141-151); this backend's kernels split work by shape, so chunked runs agree within tolerance.
+(test_model.cpp:141-151); this backend's default kernels split work by shape, so chunked runs agree within tolerance
+here. Its batch-invariant mode restores the reference's bitwise guarantee (tests/test_gpu_batch_invariant.py).
 """
 import numpy as np
 import pytest
