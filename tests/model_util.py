@@ -134,3 +134,49 @@ class GpuModel:
             self.be.free(p)
         self.bufs.clear()
         self.be.release_weights()
+
+
+def write_model_dir(m, path):
+    """Writes model m for tests/ref_transformer_driver.cpp: model.txt (the LlamaConfig fields and one line per tensor)
+    and weights.bin (every tensor's bytes, 64-byte aligned). Matrices are [in, out] Tensors (ne[0] = input width) of
+    their array's type (F32, F16, or a quantized QMat's raw blocks); norms, biases and rope_freqs are F32 vectors."""
+    import os
+
+    E, H, KV, HD, FF, V = _dims(m)
+    blobs, lines, off = [], [], 0
+
+    def add(name, a):
+        nonlocal off
+        if hasattr(a, "raw"):  # tests.quant_util.QMat
+            t, data, dims, ne0, ne1 = a.t, a.raw.tobytes(), 2, a.cols, a.rows
+        else:
+            a = np.ascontiguousarray(a)
+            t = {np.dtype(np.float32): 0, np.dtype(np.float16): 1}[a.dtype]
+            data, dims = a.tobytes(), a.ndim
+            ne0, ne1 = a.shape[-1], (a.shape[0] if a.ndim == 2 else 1)
+        pad = (-off) % 64
+        blobs.append(b"\0" * pad + data)
+        off += pad
+        lines.append(f"tensor {name} {t} {dims} {ne0} {ne1} {off} {len(data)}")
+        off += len(data)
+
+    add("token_embd", m["token_embd"])
+    add("output_norm", m["output_norm"])
+    if m["output"] is not None:
+        add("output", m["output"])
+    if m["rope_freqs"] is not None:
+        add("rope_freqs", m["rope_freqs"])
+    for i, L in enumerate(m["layers"]):
+        for k in ("attn_norm", "wq", "wk", "wv", "wo", "ffn_norm", "w_gate", "w_up", "w_down", "bq", "bk", "bv"):
+            if k in L:
+                add(f"blk.{i}.{k}", L[k])
+    qwen = m["arch"] == "qwen2"
+    cfg = [f"arch {m['arch']}", f"n_layers {len(m['layers'])}", f"n_embd {E}", f"n_ff {FF}", f"n_heads {H}",
+           f"n_kv_heads {KV}", f"head_dim {HD}", f"n_vocab {V}", f"rope_base {m['base']!r}", f"rms_eps {m['eps']!r}",
+           f"rope_neox {int(qwen)}", f"qkv_bias {int('bq' in m['layers'][0])}"]
+    os.makedirs(path, exist_ok=True)
+    with open(os.path.join(path, "model.txt"), "w") as f:
+        f.write("\n".join(cfg + lines) + "\n")
+    with open(os.path.join(path, "weights.bin"), "wb") as f:
+        for b in blobs:
+            f.write(b)
