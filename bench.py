@@ -316,8 +316,9 @@ def qkv_projection(be, steps, warmup, chunk=512, chunk_reps=3):
     """The QKV projection feeding the attention path (transformer.cpp:171-194) at the Llama-3.2-1B shape: F16
     weights wq [2048, 2048], wk and wv [512, 2048] per layer, 16 layers, one matmul_multi per layer writing q and the
     new K/V cache rows. Decode: one token per step (the gemv route: weight bytes streamed once per layer);
-    prefill: chunks of `chunk` rows (the GEMM route: rocBLAS sgemm on the fp32 widening of each weight). Weights
-    start in host memory and are copied to HBM on the first (untimed) call, as a model's are."""
+    prefill: chunks of `chunk` rows (the F16 GEMM route: each activation row split into fp16 hi + lo parts by one
+    launch, then the three weights in one MFMA GEMM launch, fp32-grade results). Weights start in host memory and
+    are copied to HBM on the first (untimed) call, as a model's are."""
     shape = configs.LLAMA32_1B
     E, Q, kvw, NL = shape.n_embd, shape.n_heads * shape.head_dim, shape.n_kv_heads * shape.head_dim, 16
     rng = np.random.default_rng(17)
@@ -357,18 +358,30 @@ def qkv_projection(be, steps, warmup, chunk=512, chunk_reps=3):
     gemv_us = gemv_ms / gemv_n * 1e3
     gemv_gbs = alg_bytes / (gemv_us * 1e-6) / 1e9
     for r in range(2):
-        step(0, chunk)  # first GEMM call widens the F16 weights once; rocBLAS loads its kernels
+        step(0, chunk)  # the first GEMM calls load the kernels' code
     be.sync()
     pre_ms = timed(lambda r: step(0, chunk), chunk_reps)
     flops = 2 * chunk * E * (Q + 2 * kvw)
     pre_tflops = NL * chunk_reps * flops / (pre_ms * 1e-3) / 1e12
+    KernelTiming.enable(True, only=KernelTiming.GEMM)
+    timed(lambda r: step(0, chunk), chunk_reps)
+    be.sync()
+    gemm_ms, gemm_n = KernelTiming.read(KernelTiming.GEMM)
+    KernelTiming.enable(True, only=KernelTiming.SPLIT_ACTS)
+    timed(lambda r: step(0, chunk), chunk_reps)
+    be.sync()
+    split_ms, split_n = KernelTiming.read(KernelTiming.SPLIT_ACTS)
+    KernelTiming.enable(False)
+    gemm_us, split_us = gemm_ms / max(gemm_n, 1) * 1e3, split_ms / max(split_n, 1) * 1e3
+    gemm_tflops = flops / (gemm_us * 1e-6) / 1e12
     for p in [x, q] + kc + vc:
         be.free(p)
     be.release_weights()
     log(f"qkv projection: decode {dec_ms / steps * 1e3:.1f} us/step over {NL} layers -> {dec_gbs:.0f} GB/s; gemv "
         f"kernel {gemv_us:.2f} us -> {gemv_gbs:.0f} GB/s ({gemv_gbs / HBM_PEAK_GBS:.1%}); prefill chunk {chunk}: "
-        f"{pre_ms / chunk_reps / NL * 1e3:.1f} us/layer -> {pre_tflops:.1f} TFLOP/s "
-        f"({pre_tflops / FP32_PEAK_TFLOPS:.1%} of fp32)")
+        f"{pre_ms / chunk_reps / NL * 1e3:.1f} us/layer -> {pre_tflops:.1f} TFLOP/s; F16 GEMM kernel {gemm_us:.2f} us "
+        f"-> {gemm_tflops:.1f} TFLOP/s ({gemm_tflops / MFMA_F16_PEAK_TFLOPS:.1%} of fp16 MFMA; two MFMA products per "
+        f"multiply-add), activation split {split_us:.2f} us")
     return {"metric": "QKV projection (matmul_multi, F16 weights, llama-3.2-1b shape, 16 layers)",
             "decode": {"value": round(dec_gbs, 1), "unit": "GB/s", "us_per_step": round(dec_ms / steps * 1e3, 2),
                        "steps": steps, "roofline": {"bound": "hbm", "kernel": "gemv_kernel",
@@ -379,7 +392,16 @@ def qkv_projection(be, steps, warmup, chunk=512, chunk_reps=3):
             "prefill_chunk": {"rows": chunk, "value": round(pre_tflops, 2), "unit": "TFLOP/s",
                               "us_per_layer": round(pre_ms / chunk_reps / NL * 1e3, 2),
                               "frac_of_fp32_peak": round(pre_tflops / FP32_PEAK_TFLOPS, 4),
-                              "note": "rocBLAS sgemm x3 per layer on fp32-widened weights (fp32 math)"}}
+                              "roofline": {"bound": "mfma", "kernel": "gemm_f16w_kernel",
+                                           "achieved": round(gemm_tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                                           "unit": "TFLOP/s", "frac": round(gemm_tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                                           "avg_launch_us": round(gemm_us, 3), "launches": gemm_n,
+                                           "algorithmic_flops_per_launch": flops,
+                                           "mfma_flops_per_launch": 2 * flops},
+                              "split_acts_us": round(split_us, 3),
+                              "note": "per layer: one activation-split launch (fp16 hi + lo per row, power-of-two "
+                                      "row scale) and one F16-weight MFMA GEMM launch for wq, wk, wv (fp32-grade "
+                                      "results; no fp32 copy of the weights)"}}
 
 
 QUANT_NAMES = {2: "Q4_0", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}

@@ -252,6 +252,18 @@ int nbhs_blas_destroy(nbhs_blas h);
  * product as nbhs_gemv_multi, for any n. */
 int nbhs_sgemm_xwt(nbhs_blas h, const float* x, const float* w, float* y, int64_t n, int64_t in, int64_t out);
 
+/* F16 weights on the fp16 MFMA pipes for any n (prefill chunks), up to NBHS_GEMM_MAX_WEIGHTS weights sharing x in
+ * one launch: y[i][t * rows[i] + r] = sum_k x[t * in + k] * w[i][r * in + k], as nbhs_gemv_multi. Each activation
+ * row is scaled by a power of two and split into fp16 hi + lo parts (x s = hi + lo to ~2^-22 relative); both are
+ * multiplied by the exact fp16 weights with fp32 accumulation, so the result is fp32-grade (within the float
+ * summation bound of the reference's sum). ws: device scratch of nbhs_gemm_f16w_workspace(n, in) bytes, 256-byte
+ * aligned (the split rows). Requires in % 8 == 0 and 16-byte aligned weights; each launch is deterministic and
+ * a weight's outputs do not depend on the other weights of the call. */
+#define NBHS_GEMM_MAX_WEIGHTS 8
+int64_t nbhs_gemm_f16w_workspace(int64_t n, int64_t in);
+int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const int64_t* rows, int64_t in,
+                         const float* x, int64_t n, void* ws, int64_t ws_bytes, nbhs_stream s);
+
 /* ---- the other per-token ops (Backend::embed / rmsnorm / add / silu_mul, backend.h:55-70) ---- */
 
 /* out[t, :] = row ids[t] of table [rows, d] (F32, or F16 widened exactly); ids in device memory, already checked
@@ -313,7 +325,9 @@ enum nbhs_kernel_id {
   NBHS_K_QGEMM = 14,
   NBHS_K_PREFILL_PRECISE = 15, /* split-operand recomputation of listed prefill row tiles */
   NBHS_K_CALIBRATION = 16,     /* nbhs_mfma_loop_f16 */
-  NBHS_K_COUNT = 17
+  NBHS_K_SPLIT_ACTS = 17,      /* activation rows split into fp16 hi + lo for the F16-weight GEMM */
+  NBHS_K_GEMM = 18,            /* F16-weight GEMM (nbhs_gemm_f16w_multi) */
+  NBHS_K_COUNT = 19
 };
 int nbhs_kernel_timing_enable(int on); /* on != 0: time every kernel; 0: none (clears what was recorded) */
 int nbhs_kernel_timing_select(uint32_t kernel_mask); /* time the kernels whose bit (1 << id) is set; clears */

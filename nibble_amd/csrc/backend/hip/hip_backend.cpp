@@ -15,6 +15,7 @@ namespace {
 
 // Calls with at most this many query rows take the fp32 split-context kernel (decode, short appends).
 constexpr int64_t kDecodeMaxRows = NBHS_DECODE_MAX_ROWS;
+constexpr size_t kGemmMaxWeights = NBHS_GEMM_MAX_WEIGHTS;
 // Rows per launch of the ordered route (its grid holds one z index per row; a row's result is the same in any launch).
 constexpr int64_t kOrderedMaxRows = 32768;
 // Prefill rows at positions below this see so few keys that fp16 rounding of single V rows does not average out:
@@ -170,6 +171,13 @@ void HipBackend::reserve(const ReserveParams& rp) {
         acts = std::max(acts, b);
       }
     }
+  // The F16-weight GEMM's split activations share that buffer: max_rows rows of width up to max_width.
+  if (rp.max_rows > 0 && rp.max_width > 0) {
+    const int64_t g = nbhs_gemm_f16w_workspace(rp.max_rows, rp.max_width);
+    if (g < 0) throw Error("reserve: GEMM scratch for max_rows=" + str(rp.max_rows) + " max_width=" +
+                           str(rp.max_width) + " is too large");
+    acts = std::max(acts, g);
+  }
   // fp16 prefill staging for up to n_ctx rows. A cache row holds n_kv_heads * head_dim <= n_heads * head_dim <=
   // max_width floats (max_width is at least n_heads * head_dim, backend.h:22-23); the MFMA route's head_dim is at
   // least 64, so n_kv_heads <= max_width / 64 bounds the per-head tile statistics too.
@@ -550,6 +558,43 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
       check(nbhs_gemv_multi(int(cnt), f16, wp, yp, rows, in, x, n, stream_), "matmul (gemv)");
     }
     return;
+  }
+  // F16 weights on the fp16 MFMA GEMM (split activations, fp32-grade results, no fp32 copy of the weight): up to
+  // eight per launch, sharing one split of x. Its scratch is the activation buffer (stream order keeps the
+  // quantized launches above, which read that buffer, ahead of the split that overwrites it).
+  if (!batch_invariant_ && in % 8 == 0) {
+    size_t ng = 0;
+    for (size_t i = 0; i < dw.size(); ++i)
+      if (dw[i].type == DType::F16 && reinterpret_cast<uintptr_t>(dw[i].dev) % 16 == 0) ++ng;
+    if (ng > 0) {
+      const int64_t ws = nbhs_gemm_f16w_workspace(n, in);
+      if (ws < 0) throw Error("matmul: invalid GEMM shape n=" + str(n) + " in=" + str(in));
+      ensure(acts_buf_, acts_buf_bytes_, size_t(ws));
+      const void* wp[kGemmMaxWeights];
+      float* yp[kGemmMaxWeights];
+      int64_t rows[kGemmMaxWeights];
+      size_t cnt = 0, kept = 0;
+      auto flush = [&]() {
+        if (cnt == 0) return;
+        check(nbhs_gemm_f16w_multi(int(cnt), wp, yp, rows, in, x, n, acts_buf_, int64_t(acts_buf_bytes_), stream_),
+              "matmul (f16 GEMM)");
+        cnt = 0;
+      };
+      for (size_t i = 0; i < dw.size(); ++i) {
+        if (dw[i].type == DType::F16 && reinterpret_cast<uintptr_t>(dw[i].dev) % 16 == 0) {
+          wp[cnt] = dw[i].dev;
+          yp[cnt] = yv[i];
+          rows[cnt] = dw[i].rows;
+          if (++cnt == kGemmMaxWeights) flush();
+        } else {  // the other weights stay for the routes below
+          dw[kept] = dw[i];
+          ys_float_[kept++] = yv[i];
+        }
+      }
+      flush();
+      dw.resize(kept);
+      ys_float_.resize(kept);
+    }
   }
   for (size_t i = 0; i < dw.size(); ++i) {
     if ((dw[i].type == DType::F16 && !dw[i].key) || batch_invariant_) {

@@ -8,8 +8,9 @@
 //  * Decode and short appends (n <= 16 rows) are HBM-bound on the weights: gemv_kernel streams every weight row once
 //    (one wave per output row, 16-byte loads, f16 weights read as f16) and keeps up to 16 rows' dot products in
 //    registers; all the weights of a matmul_multi share one launch over their stacked output rows.
-//  * Longer calls (prefill chunks) are plain GEMMs and go to rocBLAS sgemm on an fp32 copy of the weight (an f16
-//    weight widens exactly), so products and sums stay fp32.
+//  * Longer calls (prefill chunks) are GEMMs. F16 weights take the split-activation MFMA GEMM of kernels/gemm.hip;
+//    F32 weights, and F16 ones whose width is not a multiple of 8, go to rocBLAS sgemm (on an fp32 copy of an F16
+//    weight, which widens exactly), so products and sums stay fp32.
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 

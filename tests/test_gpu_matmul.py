@@ -1,8 +1,9 @@
 """GPU parity of the QKV projection (Backend::matmul / matmul_multi / add_bias) against the CPU oracle.
 
 The reference's float matmul (ref_ops.cpp:109-135) accumulates each dot product left to right in float; the GPU
-sums the same float products in another order (lane partials and a wave tree on the gemv route, rocBLAS's blocking
-on the GEMM route). Both stay within the classical bound for float summation of the same terms, so the test bound
+sums the same float products in another order (lane partials and a wave tree on the gemv route; on the F16-weight
+GEMM route each activation row is scaled by a power of two and split into fp16 hi + lo parts whose exact products
+with the fp16 weights accumulate in fp32 on MFMA; rocBLAS sgemm's blocking for F32 weights). Both stay within the classical bound for float summation of the same terms, so the test bound
 is, per output element,
     |gpu - exact| <= in * 2^-24 * sum_k |x_k w_k|      (exact = fp64 product of the same float inputs)
     |gpu - ref|   <= 2 * in * 2^-24 * sum_k |x_k w_k|  (ref = the restated reference, bit-exact to it on the CPU)
@@ -53,9 +54,11 @@ def gpu_matmul(be, w, x, n):
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16], ids=["f32", "f16"])
 @pytest.mark.parametrize("in_out", [(256, 96), (200, 40), (100, 33)], ids=["256x96", "200x40", "100x33-unaligned"])
-@pytest.mark.parametrize("n", [1, 2, 7, 16, 17, 64])
+@pytest.mark.parametrize("n", [1, 2, 7, 16, 17, 64, 65, 200])
 def test_matmul_matches_reference(backend, dtype, in_out, n):
-    """Both routes (gemv for n <= 16, GEMM above) and both weight types, aligned (in % 8 == 0) and not."""
+    """Both routes (gemv for n <= 16, GEMM above) and both weight types, aligned (in % 8 == 0) and not; partial
+    row, output and K tiles of the F16 GEMM (64 x 64 tiles, 64-deep slices: in 200 ends mid-slice, in 100 is not a
+    multiple of 8 and takes the fp32 route)."""
     in_, out_ = in_out
     rng = np.random.default_rng(1000 * n + in_ + out_)
     w = rand(rng, (out_, in_), dtype, 0.5)
@@ -115,9 +118,8 @@ def test_qkv_projection_into_cache_rows(backend, shape, n):
 @pytest.mark.parametrize("n", [3, 16, 40, 512])
 def test_device_resident_weights_match_host_weights(backend, n):
     """Weights inside a buffer from alloc() are used in place. F32 ones run the same kernels on the same bytes as
-    host weights, so the same bits. An F16 one is never widened into a scratch buffer (its bytes may change between
-    calls, and a per-call widening would allocate): it always takes the gemv route, in 16-row slices of x, so above
-    16 rows it matches the host weight's GEMM route within the summation bound rather than bitwise."""
+    host weights, so the same bits; so do F16 ones, the gemv for n <= 16 and the F16 GEMM above (which reads the
+    weight as fp16, so an in-place weight needs no widened copy)."""
     rng = np.random.default_rng(77 + n)
     in_, out_ = 256, 72
     w32 = rand(rng, (out_, in_), np.float32, 0.3)
@@ -134,18 +136,18 @@ def test_device_resident_weights_match_host_weights(backend, n):
         backend.matmul(dw16, dx, y[3], n, shape=w16.shape, dtype=nibble_amd.F16)
         got = [backend.download(p, (n, out_)) for p in y]
     assert np.array_equal(bits(got[0]), bits(got[1])), "F32: device-resident weight differs from host weight"
-    if n <= 16:
-        assert np.array_equal(bits(got[2]), bits(got[3])), "F16: device-resident weight differs from host weight"
+    assert np.array_equal(bits(got[2]), bits(got[3])), "F16: device-resident weight differs from host weight"
     assert_matmul_close(got[2], w16, x, f"host f16 n={n}")
     assert_matmul_close(got[3], w16, x, f"device f16 n={n}")
     backend.release_weights()
 
 
-def test_matmul_multi_mixed_widths_and_many_weights(backend):
+@pytest.mark.parametrize("n", [4, 40])
+def test_matmul_multi_mixed_widths_and_many_weights(backend, n):
     """Weights of different input widths fall back to one call each (backend.h:58-60); more than eight weights of
-    one width take several launches."""
+    one width take several launches (gemv at n = 4; at n = 40 the F16 ones share F16-GEMM launches and the F32 ones
+    take sgemm)."""
     rng = np.random.default_rng(5)
-    n = 4
     x = rand(rng, (n, 192))
     ws = [rand(rng, (16 + i, 192), np.float16 if i % 2 else np.float32, 0.4) for i in range(11)]
     narrow = rand(rng, (24, 96), np.float32, 0.4)
@@ -171,6 +173,7 @@ def test_weight_copies_are_kept_and_released(backend):
     backend.release_weights()
     assert backend.weight_bytes() == 0
     w = rand(rng, (64, 128), np.float16)
+    w_odd = rand(rng, (64, 100), np.float16)  # in % 8 != 0: the fp32 GEMM on a widened copy
     x = rand(rng, (20, 128))
     with Buffers(backend) as B:
         dx, dy = B.upload(x), B.alloc(20 * 64)
@@ -179,7 +182,9 @@ def test_weight_copies_are_kept_and_released(backend):
         backend.matmul(w, dx, dy, 1)
         assert backend.weight_bytes() == w.nbytes  # reused, not copied again
         backend.matmul(w, dx, dy, 20)
-        assert backend.weight_bytes() == w.nbytes + 4 * w.size  # plus its fp32 widening for the GEMM route
+        assert backend.weight_bytes() == w.nbytes  # the F16 GEMM reads the fp16 copy itself
+        backend.matmul(w_odd, dx, dy, 20)
+        assert backend.weight_bytes() == w.nbytes + w_odd.nbytes + 4 * w_odd.size  # plus the fp32 widening
     backend.release_weights()
     assert backend.weight_bytes() == 0
 
@@ -200,4 +205,67 @@ def test_matmul_rejects_bad_arguments(backend):
             backend.matmul(w, dx, dy, 0)
         with pytest.raises(nibble_amd.BackendError, match="need F32"):
             backend.add_bias(dy, nibble_amd.weight(np.zeros(32, np.float16)), 1)
+    backend.release_weights()
+
+
+def test_f16_gemm_rows_of_any_magnitude(backend):
+    """The F16 GEMM scales each activation row by its own power of two before splitting it into fp16 parts: rows
+    whose largest elements range from 1e-30 to 3e30 (and an all-zero row, and a row mixing 1e-6 and 1e4 elements)
+    all stay within the summation bound, as the fp32 product does."""
+    rng = np.random.default_rng(21)
+    in_, out_ = 320, 80
+    w = rand(rng, (out_, in_), np.float16, 0.5)
+    scales = [1e-30, 1e-12, 1e-3, 1.0, 7.0, 3e4, 1e12, 3e30]
+    x = np.concatenate([rand(rng, (3, in_)) * np.float32(s) for s in scales] + [np.zeros((1, in_), np.float32)])
+    mixed = rand(rng, (1, in_)) * np.float32(1e-6)
+    mixed[0, ::17] *= np.float32(1e10)
+    x = np.ascontiguousarray(np.concatenate([x, mixed]), np.float32)
+    got = gpu_matmul(backend, w, x, x.shape[0])
+    assert_matmul_close(got, w, x, "rows of any magnitude")
+    assert np.all(bits(got[-2]) == 0), "an all-zero row gives +0"
+    backend.release_weights()
+
+
+def test_f16_gemm_nonfinite_activations(backend):
+    """Infinite and NaN activations give the reference's non-finite outputs (an infinite element is carried by its
+    fp16 high part alone, so it does not turn into NaN through hi - lo); the other rows are unaffected."""
+    rng = np.random.default_rng(22)
+    in_, out_, n = 64, 48, 24
+    w = rand(rng, (out_, in_), np.float16, 0.5)
+    w[5, 3] = 0.0  # inf * 0 = NaN in that output of the infinite row, as in the reference
+    x = rand(rng, (n, in_))
+    x[2, 3] = np.inf
+    x[7, 10] = -np.inf
+    x[9, 0] = np.nan
+    got = gpu_matmul(backend, w, x, n)
+    ref = oracle.matmul(w, x)
+    for t in (2, 7, 9):
+        assert np.array_equal(np.isnan(got[t]), np.isnan(ref[t])), f"row {t}: NaN pattern"
+        fin = ~np.isnan(ref[t])
+        assert np.array_equal(got[t][fin], ref[t][fin]), f"row {t}: infinities"
+    ok = [t for t in range(n) if t not in (2, 7, 9)]
+    assert_matmul_close(got[ok], w, x[ok], "finite rows beside non-finite ones")
+    backend.release_weights()
+
+
+def test_f16_gemm_wide_tiles(backend):
+    """A call with many output tiles takes the 128 x 128 tile configuration (32-deep K slices): 300 rows (a partial
+    last row tile), two weights of 11000 rows (partial last weight tiles) sharing x, in = 200 (a partial last
+    slice), within the summation bound. The second weight alone (258 wide tiles) takes the 64 x 64 configuration,
+    also within the bound."""
+    rng = np.random.default_rng(23)
+    n, in_, out_ = 300, 200, 11000
+    ws = [rand(rng, (out_, in_), np.float16, 0.3) for _ in range(2)]
+    x = rand(rng, (n, in_))
+    with Buffers(backend) as B:
+        dx = B.upload(x)
+        ys = [B.alloc(n * out_) for _ in ws]
+        backend.matmul_multi(ws, dx, ys, n)
+        got = [backend.download(y, (n, out_)) for y in ys]
+        y1 = B.alloc(n * out_)
+        backend.matmul(ws[1], dx, y1, n)  # one weight: the small-tile configuration
+        single = backend.download(y1, (n, out_))
+    for i, (g, w) in enumerate(zip(got, ws)):
+        assert_matmul_close(g, w, x, f"wide tiles, weight {i}")
+    assert_matmul_close(single, ws[1], x, "small tiles, same weight")
     backend.release_weights()
