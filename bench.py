@@ -690,7 +690,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
-              "multi-GPU sharding is described in DESIGN.md, not run", file=sys.stderr)
+              "multi-GPU sharding is a design note of this repository, not run", file=sys.stderr)
         sys.exit(2)
     if args.steps < 1 or args.steps > 64 or args.warmup < 0:
         sys.exit("--steps must be in 1..64 (config 4 decodes 64 tokens), --warmup >= 0")
