@@ -257,8 +257,8 @@ int nbhs_sgemm_xwt(nbhs_blas h, const float* x, const float* w, float* y, int64_
  * row is scaled by a power of two and split into fp16 hi + lo parts (x s = hi + lo to ~2^-22 relative); both are
  * multiplied by the exact fp16 weights with fp32 accumulation, so the result is fp32-grade (within the float
  * summation bound of the reference's sum). ws: device scratch of nbhs_gemm_f16w_workspace(n, in) bytes, 256-byte
- * aligned (the split rows). Requires in % 8 == 0 and 16-byte aligned weights; each launch is deterministic and
- * a weight's outputs do not depend on the other weights of the call. */
+ * aligned (the split rows). Requires in % 8 == 0 and 16-byte aligned weights. Deterministic; each weight's tile
+ * configuration follows from its own shape, so its outputs do not depend on the other weights of the call. */
 #define NBHS_GEMM_MAX_WEIGHTS 8
 int64_t nbhs_gemm_f16w_workspace(int64_t n, int64_t in);
 int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const int64_t* rows, int64_t in,

@@ -144,14 +144,14 @@ __global__ __launch_bounds__(64) void split_acts_kernel(const float* __restrict_
 }
 
 // Tile configuration: BM activation rows x BN weight rows per tile (each of the four waves takes BM/2 x BN/2),
-// BK-deep K slices, a STAGES-deep LDS ring. Two instances: 64 x 64 tiles with 64-deep slices for grids of fewer than
-// kWideMinTiles wide tiles (a 512-row QKV or FFN-down projection: more workgroups to spread the operand traffic),
-// 128 x 128 tiles with 32-deep slices above (an FFN gate + up projection: each operand byte fetched from L2 serves
-// twice the products). Both keep 72 KB of LDS per workgroup.
+// BK-deep K slices, a STAGES-deep LDS ring. Two instances, chosen per weight: 128 x 128 tiles with 32-deep slices for
+// a weight that alone makes at least kWideMinTiles of them (an FFN gate or up projection at 512 rows: each operand
+// byte fetched from L2 serves twice the products), 64 x 64 tiles with 64-deep slices otherwise (a 512-row QKV or
+// FFN-down projection: more workgroups to spread the operand traffic). Both keep 72 KB of LDS per workgroup.
 constexpr int kSmallBM = 64, kSmallBN = 64, kSmallBK = 64, kSmallStages = 3;
 constexpr int kWideBM = 128, kWideBN = 128, kWideBK = 32, kWideStages = 3;
 constexpr int kPadK = 64;  // K padding of the split activation rows (a multiple of both slice depths)
-constexpr int64_t kWideMinTiles = 512;
+constexpr int64_t kWideMinTiles = 256;
 
 template <int BM, int BN, int BK, int STAGES>
 __global__ __launch_bounds__(kThreads) void gemm_f16w_kernel(GemmBatch b, const _Float16* __restrict__ xh,
@@ -342,24 +342,23 @@ int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const i
   const int64_t need = nbhs_gemm_f16w_workspace(n, in);
   if (need < 0 || ws_bytes < need || reinterpret_cast<uintptr_t>(ws) % 256 != 0) return NBHS_EINVAL;
   const int64_t in_pad = round_up(in, kPadK);
-  // the tile configuration by the count of wide tiles; then every operand a buffer resource addresses must fit
-  // 32-bit offsets
-  int64_t wide_tiles = 0;
-  for (int i = 0; i < n_w; ++i) wide_tiles += (rows[i] + kWideBN - 1) / kWideBN;
-  wide_tiles *= (n + kWideBM - 1) / kWideBM;
-  const bool wide = wide_tiles >= kWideMinTiles;
-  const int bm = wide ? kWideBM : kSmallBM, bn = wide ? kWideBN : kSmallBN;
-  if (bm * in_pad * 2 > INT32_MAX || n > 65535 * int64_t(bm)) return NBHS_EINVAL;
-  GemmBatch b{};
-  int64_t tiles = 0;
+  // every operand a buffer resource addresses must fit 32-bit offsets
+  if (kWideBM * in_pad * 2 > INT32_MAX || n > 65535 * int64_t(kSmallBM)) return NBHS_EINVAL;
+  // Each weight's tile configuration follows from its own shape (so its results do not depend on the other weights
+  // of the call: matmul_multi equals separate calls); the weights of each configuration share one launch.
+  GemmBatch wide{}, small{};
+  int64_t wide_tiles = 0, small_tiles = 0;
   for (int i = 0; i < n_w; ++i) {
-    if (!w[i] || !y[i] || rows[i] <= 0 || reinterpret_cast<uintptr_t>(w[i]) % 16 != 0 || bn * in * 2 > INT32_MAX)
+    if (!w[i] || !y[i] || rows[i] <= 0 || reinterpret_cast<uintptr_t>(w[i]) % 16 != 0 ||
+        kWideBN * in * 2 > INT32_MAX)
       return NBHS_EINVAL;
-    b.w[i] = GemmWeight{static_cast<const _Float16*>(w[i]), y[i], rows[i], int(tiles)};
-    tiles += (rows[i] + bn - 1) / bn;
+    const bool is_wide = (rows[i] + kWideBN - 1) / kWideBN * ((n + kWideBM - 1) / kWideBM) >= kWideMinTiles;
+    GemmBatch& b = is_wide ? wide : small;
+    int64_t& t = is_wide ? wide_tiles : small_tiles;
+    b.w[b.n_w++] = GemmWeight{static_cast<const _Float16*>(w[i]), y[i], rows[i], int(t)};
+    t += (rows[i] + (is_wide ? kWideBN : kSmallBN) - 1) / (is_wide ? kWideBN : kSmallBN);
+    if (t > INT32_MAX) return NBHS_EINVAL;
   }
-  if (tiles > INT32_MAX) return NBHS_EINVAL;
-  b.n_w = n_w;
   char* base = static_cast<char*>(ws);
   _Float16* xh = reinterpret_cast<_Float16*>(base);
   _Float16* xl = xh + n * in_pad;
@@ -368,13 +367,15 @@ int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const i
   const int vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 ? 1 : 0;
   hipError_t e = nbhs_timing::launch(NBHS_K_SPLIT_ACTS, split_acts_kernel, dim3(unsigned(n)), dim3(64), s, x, in,
                                      in_pad, xh, xl, inv, vec);
-  if (e != hipSuccess) return e;
-  const dim3 grid(unsigned(tiles), unsigned((n + bm - 1) / bm));
-  if (wide)
-    return nbhs_timing::launch(NBHS_K_GEMM, gemm_f16w_kernel<kWideBM, kWideBN, kWideBK, kWideStages>, grid,
-                               dim3(kThreads), s, b, xh, xl, inv, n, in, in_pad);
-  return nbhs_timing::launch(NBHS_K_GEMM, gemm_f16w_kernel<kSmallBM, kSmallBN, kSmallBK, kSmallStages>, grid,
-                             dim3(kThreads), s, b, xh, xl, inv, n, in, in_pad);
+  if (e == hipSuccess && wide.n_w > 0)
+    e = nbhs_timing::launch(NBHS_K_GEMM, gemm_f16w_kernel<kWideBM, kWideBN, kWideBK, kWideStages>,
+                            dim3(unsigned(wide_tiles), unsigned((n + kWideBM - 1) / kWideBM)), dim3(kThreads), s,
+                            wide, xh, xl, inv, n, in, in_pad);
+  if (e == hipSuccess && small.n_w > 0)
+    e = nbhs_timing::launch(NBHS_K_GEMM, gemm_f16w_kernel<kSmallBM, kSmallBN, kSmallBK, kSmallStages>,
+                            dim3(unsigned(small_tiles), unsigned((n + kSmallBM - 1) / kSmallBM)), dim3(kThreads), s,
+                            small, xh, xl, inv, n, in, in_pad);
+  return e;
 }
 
 }  // extern "C"

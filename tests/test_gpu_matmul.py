@@ -249,23 +249,26 @@ def test_f16_gemm_nonfinite_activations(backend):
 
 
 def test_f16_gemm_wide_tiles(backend):
-    """A call with many output tiles takes the 128 x 128 tile configuration (32-deep K slices): 300 rows (a partial
-    last row tile), two weights of 11000 rows (partial last weight tiles) sharing x, in = 200 (a partial last
-    slice), within the summation bound. The second weight alone (258 wide tiles) takes the 64 x 64 configuration,
-    also within the bound."""
+    """A weight with many output tiles takes the 128 x 128 tile configuration (32-deep K slices): 300 rows (a partial
+    last row tile), weights of 11000 rows (partial last weight tiles), in = 200 (a partial last slice), within the
+    summation bound. The configuration follows from each weight's own shape, so a call mixing two such weights and a
+    500-row one (64 x 64 tiles; the two configurations in two launches) equals separate calls bit for bit
+    (backend.h:57)."""
     rng = np.random.default_rng(23)
-    n, in_, out_ = 300, 200, 11000
-    ws = [rand(rng, (out_, in_), np.float16, 0.3) for _ in range(2)]
+    n, in_ = 300, 200
+    ws = [rand(rng, (r, in_), np.float16, 0.3) for r in (11000, 500, 11000)]
     x = rand(rng, (n, in_))
     with Buffers(backend) as B:
         dx = B.upload(x)
-        ys = [B.alloc(n * out_) for _ in ws]
+        ys = [B.alloc(n * w.shape[0]) for w in ws]
         backend.matmul_multi(ws, dx, ys, n)
-        got = [backend.download(y, (n, out_)) for y in ys]
-        y1 = B.alloc(n * out_)
-        backend.matmul(ws[1], dx, y1, n)  # one weight: the small-tile configuration
-        single = backend.download(y1, (n, out_))
+        got = [backend.download(y, (n, w.shape[0])) for y, w in zip(ys, ws)]
+        sep = []
+        for w in ws:
+            y1 = B.alloc(n * w.shape[0])
+            backend.matmul(w, dx, y1, n)
+            sep.append(backend.download(y1, (n, w.shape[0])))
     for i, (g, w) in enumerate(zip(got, ws)):
-        assert_matmul_close(g, w, x, f"wide tiles, weight {i}")
-    assert_matmul_close(single, ws[1], x, "small tiles, same weight")
+        assert_matmul_close(g, w, x, f"weight {i} ({w.shape[0]} rows)")
+        assert np.array_equal(bits(g), bits(sep[i])), f"weight {i}: matmul_multi differs from a separate call"
     backend.release_weights()
