@@ -70,9 +70,12 @@ constexpr float kPSumMax = 4096.0f;
 // it, then the list itself, then one arrival counter per list entry (zeroed by the staging launch).
 constexpr int kAuxHead = 16;
 // Per key split of a prefill row tile, the record beside its partial output: shift, sum, sum of squared weights,
-// the error estimate's score coefficient (est_c1 * |y|^2/d * largest |k|^2), the largest |v|^2 and the query
-// residual's coefficient (est_c3 * |r| * sqrt(largest |k|^2)).
-constexpr int kSplitRec = 6;
+// the error estimate's score coefficient (est_c1 * |y|^2/d * largest |k|^2), the largest |v|^2, the query
+// residual's coefficient (est_c3 * |r| * sqrt(largest |k|^2)) and the coherent V-rounding bound of the keys visited.
+constexpr int kSplitRec = 8;
+// Keys per group of the coherent V-rounding statistic (stage_kv_kernel): a run of repeated value rows at least this
+// long shows in a group mean; shorter runs weigh in the variance term as few effective keys.
+constexpr int kVGroup = 8;
 
 // Rounding-error estimate of a row computed with fp16 operands. The scaled query y = Q * log2(e)/sqrt(d) enters
 // the scores as two fp16 parts, y = hi + lo + r (hi = fp16(y), lo = fp16(y - hi), |r| ~ 2^-22 |y|), so its
@@ -86,13 +89,20 @@ constexpr int kSplitRec = 6;
 //   var <= (sum_j p_j^2 / l^2) [2 ln2^2 (u^2/3) (|y|^2/d) K (V^2 + O^2) + (u^2/3) (3 V^2 + 2 O^2)].
 // The query's residual r is common to every key of the row, so its term c_d = ln2 sum_j w_j (r.k_j)(v_jd - o_d)
 // does not average out; it is bounded outright, |c_d| <= ln2 |r| sqrt(K) (V + O), with |r| computed exactly per row.
-// The row is accepted when kEstZ * sqrt(var) + ln2 |r| sqrt(K) (V + O) <= kEstBudget (the 1e-3 parity bar).
+// The V roundings are independent only across distinct value rows: equal rows (a token repeated in the prompt - V
+// carries no rotation) round equally, and their shared error survives the weighted mean whatever the number of keys
+// (up to 1.95e-3 for elements of 4 to 8). That part is bounded by C, the largest |mean fp16 rounding error| of V over
+// an aligned group of kVGroup keys, any dimension, over the tiles the row visits: for keys weighted alike within a
+// group, the weighted mean of the errors is a mean of group means. A run shorter than a group is a few keys of large
+// weight, which the variance term counts through sum p^2.
+// The row is accepted when kEstZ * sqrt(var) + ln2 |r| sqrt(K) (V + O) + C <= kEstBudget (the 1e-3 parity bar).
 // Checked against an exact emulation of this kernel's rounding over N(0,1) data at score scales 0.5-30, keys with
 // 1 % outlier rows x8, outlier V rows, a query aligned with one key, low-rank keys, a large common key or value
 // component, and q, K and V projected from shared low-rank hidden states (K and V correlated: the case where an
 // unsplit query's rounding adds up coherently over the keys), 65-8192 keys, head_dim 64 and 128: the emulated error
-// stayed within 0.71 sqrt(var) (tests/test_error_estimate.py), so an accepted row errs by at most 0.71 / 1.5 of the
-// bar.
+// stayed within 0.71 sqrt(var) (tests/test_error_estimate.py). With value rows repeated (runs of 1-2048 equal rows,
+// attended evenly or strongly, or two rows alternating) it stayed within 0.90 of the whole estimate, so an accepted
+// row errs by at most 0.9 of the bar.
 constexpr float kEstZ = 1.5f;
 constexpr float kEstBudget = 1e-3f;
 constexpr double kEstU = 1.0 / 2048.0;
@@ -179,10 +189,11 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(KVT* ck, KVT* cv, const f
                                                        const float* __restrict__ vn, _Float16* __restrict__ k16,
                                                        _Float16* __restrict__ vt16, int64_t pos0, int64_t rows,
                                                        int64_t rows_pad, int n_kv, const float2* __restrict__ cs,
-                                                       int neox, float2* __restrict__ kstats,
+                                                       int neox, float4* __restrict__ kstats,
                                                        uint32_t* __restrict__ aux, int aux_cap) {
   __shared__ _Float16 tr[HD][kBN + kPad];
-  __shared__ float red[2][4];
+  __shared__ float dvs[HD][kBN + 1];  // V's fp16 rounding errors fp16(v) - v (exact in fp32), [d][key]
+  __shared__ float red[3][4];
   const int g = blockIdx.y;
   const int64_t r0 = int64_t(blockIdx.x) * kBN;
   constexpr int H2 = HD / 2;
@@ -249,14 +260,14 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(KVT* ck, KVT* cv, const f
     _Float16* kd = k16 + (int64_t(g) * rows_pad + row) * HD + 4 * d4;
     *reinterpret_cast<half4_t*>(kd) = half4_t{(_Float16)k0.x, (_Float16)k0.y, (_Float16)k0.z, (_Float16)k0.w};
     *reinterpret_cast<half4_t*>(kd + H2) = half4_t{(_Float16)k1.x, (_Float16)k1.y, (_Float16)k1.z, (_Float16)k1.w};
-    tr[4 * d4 + 0][r] = (_Float16)v0.x;
-    tr[4 * d4 + 1][r] = (_Float16)v0.y;
-    tr[4 * d4 + 2][r] = (_Float16)v0.z;
-    tr[4 * d4 + 3][r] = (_Float16)v0.w;
-    tr[H2 + 4 * d4 + 0][r] = (_Float16)v1.x;
-    tr[H2 + 4 * d4 + 1][r] = (_Float16)v1.y;
-    tr[H2 + 4 * d4 + 2][r] = (_Float16)v1.z;
-    tr[H2 + 4 * d4 + 3][r] = (_Float16)v1.w;
+    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = (e < 4 ? 0 : H2) + 4 * d4 + (e & 3);
+      const _Float16 h = (_Float16)vv[e];
+      tr[d][r] = h;
+      dvs[d][r] = float(h) - vv[e];
+    }
   }
   __syncthreads();
   // V^T: each d row of the tile is 64 keys (128 B), stored in the key order of the PV MFMA operand (vt_key).
@@ -268,20 +279,34 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(KVT* ck, KVT* cv, const f
     *reinterpret_cast<half8_t*>(vt16 + (int64_t(g) * HD + d) * rows_pad + r0 + 8 * c8) = x;
   }
   if (kstats) {  // the tile's statistics for the prefill kernel's error estimate
+    // The largest mean fp16 rounding error of V over a group of kVGroup consecutive keys, any dimension: the part
+    // of V's rounding that can add up coherently over keys (repeated value rows round alike), summed in a fixed
+    // order so that the statistic, and the decisions taken on it, repeat bit for bit.
+    float vcoh = 0.f;
+    for (int idx = threadIdx.x; idx < HD * (kBN / kVGroup); idx += 256) {
+      const int d = idx / (kBN / kVGroup), g0 = (idx % (kBN / kVGroup)) * kVGroup;
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < kVGroup; ++e) sum += dvs[d][g0 + e];
+      vcoh = fmaxf(vcoh, fabsf(sum) * (1.0f / kVGroup));
+    }
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) {
       k2max = fmaxf(k2max, __shfl_xor(k2max, m, 64));
       vmax = fmaxf(vmax, __shfl_xor(vmax, m, 64));
+      vcoh = fmaxf(vcoh, __shfl_xor(vcoh, m, 64));
     }
     if ((threadIdx.x & 63) == 0) {
       red[0][threadIdx.x >> 6] = k2max;
       red[1][threadIdx.x >> 6] = vmax;
+      red[2][threadIdx.x >> 6] = vcoh;
     }
     __syncthreads();
     if (threadIdx.x == 0)
       kstats[int64_t(g) * (rows_pad / kBN) + blockIdx.x] =
-          make_float2(fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3])),
-                      fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3])));
+          make_float4(fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3])),
+                      fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3])),
+                      fmaxf(fmaxf(red[2][0], red[2][1]), fmaxf(red[2][2], red[2][3])), 0.f);
   }
 }
 
@@ -305,7 +330,7 @@ void attn_prefill_kernel(
     float* __restrict__ out, int64_t n, int64_t pos0, int n_heads, int n_kv, int group, int64_t rows_pad,
     int n_tiles, float qscale, const float2* __restrict__ q_rope, int q_rope_neox, const KVT* __restrict__ kc,
     const KVT* __restrict__ vc, int64_t fp32_rows, int fp32_n_sub, int n_split, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, const float2* __restrict__ kstats, uint32_t* __restrict__ aux, int aux_cap,
+    float* __restrict__ ws_ml, const float4* __restrict__ kstats, uint32_t* __restrict__ aux, int aux_cap,
     float est_c1, float est_c2, float est_c3) {
   // Workgroups past the MFMA tiles: query row t < fp32_rows of the call (q and out start fp32_rows rows before
   // this launch's MFMA rows) for KV head x head subgroup `by`, in fp32 over its whole causal window.
@@ -440,7 +465,8 @@ void attn_prefill_kernel(
   // the shift is subtracted on the VALU instead, which has slack.
   constexpr bool kFold = kQB == 1;
   float m_sh[kQB], l_run[kQB], l2_run[kQB];  // l2_run: sum of the squared fp16 weights (the error estimate's)
-  float kmx = 0.f, vmx = 0.f;  // largest |k row|^2 and |v| element over the key tiles this wave visits
+  // largest |k row|^2, |v| element and mean V rounding error of a key group over the key tiles this wave visits
+  float kmx = 0.f, vmx = 0.f, vcm = 0.f;
   floatx16 mneg;
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
@@ -528,9 +554,10 @@ void attn_prefill_kernel(
     asm volatile("" ::: "memory");
     if (kt + kStages - 1 < kt1) fetch(kt + kStages - 1, (cur + kStages - 1) % kStages);
     if (wave_active && int64_t(kt) * kBN < wave_kend) {
-      const float2 tst = kstats[int64_t(g) * (rows_pad / kBN) + kt];  // the tile's statistics (stage_kv_kernel)
+      const float4 tst = kstats[int64_t(g) * (rows_pad / kBN) + kt];  // the tile's statistics (stage_kv_kernel)
       kmx = fmaxf(kmx, tst.x);
       vmx = fmaxf(vmx, tst.y);
+      vcm = fmaxf(vcm, tst.z);
       // S^T for the tile's two 32-key halves and every query block, K times the query's high and then its low
       // part in one accumulator; each K fragment read from LDS serves both parts and all blocks, and the chains
       // are interleaved so consecutive MFMAs do not wait on each other's results. The raised wave priority keeps
@@ -687,7 +714,8 @@ void attn_prefill_kernel(
     const float est =
         l2_tot / (l_tot * l_tot) * (est_c1 * qn2[qb] * kmx * (vg2 + om2) + est_c2 * (3.f * vg2 + 2.f * om2));
     const float rk = est_c3 * sqrtf(qr2[qb] * kmx);  // the query residual's bound, per unit of (V + O)
-    flag = flag || (n_split == 1 && active[qb] && l_tot > 0.f && !(sqrtf(est) + rk * (vmx + om) <= 1.0f));
+    flag = flag || (n_split == 1 && active[qb] && l_tot > 0.f &&
+                    !(sqrtf(est) + rk * (vmx + om) + vcm * (1.0f / kEstBudget) <= 1.0f));
     if (n_split > 1 && active[qb] && hf == 0) {
       // a key split judges nothing alone (few keys look sharp): its terms go to the merge, which estimates the row
       float* rec = ws_ml + ((t[qb] * n_heads + head[qb]) * n_split + split) * kSplitRec;
@@ -695,6 +723,7 @@ void attn_prefill_kernel(
       rec[3] = est_c1 * qn2[qb] * kmx;
       rec[4] = vg2;
       rec[5] = rk;
+      rec[6] = vcm;
     }
   }
   if (__syncthreads_or(flag) && threadIdx.x == 0) {
@@ -1127,18 +1156,21 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
   const float4* po = reinterpret_cast<const float4*>(ws_o + rh * n_split * HD) + c4;
   float2 ml01[SPM], ml23[SPM];  // (shift, sum), (sum of squared weights, score coefficient)
   float2 ml45[SPM];             // (largest |v|^2, query residual coefficient)
+  float2 ml67[SPM];             // (largest mean V rounding error of a key group, unused)
   float4 o[SPM];
 #pragma unroll
   for (int sp = 0; sp < SPM; ++sp) {
     ml01[sp] = make_float2(-INFINITY, 0.f);
     ml23[sp] = make_float2(0.f, 0.f);
     ml45[sp] = make_float2(0.f, 0.f);
+    ml67[sp] = make_float2(0.f, 0.f);
     o[sp] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (sp < n_split) {
       const float* rec = ml + kSplitRec * sp;
       ml01[sp] = *reinterpret_cast<const float2*>(rec);
       ml23[sp] = *reinterpret_cast<const float2*>(rec + 2);
       ml45[sp] = *reinterpret_cast<const float2*>(rec + 4);
+      ml67[sp] = *reinterpret_cast<const float2*>(rec + 6);
       o[sp] = po[int64_t(sp) * V4];
     }
   }
@@ -1147,7 +1179,7 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
   for (int sp = 0; sp < SPM; ++sp) mx = fmaxf(mx, ml01[sp].x);
   const float ms = mx == -INFINITY ? 0.0f : mx;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  float l = 0.f, l2 = 0.f, a = 0.f, b = 0.f, rk = 0.f;
+  float l = 0.f, l2 = 0.f, a = 0.f, b = 0.f, rk = 0.f, vc = 0.f;
 #pragma unroll
   for (int sp = 0; sp < SPM; ++sp) {
     const float w = sp < n_split ? exp2_raw(ml01[sp].x - ms) : 0.f;  // the missing splits' partials are zeros
@@ -1161,6 +1193,7 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
       a = fmaxf(a, ml23[sp].y);
       b = fmaxf(b, ml45[sp].x);
       rk = fmaxf(rk, ml45[sp].y);
+      vc = fmaxf(vc, ml67[sp].x);
     }
   }
   const float inv = 1.0f / l;
@@ -1171,7 +1204,7 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
   for (int m = 1; m < V4; m <<= 1) om = fmaxf(om, __shfl_xor(om, m, 64));  // over the row's V4 lanes
   const float om2 = om * om;
   const float est = l2 * inv * inv * (a * (b + om2) + est_c2 * (3.f * b + 2.f * om2));
-  if (c4 == 0 && l > 0.f && !(sqrtf(est) + rk * (sqrtf(b) + om) <= 1.0f)) {
+  if (c4 == 0 && l > 0.f && !(sqrtf(est) + rk * (sqrtf(b) + om) + vc * (1.0f / kEstBudget) <= 1.0f)) {
     const int64_t t = rh / n_heads;
     const int head = int(rh % n_heads), g = head / group;
     const int64_t p = t * group + head % group;
@@ -1212,9 +1245,9 @@ extern "C" {
 
 int64_t nbhs_prefill_staging_halves(int64_t rows, int64_t n_kv_heads, int64_t head_dim) {
   if (rows < 0 || n_kv_heads <= 0 || head_dim <= 0) return -1;
-  // the operands, then (in the V^T buffer) one float2 of statistics per (KV head, 64-row tile)
+  // the operands, then (in the V^T buffer) one float4 of statistics per (KV head, 64-row tile)
   const int64_t rows_pad = round_up(rows, kBN);
-  return n_kv_heads * rows_pad * head_dim + n_kv_heads * (rows_pad / kBN) * 4;
+  return n_kv_heads * rows_pad * head_dim + n_kv_heads * (rows_pad / kBN) * 8;
 }
 
 int64_t nbhs_prefill_aux_words(int64_t n, int64_t n_heads, int64_t n_kv_heads) {
@@ -1234,8 +1267,8 @@ int64_t nbhs_prefill_aux_words_bound(int64_t max_rows, int64_t n_heads) {
 }
 
 namespace {
-float2* stats_of(void* vt16, int64_t rows_pad, int64_t n_kv, int64_t head_dim) {
-  return reinterpret_cast<float2*>(static_cast<_Float16*>(vt16) + n_kv * rows_pad * head_dim);
+float4* stats_of(void* vt16, int64_t rows_pad, int64_t n_kv, int64_t head_dim) {
+  return reinterpret_cast<float4*>(static_cast<_Float16*>(vt16) + n_kv * rows_pad * head_dim);
 }
 // list entries a work-list buffer of aux_words words holds (its layout follows this capacity)
 int aux_cap_of(int64_t aux_words) { return aux_words > kAuxHead ? int((aux_words - kAuxHead) / 3) : 0; }
@@ -1362,7 +1395,7 @@ int prefill_impl(const float* q, const void* k16, const void* vt16, float* out, 
   if (blocks >= int64_t(1) << 31) return NBHS_EINVAL;
   const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
   const int64_t off = fp32_rows * n_heads * head_dim;  // the MFMA rows start fp32_rows rows in
-  const float2* kstats = stats_of(const_cast<void*>(vt16), staged_rows_pad, n_kv_heads, head_dim);
+  const float4* kstats = stats_of(const_cast<void*>(vt16), staged_rows_pad, n_kv_heads, head_dim);
   // error-estimate coefficients, with the acceptance test folded in: flag when
   // sqrt(var * Z^2 / budget^2) + (ln2 / budget) |r| sqrt(K) (V + O) > 1
   const double u2 = kEstU * kEstU, zb = double(kEstZ) * kEstZ / (double(kEstBudget) * kEstBudget);

@@ -66,6 +66,22 @@ CORR_CASES = [
     ("prefill_corr_d128", 192, 1856, 8, 2, 128, 0.7, 2, 0.8),
 ]
 
+# (name, n, pos0, H, KV, D, kind, run_start, run_len): value rows that repeat, as the value rows of a token repeated
+# in the prompt do (V carries no rotation). "const": every row of a KV head's V equal; "alt": two rows alternating
+# over the whole window; "run": run_len rows from run_start equal, their keys equal too and aligned with the queries,
+# so the run takes most of each row's weight. The repeated rows hold elements of 4-5 that sit just below the midpoint
+# of two fp16 neighbours (fp16 rounding error 0.49 ulp = 1.9e-3, all towards zero): rounded to fp16 once per row,
+# equal rows carry equal errors, and the output, a weighted mean of the rows, carries their mean whatever the number
+# of keys. Deep chunks (the MFMA route), a short chunk whose keys are split over workgroups, Qwen's 7-to-1 grouping
+# and head_dim 128.
+REPEAT_CASES = [
+    ("repeat_const_v", 256, 1792, 32, 8, 64, "const", 0, 0),
+    ("repeat_run_attended", 256, 3840, 32, 8, 64, "run", 1000, 64),
+    ("repeat_alt_d128", 192, 1856, 8, 2, 128, "alt", 0, 0),
+    ("repeat_const_chunk", 64, 4032, 32, 8, 64, "const", 0, 0),
+    ("repeat_run_qwen", 384, 1664, 14, 2, 64, "run", 200, 128),
+]
+
 # (name, n, heads, hd, pos0, base, neox, llama3)
 ROPE_CASES = [
     ("qwen_q_pos512", 1, 14, 64, 512, 1e6, True, False),
@@ -127,6 +143,39 @@ def corr_inputs(i, n, pos0, H, KV, D, qscale, rank, vmix):
     return q, k, v
 
 
+def repeat_inputs(i, n, pos0, H, KV, D, kind, run_start, run_len):
+    """q [n, H, D], k, v [pos0 + n, KV, D] of a REPEAT_CASES entry. A repeated value row is a N(0,1) row whose
+    elements beyond 1.5 in magnitude become +-(4 + (m + 0.49) 2^-8), m in [0, 256): float32 values 0.49 fp16 ulps
+    above a representable fp16 value."""
+    ctx = pos0 + n
+    q = synth.normal_array((n, H, D), 903, i, 1)
+    k = synth.normal_array((ctx, KV, D), 903, i, 2)
+    v = synth.normal_array((ctx, KV, D), 903, i, 3)
+
+    def big_row(tensor, like=None):
+        """like: a row whose large elements fix where this row's are, and their signs."""
+        z = synth.normal_array((KV, D), 903, i, tensor).astype(np.float64)
+        m = np.floor(np.abs(z) * 1e4) % 256
+        mask, sign = (np.abs(z) > 1.5, np.sign(z)) if like is None else (np.abs(like) >= 4, np.sign(like))
+        return np.where(mask, sign * (4.0 + (m + 0.49) / 256.0), z).astype(np.float32)
+    a = big_row(4)
+    if kind == "const":
+        v[:] = a
+    elif kind == "alt":
+        b = big_row(5, like=a)
+        v[0::2], v[1::2] = a, b
+    elif kind == "run":
+        s = slice(run_start, run_start + run_len)
+        v[s] = a
+        key = synth.normal_array((KV, D), 903, i, 6)
+        k[s] = key
+        g = H // KV  # query head h reads KV head h // g: aligned with that head's run key, plus noise
+        q = (0.75 * np.repeat(key, g, axis=0)[None] + 0.5 * q).astype(np.float32)
+    else:
+        raise ValueError(kind)
+    return q, k, v
+
+
 def rope_input(i, n, heads, hd):
     return synth.normal_array((n, heads, hd), 901, i, 1)
 
@@ -149,6 +198,12 @@ def main():
         q, k, v = corr_inputs(i, n, pos0, H, KV, D, qs, rank, vmix)
         out[f"attn/{name}/shape"] = np.array([i, n, pos0, H, KV, D], np.int64)
         out[f"attn/{name}/qscale"] = np.array([qs], np.float32)
+        out[f"attn/{name}/input_sha256"] = sha(q, k, v)
+        put_output(out, f"attn/{name}/scalar", oracle.ref_attention_scalar(q, k, v, pos0, KV))
+        put_output(out, f"attn/{name}/simd", oracle.ref_attention_simd(q, k, v, pos0, KV))
+    for i, (name, n, pos0, H, KV, D, kind, rs, rl) in enumerate(REPEAT_CASES):
+        q, k, v = repeat_inputs(i, n, pos0, H, KV, D, kind, rs, rl)
+        out[f"attn/{name}/shape"] = np.array([i, n, pos0, H, KV, D], np.int64)
         out[f"attn/{name}/input_sha256"] = sha(q, k, v)
         put_output(out, f"attn/{name}/scalar", oracle.ref_attention_scalar(q, k, v, pos0, KV))
         put_output(out, f"attn/{name}/simd", oracle.ref_attention_simd(q, k, v, pos0, KV))

@@ -73,6 +73,32 @@ def test_attention_restatement_reproduces_reference_vectors_correlated(case):
         assert matches_gold(f"attn/{name}/simd", oracle.attention_parallel(q, k, v, pos0, KV, threads=8))
 
 
+@pytest.mark.parametrize("case", make_golden.REPEAT_CASES, ids=[c[0] for c in make_golden.REPEAT_CASES])
+def test_attention_restatement_reproduces_reference_vectors_repeated_values(case):
+    """The repeated-value-row cases (runs of equal value rows with elements near an fp16 rounding midpoint)."""
+    name, n, pos0, H, KV, D = case[:6]
+    i = int(GOLD[f"attn/{name}/shape"][0])
+    q, k, v = make_golden.repeat_inputs(i, *case[1:])
+    assert np.array_equal(GOLD[f"attn/{name}/input_sha256"], sha(q, k, v)), "input generator drifted"
+    assert matches_gold(f"attn/{name}/scalar", oracle.attention_scalar(q, k, v, pos0, KV))
+    if oracle.have_avx2():
+        assert matches_gold(f"attn/{name}/simd", oracle.attention_parallel(q, k, v, pos0, KV, threads=8))
+
+
+def test_repeated_value_cases_defeat_an_fp16_value_cache():
+    """What the repeated-value cases are for: V rounded to fp16 once per row moves the reference's output by more
+    than the 1e-3 bar (the equal rows' equal rounding errors survive the weighted mean). Checked on the const case
+    with the scalar restatement over fp16-rounded V."""
+    case = make_golden.REPEAT_CASES[0]
+    assert case[6] == "const"
+    name, n, pos0, H, KV, D = case[:6]
+    q, k, v = make_golden.repeat_inputs(0, *case[1:])
+    q, k, v = q[:4], k[:pos0 + 4], v[:pos0 + 4]
+    ref = oracle.attention_scalar(q, k, v, pos0, KV)
+    rounded = oracle.attention_scalar(q, k, v.astype(np.float16).astype(np.float32), pos0, KV)
+    assert float(np.max(np.abs(rounded - ref))) > 1.8e-3
+
+
 @pytest.mark.parametrize("case", make_golden.ROPE_CASES, ids=[c[0] for c in make_golden.ROPE_CASES])
 def test_rope_restatement_reproduces_reference_vectors(case):
     name, n, heads, hd, pos0, base, neox, l3 = case
