@@ -70,39 +70,36 @@ constexpr float kPSumMax = 4096.0f;
 // it, then the list itself, then one arrival counter per list entry (zeroed by the staging launch).
 constexpr int kAuxHead = 16;
 // Per key split of a prefill row tile, the record beside its partial output: shift, sum, sum of squared weights,
-// the error estimate's score coefficient (est_c1 * |y|^2/d * largest |k|^2), the largest |v|^2, the query
-// residual's coefficient (est_c3 * |r| * sqrt(largest |k|^2)) and the coherent V-rounding bound of the keys visited.
-constexpr int kSplitRec = 8;
-// Keys per group of the coherent V-rounding statistic (stage_kv_kernel): a run of repeated value rows at least this
-// long shows in a group mean; shorter runs weigh in the variance term as few effective keys.
-constexpr int kVGroup = 8;
+// the error estimate's score coefficient (est_c1 * |y|^2/d * largest |k|^2), the largest |v|^2 and the query
+// residual's coefficient (est_c3 * |r| * sqrt(largest |k|^2)).
+constexpr int kSplitRec = 6;
 
 // Rounding-error estimate of a row computed with fp16 operands. The scaled query y = Q * log2(e)/sqrt(d) enters
 // the scores as two fp16 parts, y = hi + lo + r (hi = fp16(y), lo = fp16(y - hi), |r| ~ 2^-22 |y|), so its
-// rounding is not a per-row error shared by every key: K, V and the weights P are rounded to nearest (relative
-// error at most u = 2^-11), and those roundings, one per key, are modelled as independent with variance u^2/3
-// each; accumulation is fp32. To first order the output error of dimension d is
+// rounding is not a per-row error shared by every key. K and V are staged with stochastic rounding (f16_sr): one
+// independent, zero-mean error per element whatever the data, of variance at most u^2 x^2 (u = 2^-11); the weights
+// P are rounded to nearest, one rounding per key modelled as independent with variance u^2/3; accumulation is fp32.
+// To first order the output error of dimension d is
 //   sum_j w_j [ln2 (e_j - e_mean)(v_jd - o_d) + eps_v,jd v_jd + (eps_p,j - eps_p,mean)(v_jd - o_d)] + c_d,
 // w_j = p_j / l, with e_j the score error (log2 units) of key j from rounding k_j: variance about
-// (u^2/3) |y|^2/d |k_j|^2. Bounding |k_j|^2 by the largest row norm K, |v_jd| by the largest element V and
+// u^2 |y|^2/d |k_j|^2. Bounding |k_j|^2 by the largest row norm K, |v_jd| by the largest element V and
 // (v - o)^2 by 2 (V^2 + O^2), O the row's largest output:
-//   var <= (sum_j p_j^2 / l^2) [2 ln2^2 (u^2/3) (|y|^2/d) K (V^2 + O^2) + (u^2/3) (3 V^2 + 2 O^2)].
+//   var <= (sum_j p_j^2 / l^2) [2 ln2^2 u^2 (|y|^2/d) K (V^2 + O^2) + (u^2/3) (5 V^2 + 2 O^2)].
+// Over an fp16 cache K and V are staged exactly and only the weights' term (u^2/3) 2 (V^2 + O^2) remains.
 // The query's residual r is common to every key of the row, so its term c_d = ln2 sum_j w_j (r.k_j)(v_jd - o_d)
 // does not average out; it is bounded outright, |c_d| <= ln2 |r| sqrt(K) (V + O), with |r| computed exactly per row.
-// The V roundings are independent only across distinct value rows: equal rows (a token repeated in the prompt - V
-// carries no rotation) round equally, and their shared error survives the weighted mean whatever the number of keys
-// (up to 1.95e-3 for elements of 4 to 8). That part is bounded by C, the largest |mean fp16 rounding error| of V over
-// an aligned group of kVGroup keys, any dimension, over the tiles the row visits: for keys weighted alike within a
-// group, the weighted mean of the errors is a mean of group means. A run shorter than a group is a few keys of large
-// weight, which the variance term counts through sum p^2.
-// The row is accepted when kEstZ * sqrt(var) + ln2 |r| sqrt(K) (V + O) + C <= kEstBudget (the 1e-3 parity bar).
-// Checked against an exact emulation of this kernel's rounding over N(0,1) data at score scales 0.5-30, keys with
-// 1 % outlier rows x8, outlier V rows, a query aligned with one key, low-rank keys, a large common key or value
-// component, and q, K and V projected from shared low-rank hidden states (K and V correlated: the case where an
-// unsplit query's rounding adds up coherently over the keys), 65-8192 keys, head_dim 64 and 128: the emulated error
-// stayed within 0.71 sqrt(var) (tests/test_error_estimate.py). With value rows repeated (runs of 1-2048 equal rows,
-// attended evenly or strongly, or two rows alternating) it stayed within 0.90 of the whole estimate, so an accepted
-// row errs by at most 0.9 of the bar.
+// The row is accepted when kEstZ * sqrt(var) + ln2 |r| sqrt(K) (V + O) <= kEstBudget (the 1e-3 parity bar).
+// Checked against an exact emulation of this kernel's rounding (its stochastic rounding bit for bit) over N(0,1)
+// data at score scales 0.5-30, keys with 1 % outlier rows x8, outlier V rows, a query aligned with one key,
+// low-rank keys, a large common key or value component, q, K and V projected from shared low-rank hidden states (K
+// and V correlated: the case where an unsplit query's rounding adds up coherently over the keys), 65-8192 keys,
+// head_dim 64 and 128: the emulated error stayed within 0.62 sqrt(var) (tests/test_error_estimate.py). With value
+// rows repeated - in runs, alternating or recurring at scattered positions, their large elements 0.1-0.49 ulp off
+// the fp16 grid, where rounding to nearest erred by up to 1.97e-3 on rows this estimate keeps - it stayed within
+// 1.3 sqrt(var), so an accepted row errs by at most 1.3 / 1.5 of the bar. The model is statistical: values placed
+// on purpose at the largest stochastic-rounding variance in every dimension make sqrt(var) tight, and the largest
+// of a row's dimensions can then exceed 1.5 sqrt(var) (emulated: up to 1.07e-3 on 2 of 300 such rows kept);
+// set_attention_fp32 routes every row through fp32 for callers that need the bar for any input.
 constexpr float kEstZ = 1.5f;
 constexpr float kEstBudget = 1e-3f;
 constexpr double kEstU = 1.0 / 2048.0;
@@ -177,8 +174,40 @@ __device__ __forceinline__ float4 as_cached(float4 x) {
   }
 }
 
+// Stochastic rounding of the staged operands. Rounded to nearest, equal cache values round alike wherever they sit,
+// so value rows that repeat (a token recurring in the prompt: V carries no rotation), key dimensions that RoPE
+// barely turns over a window, or values that sit on a common offset from the fp16 grid carry one shared rounding
+// error that the softmax's weighted mean does not average out (up to 1.95e-3 for elements of 4 to 8). Each element
+// is instead rounded up or down with probability given by its distance to the two fp16 neighbours, with random bits
+// hashed from its (position, KV head, dimension): the errors are zero-mean and independent from key to key whatever
+// the data, which is what the error estimate's variance model takes them to be, and the staging repeats bit for bit
+// (the same row is staged to the same fp16 values in every call). The variance of one such rounding is at most
+// ulp^2/4 <= u^2 x^2 (u = 2^-11), three times the u^2 x^2 / 3 of a rounding to nearest modelled as uniform.
+//
+// sr_bits: lowbias32 (Chris Wellons' integer hash, public domain) of a key built from the element's coordinates.
+__device__ __forceinline__ uint32_t sr_bits(int64_t row, int g, int d, int hd) {
+  uint32_t x = uint32_t(row) * 0x9E3779B1u + uint32_t(g * hd + d) * 0x85EBCA77u + 0x27D4EB2Fu;
+  x ^= x >> 16;
+  x *= 0x7FEB352Du;
+  x ^= x >> 15;
+  x *= 0x846CA68Bu;
+  x ^= x >> 16;
+  return x;
+}
+// x to fp16, rounded up or down at random: r13 (13 uniform bits) is added below the 10 mantissa bits fp16 keeps,
+// and the 13 bits below them are dropped, so the magnitude rounds up with probability (dropped part) / ulp. Applied
+// where the result is an fp16 normal number below 2^15 (the truncated value is then exactly representable); other
+// values (fp16 subnormals, whose rounding error is below 2^-25; magnitudes of 2^15 and more; inf and NaN) are
+// rounded to nearest.
+__device__ __forceinline__ _Float16 f16_sr(float x, uint32_t r13) {
+  const uint32_t b = __float_as_uint(x), mag = b & 0x7FFFFFFFu;
+  if (mag >= 0x38800000u && mag < 0x47000000u) return (_Float16)__uint_as_float((b + r13) & ~0x1FFFu);
+  return (_Float16)x;
+}
+
 // ---- staging: cache rows -> fp16 K [KV][rows_pad][HD] and transposed V [KV][HD][rows_pad] ----
-// The cache holds fp32 (KVT float) or fp16 (KVT _Float16) elements; an fp16 cache's rows are staged unchanged.
+// The cache holds fp32 (KVT float) or fp16 (KVT _Float16) elements; an fp16 cache's rows are staged unchanged, an
+// fp32 cache's are rounded to fp16 stochastically (f16_sr).
 // Rows [0, pos0) come from the cache ck/cv; rows [pos0, rows), when kn/vn are given, are the appended rows: K
 // rotated by RoPE at its position (cs, neox) in fp32, and both written into the cache (rounded to fp16 for an fp16
 // cache) as well as staged - the KV append and the staging in one pass. A thread takes one row and dimensions [4 d4, 4 d4 + 4) and the same four
@@ -189,11 +218,10 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(KVT* ck, KVT* cv, const f
                                                        const float* __restrict__ vn, _Float16* __restrict__ k16,
                                                        _Float16* __restrict__ vt16, int64_t pos0, int64_t rows,
                                                        int64_t rows_pad, int n_kv, const float2* __restrict__ cs,
-                                                       int neox, float4* __restrict__ kstats,
+                                                       int neox, float2* __restrict__ kstats,
                                                        uint32_t* __restrict__ aux, int aux_cap) {
   __shared__ _Float16 tr[HD][kBN + kPad];
-  __shared__ float dvs[HD][kBN + 1];  // V's fp16 rounding errors fp16(v) - v (exact in fp32), [d][key]
-  __shared__ float red[3][4];
+  __shared__ float red[2][4];
   const int g = blockIdx.y;
   const int64_t r0 = int64_t(blockIdx.x) * kBN;
   constexpr int H2 = HD / 2;
@@ -257,17 +285,26 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(KVT* ck, KVT* cv, const f
     k2max = fmaxf(k2max, ss);
     vmax = fmaxf(vmax, fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
                              fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w)))));
-    _Float16* kd = k16 + (int64_t(g) * rows_pad + row) * HD + 4 * d4;
-    *reinterpret_cast<half4_t*>(kd) = half4_t{(_Float16)k0.x, (_Float16)k0.y, (_Float16)k0.z, (_Float16)k0.w};
-    *reinterpret_cast<half4_t*>(kd + H2) = half4_t{(_Float16)k1.x, (_Float16)k1.y, (_Float16)k1.z, (_Float16)k1.w};
+    const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
     const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    _Float16 kh[8], vh[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int d = (e < 4 ? 0 : H2) + 4 * d4 + (e & 3);
-      const _Float16 h = (_Float16)vv[e];
-      tr[d][r] = h;
-      dvs[d][r] = float(h) - vv[e];
+      if constexpr (sizeof(KVT) == 4) {
+        // one hash per element: bits 0..12 round its K value, bits 13..25 its V value
+        const uint32_t rb = sr_bits(row, g, (e < 4 ? 0 : H2) + 4 * d4 + (e & 3), HD);
+        kh[e] = f16_sr(kk[e], rb & 0x1FFFu);
+        vh[e] = f16_sr(vv[e], (rb >> 13) & 0x1FFFu);
+      } else {
+        kh[e] = (_Float16)kk[e];  // already fp16 values
+        vh[e] = (_Float16)vv[e];
+      }
     }
+    _Float16* kd = k16 + (int64_t(g) * rows_pad + row) * HD + 4 * d4;
+    *reinterpret_cast<half4_t*>(kd) = half4_t{kh[0], kh[1], kh[2], kh[3]};
+    *reinterpret_cast<half4_t*>(kd + H2) = half4_t{kh[4], kh[5], kh[6], kh[7]};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tr[(e < 4 ? 0 : H2) + 4 * d4 + (e & 3)][r] = vh[e];
   }
   __syncthreads();
   // V^T: each d row of the tile is 64 keys (128 B), stored in the key order of the PV MFMA operand (vt_key).
@@ -279,34 +316,20 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(KVT* ck, KVT* cv, const f
     *reinterpret_cast<half8_t*>(vt16 + (int64_t(g) * HD + d) * rows_pad + r0 + 8 * c8) = x;
   }
   if (kstats) {  // the tile's statistics for the prefill kernel's error estimate
-    // The largest mean fp16 rounding error of V over a group of kVGroup consecutive keys, any dimension: the part
-    // of V's rounding that can add up coherently over keys (repeated value rows round alike), summed in a fixed
-    // order so that the statistic, and the decisions taken on it, repeat bit for bit.
-    float vcoh = 0.f;
-    for (int idx = threadIdx.x; idx < HD * (kBN / kVGroup); idx += 256) {
-      const int d = idx / (kBN / kVGroup), g0 = (idx % (kBN / kVGroup)) * kVGroup;
-      float sum = 0.f;
-#pragma unroll
-      for (int e = 0; e < kVGroup; ++e) sum += dvs[d][g0 + e];
-      vcoh = fmaxf(vcoh, fabsf(sum) * (1.0f / kVGroup));
-    }
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) {
       k2max = fmaxf(k2max, __shfl_xor(k2max, m, 64));
       vmax = fmaxf(vmax, __shfl_xor(vmax, m, 64));
-      vcoh = fmaxf(vcoh, __shfl_xor(vcoh, m, 64));
     }
     if ((threadIdx.x & 63) == 0) {
       red[0][threadIdx.x >> 6] = k2max;
       red[1][threadIdx.x >> 6] = vmax;
-      red[2][threadIdx.x >> 6] = vcoh;
     }
     __syncthreads();
     if (threadIdx.x == 0)
       kstats[int64_t(g) * (rows_pad / kBN) + blockIdx.x] =
-          make_float4(fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3])),
-                      fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3])),
-                      fmaxf(fmaxf(red[2][0], red[2][1]), fmaxf(red[2][2], red[2][3])), 0.f);
+          make_float2(fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3])),
+                      fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3])));
   }
 }
 
@@ -330,8 +353,8 @@ void attn_prefill_kernel(
     float* __restrict__ out, int64_t n, int64_t pos0, int n_heads, int n_kv, int group, int64_t rows_pad,
     int n_tiles, float qscale, const float2* __restrict__ q_rope, int q_rope_neox, const KVT* __restrict__ kc,
     const KVT* __restrict__ vc, int64_t fp32_rows, int fp32_n_sub, int n_split, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, const float4* __restrict__ kstats, uint32_t* __restrict__ aux, int aux_cap,
-    float est_c1, float est_c2, float est_c3) {
+    float* __restrict__ ws_ml, const float2* __restrict__ kstats, uint32_t* __restrict__ aux, int aux_cap,
+    float est_c1, float est_cv, float est_co, float est_c3) {
   // Workgroups past the MFMA tiles: query row t < fp32_rows of the call (q and out start fp32_rows rows before
   // this launch's MFMA rows) for KV head x head subgroup `by`, in fp32 over its whole causal window.
   static_assert(kWaves * 64 == nbh_decode::kDecodeThreads, "the fp32 rows' body runs on the MFMA workgroup size");
@@ -465,8 +488,7 @@ void attn_prefill_kernel(
   // the shift is subtracted on the VALU instead, which has slack.
   constexpr bool kFold = kQB == 1;
   float m_sh[kQB], l_run[kQB], l2_run[kQB];  // l2_run: sum of the squared fp16 weights (the error estimate's)
-  // largest |k row|^2, |v| element and mean V rounding error of a key group over the key tiles this wave visits
-  float kmx = 0.f, vmx = 0.f, vcm = 0.f;
+  float kmx = 0.f, vmx = 0.f;  // largest |k row|^2 and |v| element over the key tiles this wave visits
   floatx16 mneg;
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
@@ -554,10 +576,9 @@ void attn_prefill_kernel(
     asm volatile("" ::: "memory");
     if (kt + kStages - 1 < kt1) fetch(kt + kStages - 1, (cur + kStages - 1) % kStages);
     if (wave_active && int64_t(kt) * kBN < wave_kend) {
-      const float4 tst = kstats[int64_t(g) * (rows_pad / kBN) + kt];  // the tile's statistics (stage_kv_kernel)
+      const float2 tst = kstats[int64_t(g) * (rows_pad / kBN) + kt];  // the tile's statistics (stage_kv_kernel)
       kmx = fmaxf(kmx, tst.x);
       vmx = fmaxf(vmx, tst.y);
-      vcm = fmaxf(vcm, tst.z);
       // S^T for the tile's two 32-key halves and every query block, K times the query's high and then its low
       // part in one accumulator; each K fragment read from LDS serves both parts and all blocks, and the chains
       // are interleaved so consecutive MFMAs do not wait on each other's results. The raised wave priority keeps
@@ -712,10 +733,9 @@ void attn_prefill_kernel(
     om = fmaxf(om, __shfl_xor(om, 32, 64)) / l_tot;
     const float om2 = om * om, vg2 = vmx * vmx;
     const float est =
-        l2_tot / (l_tot * l_tot) * (est_c1 * qn2[qb] * kmx * (vg2 + om2) + est_c2 * (3.f * vg2 + 2.f * om2));
+        l2_tot / (l_tot * l_tot) * (est_c1 * qn2[qb] * kmx * (vg2 + om2) + est_cv * vg2 + est_co * om2);
     const float rk = est_c3 * sqrtf(qr2[qb] * kmx);  // the query residual's bound, per unit of (V + O)
-    flag = flag || (n_split == 1 && active[qb] && l_tot > 0.f &&
-                    !(sqrtf(est) + rk * (vmx + om) + vcm * (1.0f / kEstBudget) <= 1.0f));
+    flag = flag || (n_split == 1 && active[qb] && l_tot > 0.f && !(sqrtf(est) + rk * (vmx + om) <= 1.0f));
     if (n_split > 1 && active[qb] && hf == 0) {
       // a key split judges nothing alone (few keys look sharp): its terms go to the merge, which estimates the row
       float* rec = ws_ml + ((t[qb] * n_heads + head[qb]) * n_split + split) * kSplitRec;
@@ -723,7 +743,6 @@ void attn_prefill_kernel(
       rec[3] = est_c1 * qn2[qb] * kmx;
       rec[4] = vg2;
       rec[5] = rk;
-      rec[6] = vcm;
     }
   }
   if (__syncthreads_or(flag) && threadIdx.x == 0) {
@@ -1146,7 +1165,8 @@ template <int HD, int SPM>
 __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restrict__ ws_o,
                                                            const float* __restrict__ ws_ml, float* __restrict__ out,
                                                            int64_t rows_heads, int n_split, int n_heads, int group,
-                                                           uint32_t* __restrict__ aux, int aux_cap, float est_c2) {
+                                                           uint32_t* __restrict__ aux, int aux_cap, float est_cv,
+                                                           float est_co) {
   constexpr int V4 = HD / 4;
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i >= rows_heads * V4) return;  // whole rows only: rows_heads * V4 is a multiple of V4, and V4 divides 256
@@ -1156,21 +1176,18 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
   const float4* po = reinterpret_cast<const float4*>(ws_o + rh * n_split * HD) + c4;
   float2 ml01[SPM], ml23[SPM];  // (shift, sum), (sum of squared weights, score coefficient)
   float2 ml45[SPM];             // (largest |v|^2, query residual coefficient)
-  float2 ml67[SPM];             // (largest mean V rounding error of a key group, unused)
   float4 o[SPM];
 #pragma unroll
   for (int sp = 0; sp < SPM; ++sp) {
     ml01[sp] = make_float2(-INFINITY, 0.f);
     ml23[sp] = make_float2(0.f, 0.f);
     ml45[sp] = make_float2(0.f, 0.f);
-    ml67[sp] = make_float2(0.f, 0.f);
     o[sp] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (sp < n_split) {
       const float* rec = ml + kSplitRec * sp;
       ml01[sp] = *reinterpret_cast<const float2*>(rec);
       ml23[sp] = *reinterpret_cast<const float2*>(rec + 2);
       ml45[sp] = *reinterpret_cast<const float2*>(rec + 4);
-      ml67[sp] = *reinterpret_cast<const float2*>(rec + 6);
       o[sp] = po[int64_t(sp) * V4];
     }
   }
@@ -1179,7 +1196,7 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
   for (int sp = 0; sp < SPM; ++sp) mx = fmaxf(mx, ml01[sp].x);
   const float ms = mx == -INFINITY ? 0.0f : mx;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  float l = 0.f, l2 = 0.f, a = 0.f, b = 0.f, rk = 0.f, vc = 0.f;
+  float l = 0.f, l2 = 0.f, a = 0.f, b = 0.f, rk = 0.f;
 #pragma unroll
   for (int sp = 0; sp < SPM; ++sp) {
     const float w = sp < n_split ? exp2_raw(ml01[sp].x - ms) : 0.f;  // the missing splits' partials are zeros
@@ -1193,7 +1210,6 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
       a = fmaxf(a, ml23[sp].y);
       b = fmaxf(b, ml45[sp].x);
       rk = fmaxf(rk, ml45[sp].y);
-      vc = fmaxf(vc, ml67[sp].x);
     }
   }
   const float inv = 1.0f / l;
@@ -1203,8 +1219,8 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
 #pragma unroll
   for (int m = 1; m < V4; m <<= 1) om = fmaxf(om, __shfl_xor(om, m, 64));  // over the row's V4 lanes
   const float om2 = om * om;
-  const float est = l2 * inv * inv * (a * (b + om2) + est_c2 * (3.f * b + 2.f * om2));
-  if (c4 == 0 && l > 0.f && !(sqrtf(est) + rk * (sqrtf(b) + om) + vc * (1.0f / kEstBudget) <= 1.0f)) {
+  const float est = l2 * inv * inv * (a * (b + om2) + est_cv * b + est_co * om2);
+  if (c4 == 0 && l > 0.f && !(sqrtf(est) + rk * (sqrtf(b) + om) <= 1.0f)) {
     const int64_t t = rh / n_heads;
     const int head = int(rh % n_heads), g = head / group;
     const int64_t p = t * group + head % group;
@@ -1245,9 +1261,9 @@ extern "C" {
 
 int64_t nbhs_prefill_staging_halves(int64_t rows, int64_t n_kv_heads, int64_t head_dim) {
   if (rows < 0 || n_kv_heads <= 0 || head_dim <= 0) return -1;
-  // the operands, then (in the V^T buffer) one float4 of statistics per (KV head, 64-row tile)
+  // the operands, then (in the V^T buffer) one float2 of statistics per (KV head, 64-row tile)
   const int64_t rows_pad = round_up(rows, kBN);
-  return n_kv_heads * rows_pad * head_dim + n_kv_heads * (rows_pad / kBN) * 8;
+  return n_kv_heads * rows_pad * head_dim + n_kv_heads * (rows_pad / kBN) * 4;
 }
 
 int64_t nbhs_prefill_aux_words(int64_t n, int64_t n_heads, int64_t n_kv_heads) {
@@ -1267,8 +1283,8 @@ int64_t nbhs_prefill_aux_words_bound(int64_t max_rows, int64_t n_heads) {
 }
 
 namespace {
-float4* stats_of(void* vt16, int64_t rows_pad, int64_t n_kv, int64_t head_dim) {
-  return reinterpret_cast<float4*>(static_cast<_Float16*>(vt16) + n_kv * rows_pad * head_dim);
+float2* stats_of(void* vt16, int64_t rows_pad, int64_t n_kv, int64_t head_dim) {
+  return reinterpret_cast<float2*>(static_cast<_Float16*>(vt16) + n_kv * rows_pad * head_dim);
 }
 // list entries a work-list buffer of aux_words words holds (its layout follows this capacity)
 int aux_cap_of(int64_t aux_words) { return aux_words > kAuxHead ? int((aux_words - kAuxHead) / 3) : 0; }
@@ -1395,11 +1411,16 @@ int prefill_impl(const float* q, const void* k16, const void* vt16, float* out, 
   if (blocks >= int64_t(1) << 31) return NBHS_EINVAL;
   const float qscale = (1.0f / std::sqrt(float(head_dim))) * kLog2e;
   const int64_t off = fp32_rows * n_heads * head_dim;  // the MFMA rows start fp32_rows rows in
-  const float4* kstats = stats_of(const_cast<void*>(vt16), staged_rows_pad, n_kv_heads, head_dim);
+  const float2* kstats = stats_of(const_cast<void*>(vt16), staged_rows_pad, n_kv_heads, head_dim);
   // error-estimate coefficients, with the acceptance test folded in: flag when
   // sqrt(var * Z^2 / budget^2) + (ln2 / budget) |r| sqrt(K) (V + O) > 1
   const double u2 = kEstU * kEstU, zb = double(kEstZ) * kEstZ / (double(kEstBudget) * kEstBudget);
-  const float est_c1 = float(2.0 * kLn2 * kLn2 * (u2 / 3.0) * zb), est_c2 = float(u2 / 3.0 * zb);
+  // Per unit variance of a rounding (u^2 / 3 to nearest, u^2 stochastic): an fp32 cache's K and V are staged with
+  // stochastic rounding (score term 2 ln2^2 u^2 (|y|^2/d) K (V^2 + O^2), V's own rounding u^2 V^2); an fp16 cache's
+  // are staged exactly, leaving the weights' rounding alone, (u^2/3) 2 (V^2 + O^2).
+  constexpr bool kRoundedKV = sizeof(KVT) == 4;
+  const float est_c1 = kRoundedKV ? float(2.0 * kLn2 * kLn2 * u2 * zb) : 0.f;
+  const float est_cv = float((kRoundedKV ? 5.0 : 2.0) * u2 / 3.0 * zb), est_co = float(2.0 * u2 / 3.0 * zb);
   const float est_c3 = float(kLn2 / kEstBudget);
   const float2* q_rope = reinterpret_cast<const float2*>(q_rope_cs);
   hipError_t e = nbhs_timing::launch(
@@ -1408,13 +1429,14 @@ int prefill_impl(const float* q, const void* k16, const void* vt16, float* out, 
       dim3(kWaves * 64), s, q + off, static_cast<const _Float16*>(k16), static_cast<const _Float16*>(vt16), out + off,
       n_mfma, pos0 + fp32_rows, int(n_heads), int(n_kv_heads), int(group), staged_rows_pad, int(tiles), qscale,
       q_rope, q_rope_neox, k_cache, v_cache, fp32_rows, int(fp32_sub), sp, ws_o, ws_ml, kstats, aux, int(aux_cap),
-      est_c1, est_c2, est_c3);
+      est_c1, est_cv, est_co, est_c3);
   if (e != hipSuccess) return e;
   if (sp > 1) {
     const int64_t threads = n_mfma * n_heads * (head_dim / 4);
     e = nbhs_timing::launch(NBHS_K_DECODE_COMBINE, head_dim == 64 ? split_merge_for<64>(sp) : split_merge_for<128>(sp),
                             dim3(unsigned((threads + 255) / 256)), dim3(256), s, ws_o, ws_ml, out + off,
-                            n_mfma * n_heads, sp, int(n_heads), int(group), aux, int(aux_cap), est_c2);
+                            n_mfma * n_heads, sp, int(n_heads), int(group), aux, int(aux_cap), est_cv,
+                            est_co);
     if (e != hipSuccess) return e;
   }
   // The listed row tiles, recomputed with split operands (a persistent launch; nothing to do when none was listed).

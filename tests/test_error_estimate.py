@@ -1,15 +1,19 @@
-"""The prefill MFMA kernel's per-row rounding-error estimate (kernels/attn_prefill.hip, kEstZ / kEstBudget and the
-`est` / residual expressions of attn_prefill_kernel), checked on the CPU against an emulation of the kernel's rounding:
-the scaled query y = Q * log2(e) / sqrt(d) (fp32) enters the scores as two fp16 parts hi = fp16(y), lo = fp16(y - hi);
-K, V and the softmax weights P are rounded to fp16 (nearest); sums in high precision; all against the exact fp64
+"""The prefill MFMA kernel's per-row rounding-error estimate (kernels/attn_prefill.hip, kEstZ / kEstBudget, the `est` /
+residual expressions of attn_prefill_kernel and prefill_split_merge, and the staging's stochastic rounding f16_sr /
+sr_bits), checked on the CPU against an emulation of the kernel's rounding: the scaled query y = Q * log2(e) / sqrt(d)
+(fp32) enters the scores as two fp16 parts hi = fp16(y), lo = fp16(y - hi); K and V are staged to fp16 with the
+kernel's stochastic rounding (its hash and bit manipulation restated here exactly, so the emulation rounds each element
+as the GPU does); the softmax weights P are rounded to nearest; sums in high precision; all against the exact fp64
 softmax. Rows whose estimate passes (1.5 sqrt(var) + ln2 |r| sqrt(K) (V + O) <= 1e-3, r = y - hi - lo) are the rows
-the kernel keeps; every other row tile is recomputed with split operands. A third term, the largest mean fp16
-rounding error of V over a group of 8 keys, covers value rows that repeat, whose equal roundings add up coherently. The cases span the windows the MFMA route
-takes (65 keys and up: rows below position 128 run in fp32), score scales 0.5 to 30, the outlier shapes the
-estimate's bounds must cover, and q, K and V projected from shared low-rank hidden states, where K and V correlate
-(as in a transformer) and a rounding of the query, common to every key of the row, would add up coherently instead
-of averaging out: the reason the kernel splits the query. Reference semantics: ref_ops.cpp:188-214 computes the row
-in fp32 for any input; tests/test_ops.cpp:196-216 holds its SIMD tier to the scalar one for any data."""
+the kernel keeps; every other row tile is recomputed with split operands.
+
+The cases span the windows the MFMA route takes (65 keys and up: rows below position 128 run in fp32), score scales
+0.5 to 30, the outlier shapes the estimate's bounds must cover, q, K and V projected from shared low-rank hidden
+states (K and V correlate, as in a transformer, and a rounding of the query, common to every key of the row, would add
+up coherently: the reason the kernel splits the query), and value rows that repeat - in runs, alternating, or at
+scattered positions like a token recurring in a prompt - where rounding to nearest gives equal rows equal errors that
+add up coherently: the reason the staging rounds stochastically. Reference semantics: ref_ops.cpp:188-214 computes
+the row in fp32 for any input; tests/test_ops.cpp:196-216 holds its SIMD tier to the scalar one for any data."""
 import importlib.util
 import os
 
@@ -21,11 +25,43 @@ LN2 = float(np.log(2.0))
 Z, BUDGET = 1.5, 1e-3   # kEstZ, kEstBudget
 TILE = 64               # keys per tile (kBN): the tile statistics are per-tile maxima
 ROWS_PER_TILE = 128     # packed query rows of one MFMA row tile (kRowsPerBlock): flagged or kept together
-VGROUP = 8              # kVGroup: keys per group of the coherent V-rounding statistic
+M32 = np.uint64(0xFFFFFFFF)
 
 
 def f16(x):
     return np.asarray(x, np.float64).astype(np.float16).astype(np.float64)
+
+
+def sr_bits(rows, g, hd):
+    """[len(rows), hd] words of sr_bits(row, g, d, hd) (attn_prefill.hip): lowbias32 of row * 0x9E3779B1 +
+    (g * hd + d) * 0x85EBCA77 + 0x27D4EB2F, in 32-bit arithmetic."""
+    r = np.asarray(rows, np.uint64)[:, None] & M32
+    d = np.arange(hd, dtype=np.uint64)[None, :]
+    x = (r * np.uint64(0x9E3779B1) + (np.uint64(g * hd) + d) * np.uint64(0x85EBCA77) + np.uint64(0x27D4EB2F)) & M32
+    x ^= x >> np.uint64(16)
+    x = (x * np.uint64(0x7FEB352D)) & M32
+    x ^= x >> np.uint64(15)
+    x = (x * np.uint64(0x846CA68B)) & M32
+    x ^= x >> np.uint64(16)
+    return x.astype(np.uint32)
+
+
+def f16_sr(x, r13):
+    """f16_sr (attn_prefill.hip) on float32 x with 13 random bits r13: (bits(x) + r13) with the low 13 bits cleared,
+    for magnitudes in [2^-14, 2^15); rounding to nearest elsewhere. Returned as float64."""
+    x32 = np.asarray(x, np.float32)
+    b = x32.view(np.uint32)
+    mag = b & np.uint32(0x7FFFFFFF)
+    t = ((b + np.asarray(r13, np.uint32)) & np.uint32(0xFFFFE000)).view(np.float32)
+    ok = (mag >= np.uint32(0x38800000)) & (mag < np.uint32(0x47000000))
+    return np.where(ok, t, x32).astype(np.float16).astype(np.float64)
+
+
+def stage(k, v, g=0, row0=0):
+    """K and V rows row0, row0 + 1, ... of KV head g as the staging writes them: one hash word per element, bits
+    0..12 for K and 13..25 for V."""
+    bits = sr_bits(np.arange(row0, row0 + len(k)), g, k.shape[1])
+    return f16_sr(k, bits & np.uint32(0x1FFF)), f16_sr(v, (bits >> np.uint32(13)) & np.uint32(0x1FFF))
 
 
 def make(kind, n, hd, qscale, rng):
@@ -85,34 +121,29 @@ def query_parts(qh):
     return hi + lo, qh - hi - lo
 
 
-def emulate(q, k, v, split_q=True):
-    """(max-abs error of the fp16-operand row against fp64, the kernel's inputs to the estimate). split_q=False is
-    the query rounded once (the kernel before the split), kept for the planted-mistake checks."""
+def emulate(q, k, v, split_q=True, sr=True, g=0):
+    """(max-abs error of the fp16-operand row against fp64, the kernel's inputs to the estimate), keys at positions
+    0, 1, ... of KV head g. split_q=False is the query rounded once and sr=False K and V rounded to nearest (the
+    kernel before the split and before the stochastic staging), kept for the planted-mistake checks."""
     qh = scaled_query(q)
     s_ex = qh @ k.T
     w = np.exp2(s_ex - s_ex.max())
     ref = (w @ v) / w.sum()
     qq = query_parts(qh)[0] if split_q else f16(qh)
-    s = qq @ f16(k).T
+    kk, vv = stage(k, v, g) if sr else (f16(k), f16(v))
+    s = qq @ kk.T
     p = f16(np.exp2(s - s.max()))
     l = p.sum()
-    o = (p @ f16(v)) / l
+    o = (p @ vv) / l
     return float(np.abs(o - ref).max()), qh, p, l, o
 
 
-def vcoh(v):
-    """The largest mean fp16 rounding error of V over a group of VGROUP consecutive keys (groups aligned from key 0,
-    as the kernel's tiles are), any dimension: a deterministic bound on the part of V's rounding that repeated value
-    rows make coherent (stage_kv_kernel's third tile statistic, maximised over the tiles a row visits)."""
-    d = f16(v) - v
-    return max(float(np.abs(d[g:g + VGROUP].mean(0)).max()) for g in range(0, len(v), VGROUP))
-
-
-def estimate(qh, k, v, p, l, o, drop_v_term=False, u=U, score_roundings=1):
-    """(sqrt(var), residual bound, coherent V bound) as the kernel evaluates them: var = (sum p^2 / l^2) [2 ln2^2
-    (s u^2/3) (|y|^2/d) K (V^2 + O^2) + (u^2/3)(3 V^2 + 2 O^2)], s the roundings per score (1: the key's; 2 counts a
-    rounded query too), K the largest per-tile max of |k_j|^2, V the largest |v| element, O the row's largest output;
-    the residual bound ln2 |r| sqrt(K) (V + O); and vcoh(v)."""
+def estimate(qh, k, v, p, l, o, drop_v_term=False, u=U, sr=True, query_rounded=False):
+    """(sqrt(var), residual bound) as the kernel evaluates them: var = (sum p^2 / l^2) [2 ln2^2 (c u^2/3) (|y|^2/d) K
+    (V^2 + O^2) + (u^2/3)(c V^2 + 2 (V^2 + O^2))], c = 3 for stochastically rounded K and V (variance up to u^2 x^2)
+    and 1 for rounding to nearest (u^2 x^2 / 3), plus 1 in the score term when the query is rounded once; K the
+    largest per-tile max of |k_j|^2, V the largest |v| element, O the row's largest output; the residual bound
+    ln2 |r| sqrt(K) (V + O)."""
     hd = qh.size
     nt = (len(k) + TILE - 1) // TILE
     kmx = max(float(np.max(np.sum(k[t * TILE:(t + 1) * TILE] ** 2, 1))) for t in range(nt))
@@ -120,18 +151,63 @@ def estimate(qh, k, v, p, l, o, drop_v_term=False, u=U, score_roundings=1):
     om = float(np.abs(o).max())
     om2, vg2 = om * om, vmx * vmx
     qn2 = float(qh @ qh) / hd
-    c1 = 2 * LN2 * LN2 * (score_roundings * u * u / 3)
+    c = 3.0 if sr else 1.0
+    c1 = 2 * LN2 * LN2 * ((c + (1.0 if query_rounded else 0.0)) * u * u / 3)
     c2 = 0.0 if drop_v_term else u * u / 3
-    var = float(np.sum(p * p)) / (l * l) * (c1 * qn2 * kmx * (vg2 + om2) + c2 * (3 * vg2 + 2 * om2))
+    var = float(np.sum(p * p)) / (l * l) * (c1 * qn2 * kmx * (vg2 + om2) + c2 * (c * vg2 + 2 * (vg2 + om2)))
     r = query_parts(qh)[1]
     coh = LN2 * float(np.linalg.norm(r)) * np.sqrt(kmx) * (vmx + om)
-    return float(np.sqrt(var)), coh, vcoh(v)
+    return float(np.sqrt(var)), coh
 
 
 def kept(est):
-    sv, coh, vc = est
-    return Z * sv + coh + vc <= BUDGET
+    sv, coh = est
+    return Z * sv + coh <= BUDGET
 
+
+# ------------------------------------------------------------------------------------------ stochastic rounding
+
+def test_stochastic_rounding_lands_on_a_neighbour_and_is_unbiased():
+    """f16_sr returns one of x's two fp16 neighbours (x itself when representable), rounds to nearest outside
+    [2^-14, 2^15), and rounds up with probability equal to x's fractional position between the neighbours: over
+    65536 positions a value 0.3 ulp above an fp16 number rounds up 30 % of the time (+- 1 %), so the mean error is
+    ~0 where rounding to nearest errs by -0.3 ulp every time."""
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(20000) * np.exp(rng.uniform(-8, 8, 20000))).astype(np.float32)
+    r = rng.integers(0, 1 << 13, x.size).astype(np.uint32)
+    y = f16_sr(x, r)
+    lo = x.astype(np.float16)
+    lo = np.where(lo.astype(np.float32) > x, np.nextafter(lo, np.float16(-np.inf)), lo).astype(np.float64)
+    hi = np.nextafter(lo.astype(np.float16), np.float16(np.inf)).astype(np.float64)
+    inside = (np.abs(x) >= 2.0 ** -14) & (np.abs(x) < 2.0 ** 15)
+    assert np.all((y[inside] == lo[inside]) | (y[inside] == hi[inside]))
+    assert np.array_equal(y[~inside], f16(x[~inside]))
+    exact = np.float16(rng.standard_normal(1000)).astype(np.float32)
+    assert np.array_equal(f16_sr(exact, rng.integers(0, 1 << 13, 1000).astype(np.uint32)), exact.astype(np.float64))
+    base = np.float32(4.0 + 17 / 256)
+    x03 = np.float32(base + 0.3 / 256)
+    k, v = stage(np.full((65536, 1), x03), np.full((65536, 1), x03))
+    for z in (k, v):
+        up = float(np.mean(z > x03))
+        assert abs(up - 0.3) < 0.01, up
+    assert abs(float(np.mean(v - x03))) < 3e-5 and abs(float(f16(x03) - x03) + 0.3 / 256) < 1e-6
+
+
+def test_stochastic_rounding_bits_are_independent_across_neighbours():
+    """The hash words of neighbouring positions and dimensions look independent: the K and V bit fields of a 4096 x
+    64 block are uniform (each of 8 bins within 3 % of its share) and uncorrelated between adjacent rows, adjacent
+    dimensions and the K and V fields of one element (|corr| < 0.02)."""
+    bits = sr_bits(np.arange(4096), 3, 64)
+    kb = (bits & np.uint32(0x1FFF)).astype(np.float64)
+    vb = ((bits >> np.uint32(13)) & np.uint32(0x1FFF)).astype(np.float64)
+    for f in (kb, vb):
+        counts = np.bincount((f.ravel() // 1024).astype(int), minlength=8)
+        assert np.all(np.abs(counts / f.size - 0.125) < 0.03 * 0.125 * 8), counts
+    for a, b in ((kb[1:], kb[:-1]), (kb[:, 1:], kb[:, :-1]), (kb, vb), (vb[1:], vb[:-1])):
+        assert abs(np.corrcoef(a.ravel(), b.ravel())[0, 1]) < 0.02
+
+
+# ------------------------------------------------------------------------------------------ families
 
 KINDS = ["n01", "kout", "vout", "align", "lowrank", "kmean", "vmean"]
 SCALES = [0.5, 1.0, 2.0, 5.0, 30.0]
@@ -160,8 +236,57 @@ def corr_rows(seed):
                             yield (f"corr{rank}/{vmix}/{'qp' if qproj else 'qr'}", qs, n, hd, q, k, v)
 
 
-def with_emulation(cases, split_q):
-    return [c + emulate(*c[4:], split_q=split_q) for c in cases]
+def big_row(rng, hd, count=6):
+    """A value row whose `count` largest elements are 4 + (m + f) 2^-8 for f in {0.49, 0.3, 0.1}: fp16 rounding to
+    nearest errs by -f ulp (up to 1.9e-3) on each, the same for every copy of the row."""
+    r = rng.standard_normal(hd)
+    idx = rng.choice(hd, count, replace=False)
+    r[idx] = rng.choice([-1, 1], count) * (4 + (rng.integers(0, 256, count) + rng.choice([0.49, 0.3, 0.1], count))
+                                            / 256)
+    return r
+
+
+def repeated_rows(seed, count):
+    """Rows whose value rows repeat (V carries no rotation, so a token repeated in the prompt repeats its value row):
+    runs of L equal rows at a random place in the window (the query attending evenly or to the run, whose keys are
+    aligned with it), two rows alternating over the whole window, or one row recurring at scattered positions every
+    2-33 keys (its keys equal, aligned with the query, or unrelated)."""
+    rng = np.random.default_rng(seed)
+    for i in range(count):
+        hd = (64, 128)[i % 2]
+        n = int(rng.choice([129, 300, 600, 1000, 2048, 4096]))
+        q = rng.standard_normal(hd) * float(rng.choice([0.5, 1.0, 2.0, 3.0]))
+        k = rng.standard_normal((n, hd))
+        v = rng.standard_normal((n, hd))
+        kind = rng.choice(["run", "run-attended", "alternating", "scattered"])
+        if kind == "alternating":
+            v[0::2], v[1::2] = big_row(rng, hd), big_row(rng, hd)
+            name = kind
+        elif kind == "scattered":
+            period = int(rng.choice([2, 3, 5, 7, 10, 16, 33]))
+            pos = np.arange(int(rng.integers(0, period)), n, period)
+            v[pos] = big_row(rng, hd)
+            keys = rng.choice(["equal", "aligned", "unrelated"])
+            along = q / np.linalg.norm(q) * np.sqrt(hd) * float(rng.choice([0.5, 1.0, 1.5]))
+            if keys == "equal":
+                k[pos] = along
+            elif keys == "aligned":
+                k[pos] += along
+            name = f"scattered-{keys}/p{period}"
+        else:
+            L = int(rng.choice([1, 2, 4, 8, 16, 32, 64, n]))
+            s0 = int(rng.integers(0, max(1, n - L)))
+            v[s0:s0 + L] = big_row(rng, hd)
+            if kind == "run-attended":
+                m = min(L, n - s0)
+                k[s0:s0 + m] = (q / np.linalg.norm(q) * np.linalg.norm(k[s0]) * 1.5
+                                + 0.05 * rng.standard_normal((m, hd)))
+            name = f"{kind}/L{L}"
+        yield (name, 1.0, n, hd, q, k, v)
+
+
+def with_emulation(cases, split_q=True, sr=True):
+    return [c + emulate(*c[4:], split_q=split_q, sr=sr) for c in cases]
 
 
 @pytest.fixture(scope="module")
@@ -176,15 +301,22 @@ def corr_cases():
 
 @pytest.fixture(scope="module")
 def cases(plain_cases, corr_cases):
-    return with_emulation(plain_cases + corr_cases, True)
+    return with_emulation(plain_cases + corr_cases)
 
+
+@pytest.fixture(scope="module")
+def repeated_cases():
+    return list(repeated_rows(17, 400))
+
+
+# ------------------------------------------------------------------------------------------ the estimate
 
 def test_estimate_bounds_the_emulated_error(cases):
-    """The emulated error stays below the estimate's sqrt(var) alone (measured: at most ~0.71 on these cases), so a
+    """The emulated error stays below the estimate's sqrt(var) alone (measured: at most ~0.62 on these cases), so a
     row the kernel keeps errs by well under the 1e-3 bar; this holds on the correlated families too."""
     worst, at = 0.0, None
     for kind, qs, n, hd, q, k, v, err, qh, p, l, o in cases:
-        sv, coh, _ = estimate(qh, k, v, p, l, o)
+        sv, coh = estimate(qh, k, v, p, l, o)
         if err / sv > worst:
             worst, at = err / sv, (kind, qs, n, hd)
     assert worst < 0.95, f"emulated error up to {worst:.3f} sqrt(var) at {at}"
@@ -195,7 +327,7 @@ def test_residual_term_is_small(cases):
     the strength of the variance term alone (hi + lo leave ~2^-22 |y|; measured at most 1.4e-4)."""
     worst = 0.0
     for kind, qs, n, hd, q, k, v, err, qh, p, l, o in cases:
-        sv, coh, _ = estimate(qh, k, v, p, l, o)
+        sv, coh = estimate(qh, k, v, p, l, o)
         if Z * sv <= BUDGET:
             worst = max(worst, coh)
     assert worst < 0.2 * BUDGET, worst
@@ -233,30 +365,30 @@ def reproducer():
 
 
 def test_reproducer_row_is_flagged_or_within_the_bar():
-    """With the query rounded once, the row is kept (estimate 7.9e-4) and errs by 1.13e-3 - the query's rounding is
-    shared by all 4096 keys and K, V correlate. With the split query it is within the bar and inside its estimate."""
+    """With the query rounded once (and K, V rounded to nearest: that kernel), the row is kept and errs by 1.13e-3 -
+    the query's rounding is shared by all 4096 keys and K, V correlate. With the split query and the stochastic
+    staging it is within the bar and inside its estimate."""
     q, k, v = reproducer()
-    err0, qh, p, l, o = emulate(q, k, v, split_q=False)
-    sv0, coh0, _ = estimate(qh, k, v, p, l, o, score_roundings=2)
-    assert Z * sv0 + coh0 <= BUDGET and err0 > BUDGET, err0  # kept by the estimate of that kernel
+    err0, qh, p, l, o = emulate(q, k, v, split_q=False, sr=False)
+    assert kept(estimate(qh, k, v, p, l, o, sr=False, query_rounded=True)) and err0 > BUDGET, err0
     err, qh, p, l, o = emulate(q, k, v)
-    sv, coh, _ = estimate(qh, k, v, p, l, o)
+    sv, coh = estimate(qh, k, v, p, l, o)
     assert err <= BUDGET and err <= 0.95 * sv, (err, sv)
 
 
 def test_an_unsplit_query_underestimates_on_correlated_rows(corr_cases):
-    """Planted mistake: the query rounded to fp16 once (the estimate then counting two roundings per score) is
-    outgrown by the emulated error on correlated rows - the bound checked above would fail."""
+    """Planted mistake: the query rounded to fp16 once (the estimate then counting its rounding in the score term)
+    is outgrown by the emulated error on correlated rows - the bound checked above would fail."""
     worst = 0.0
     for kind, qs, n, hd, q, k, v in corr_cases[::3]:
-        err, qh, p, l, o = emulate(q, k, v, split_q=False)
-        worst = max(worst, err / estimate(qh, k, v, p, l, o, score_roundings=2)[0])
+        err, qh, p, l, o = emulate(q, k, v, split_q=False, sr=False)
+        worst = max(worst, err / estimate(qh, k, v, p, l, o, sr=False, query_rounded=True)[0])
     assert worst > 1.5, worst
 
 
 def test_a_dropped_value_rounding_term_underestimates(cases):
-    """Planted mistake: without the value-rounding term (u^2/3)(3 V^2 + 2 O^2) the estimate falls below the emulated
-    error somewhere (short windows, small scores), so the check above would catch it."""
+    """Planted mistake: without the value- and weight-rounding term (u^2/3)(c V^2 + 2 (V^2 + O^2)) the estimate
+    falls below the emulated error somewhere (short windows, small scores), so the check above would catch it."""
     worst = max(err / max(estimate(qh, k, v, p, l, o, drop_v_term=True)[0], 1e-30)
                 for kind, qs, n, hd, q, k, v, err, qh, p, l, o in cases)
     assert worst > 1.0, worst
@@ -294,12 +426,12 @@ def tiles(seed, count):
         yield (hd, rank, vmix, qscale, pos0), tile_rows(rng, hd, rank, vmix, qscale, pos0)
 
 
-def judge_tile(rows_, split_q=True, score_roundings=1):
+def judge_tile(rows_):
     """(tile kept, worst row error, worst err / sqrt(var)) with the kernel's rule: one row over budget flags all."""
     keep, worst, ratio = True, 0.0, 0.0
     for q, k, v in rows_:
-        err, qh, p, l, o = emulate(q, k, v, split_q=split_q)
-        est = estimate(qh, k, v, p, l, o, score_roundings=score_roundings)
+        err, qh, p, l, o = emulate(q, k, v)
+        est = estimate(qh, k, v, p, l, o)
         keep = keep and kept(est)
         worst = max(worst, err)
         ratio = max(ratio, err / est[0])
@@ -307,9 +439,8 @@ def judge_tile(rows_, split_q=True, score_roundings=1):
 
 
 def test_row_tiles_from_shared_hidden_states():
-    """Whole 128-row tiles (32 positions x 4 GQA heads, the query also projected from the hidden states; values of
-    up to 3-4, so the coherent V term alone takes half the budget and most tiles are recomputed): no row of a kept
-    tile errs by more than 6e-4, every row stays within 0.95 sqrt(var), and some tiles are kept."""
+    """Whole 128-row tiles (32 positions x 4 GQA heads, the query also projected from the hidden states): no row of
+    a kept tile errs by more than 6e-4, every row stays within 0.95 sqrt(var), and some tiles are kept."""
     kept_tiles = 0
     for cfg, rows_ in tiles(11, 48):
         keep, worst, ratio = judge_tile(rows_)
@@ -320,79 +451,38 @@ def test_row_tiles_from_shared_hidden_states():
     assert kept_tiles > 0
 
 
-def repeated_rows(seed, count):
-    """Rows whose value rows repeat: runs of L identical value rows (a token repeated in the prompt: V carries no
-    rotation, so the rows are equal and their fp16 roundings too) at a random place in the window, or two rows
-    alternating over the whole window; the repeated rows hold elements of 2 to 8, where an fp16 rounding reaches
-    0.98e-3 to 1.95e-3. The query attends evenly, or to the run (its keys aligned with q)."""
-    rng = np.random.default_rng(seed)
-    for i in range(count):
-        hd = (64, 128)[i % 2]
-        n = int(rng.choice([129, 300, 600, 2048]))
-        L = int(rng.choice([1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 64, n]))
-        q = rng.standard_normal(hd) * float(rng.choice([0.5, 1.0, 3.0, 6.0]))
-        k = rng.standard_normal((n, hd))
-        v = rng.standard_normal((n, hd))
+# ------------------------------------------------------------------------------------------ repeated value rows
 
-        def big_row():
-            r = rng.standard_normal(hd)
-            r[rng.integers(hd, size=3)] = rng.uniform(2, 8, 3) * rng.choice([-1, 1], 3)
-            return r
-        kind = rng.choice(["run", "run-attended", "alternating"])
-        if kind == "alternating":
-            a, b = big_row(), big_row()
-            v[0::2], v[1::2] = a, b
-        else:
-            s0 = int(rng.integers(0, max(1, n - L)))
-            v[s0:s0 + L] = big_row()
-            if kind == "run-attended":
-                m = min(L, n - s0)
-                k[s0:s0 + m] = (q / np.linalg.norm(q) * np.linalg.norm(k[s0]) * 1.5
-                                + 0.05 * rng.standard_normal((m, hd)))
-        yield (f"{kind}/L{L}", n, hd, q, k, v)
+def test_repeated_value_rows_stay_within_the_bar(repeated_cases):
+    """Value rows repeated in runs, alternating or at scattered positions, with elements 0.1-0.49 fp16 ulp off the
+    grid: stochastically rounded, equal rows carry independent errors and the variance model holds - every row errs
+    by less than 1.45 sqrt(var) (the largest elements, near the top of their rounding variance, make the estimate
+    tight: measured up to ~1.3), so a kept row (1.5 sqrt(var) <= 1e-3) meets the bar; kept rows measured up to
+    ~7e-4, and many rows are kept."""
+    worst, at, worst_kept, n_kept = 0.0, None, 0.0, 0
+    for kind, qs, n, hd, q, k, v in repeated_cases:
+        err, qh, p, l, o = emulate(q, k, v)
+        sv, coh = estimate(qh, k, v, p, l, o)
+        if err / sv > worst:
+            worst, at = err / sv, (kind, n, hd)
+        if Z * sv + coh <= BUDGET:
+            n_kept += 1
+            worst_kept = max(worst_kept, err)
+    assert worst < 0.95 * Z, f"emulated error up to {worst:.3f} sqrt(var) at {at}"
+    assert worst_kept <= 8e-4, worst_kept
+    assert n_kept > len(repeated_cases) // 4
 
 
-@pytest.fixture(scope="module")
-def repeated_cases():
-    return [c + emulate(*c[3:]) for c in repeated_rows(17, 160)]
-
-
-def test_repeated_value_rows_stay_within_the_estimate(repeated_cases):
-    """With value rows repeated, their fp16 roundings are equal and add up coherently: up to 1.95e-3 for elements of
-    4 to 8, whatever the number of keys. The estimate's coherent term (the largest mean rounding error of a group of
-    8 keys) covers that; runs shorter than a group weigh in the variance term as few effective keys. Every row stays
-    within 0.95 of the whole estimate, so a kept row meets the bar, and some rows are kept."""
-    worst, at, kept_rows = 0.0, None, 0
-    for kind, n, hd, q, k, v, err, qh, p, l, o in repeated_cases:
-        sv, coh, vc = estimate(qh, k, v, p, l, o)
-        total = Z * sv + coh + vc
-        if err / total > worst:
-            worst, at = err / total, (kind, n, hd)
-        if total <= BUDGET:
-            kept_rows += 1
-            assert err <= BUDGET, (kind, n, hd, err)
-    assert worst < 0.95, f"emulated error up to {worst:.3f} of the estimate at {at}"
-    assert kept_rows > 0
-
-
-def test_without_the_coherent_term_repeated_rows_miss_the_bar(repeated_cases):
-    """Planted mistake: the estimate without its coherent V term (the rounding of every value row taken as
-    independent) keeps rows with repeated value rows that miss the 1e-3 bar."""
+def test_rounding_to_nearest_misses_the_bar_on_repeated_rows(repeated_cases):
+    """Planted mistake: K and V rounded to nearest (with the estimate's constants for that rounding) - equal rows
+    then round alike and their errors add up: the estimate keeps rows that miss the 1e-3 bar (measured: over a
+    third of the scattered ones, at up to 1.97e-3)."""
     missed = 0
-    for kind, n, hd, q, k, v, err, qh, p, l, o in repeated_cases:
-        sv, coh, _ = estimate(qh, k, v, p, l, o)
-        if Z * sv + coh <= BUDGET and err > BUDGET:
+    for kind, qs, n, hd, q, k, v in repeated_cases[::2]:
+        err, qh, p, l, o = emulate(q, k, v, sr=False)
+        if kept(estimate(qh, k, v, p, l, o, sr=False)) and err > BUDGET:
             missed += 1
-    assert missed > 0
-
-
-def test_coherent_term_on_unrepeated_rows(cases):
-    """On the families without repeated rows the coherent term is what the group means of independent roundings
-    leave (about 3-5e-4 at N(0,1) values): rows stay within 0.95 of the whole estimate and accepted rows within
-    6e-4."""
-    for kind, qs, n, hd, q, k, v, err, qh, p, l, o in cases:
-        sv, coh, vc = estimate(qh, k, v, p, l, o)
-        assert err <= 0.95 * (Z * sv + coh + vc), (kind, qs, n, hd)
+    assert missed >= 10, missed
 
 
 def load_make_golden():
@@ -403,10 +493,13 @@ def load_make_golden():
     return mod
 
 
-def test_repeated_value_golden_cases_are_flagged():
+def test_repeated_value_golden_cases():
     """The repeated-value golden cases (tests/golden/make_golden.py, REPEAT_CASES) on sampled rows - first, middle
-    and last row of the call, heads spread over the KV groups: the kernel's rounding errs by more than the bar there,
-    the estimate without its coherent term keeps the row, and the whole estimate flags it."""
+    and last row of the call, heads spread over the KV groups, keys at their absolute positions and KV head, so the
+    emulation stages each element with the kernel's own random bits: with rounding to nearest every sampled row errs
+    by more than the bar while its estimate keeps it; with the stochastic staging every sampled row is within the
+    bar. On the all-equal cases (`repeat_const_*`) the estimate keeps every sampled row and the error stays within
+    4e-4 (every row of `repeat_const_chunk` is kept, so the GPU test sees the MFMA route's own result there)."""
     mg = load_make_golden()
     for i, case in enumerate(mg.REPEAT_CASES):
         name, n, pos0, H, KV, D = case[:6]
@@ -417,8 +510,9 @@ def test_repeated_value_golden_cases_are_flagged():
                 ctx = pos0 + r + 1
                 qq = q[r, h].astype(np.float64)
                 kk, vv = k[:ctx, h // g].astype(np.float64), v[:ctx, h // g].astype(np.float64)
-                err, qh, p, l, o = emulate(qq, kk, vv)
-                sv, coh, vc = estimate(qh, kk, vv, p, l, o)
-                assert err > BUDGET, (name, r, h, err)
-                assert Z * sv + coh <= BUDGET, (name, r, h)
-                assert not kept((sv, coh, vc)), (name, r, h)
+                err0, qh, p, l, o = emulate(qq, kk, vv, sr=False)
+                assert err0 > BUDGET and kept(estimate(qh, kk, vv, p, l, o, sr=False)), (name, r, h, err0)
+                err, qh, p, l, o = emulate(qq, kk, vv, g=h // g)
+                assert err <= BUDGET, (name, r, h, err)
+                if name.startswith("repeat_const"):
+                    assert kept(estimate(qh, kk, vv, p, l, o)) and err <= 4e-4, (name, r, h, err)
