@@ -236,7 +236,8 @@ def f16kv_decode(be, steps, warmup):
     (`prefill_8k`, TFLOP/s as the fp32-cache prefill counts them)."""
     shape, NL, ctx = configs.LLAMA32_1B, 16, 32768
     H, KV, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
-    rows = ctx + steps + warmup + 1
+    stamped = 8  # steps whose partial launches carry start/stop events, after the timed ones
+    rows = ctx + steps + warmup + stamped
     halves = rows * KV * D
     rng = np.random.default_rng(5)
     host = rng.standard_normal(halves).astype(np.float16).view(np.float32)
@@ -271,7 +272,8 @@ def f16kv_decode(be, steps, warmup):
     ms = e0.elapsed_ms(e1) / steps
     byts = sum(NL * 4 * KV * D * (ctx + s + 1) for s in range(warmup, warmup + steps)) / steps
     KernelTiming.enable(True, only=KernelTiming.DECODE_PARTIAL)
-    step(warmup + steps)
+    for s in range(warmup + steps, warmup + steps + stamped):
+        step(s)
     be.sync()
     pm, pn = KernelTiming.read(KernelTiming.DECODE_PARTIAL)
     KernelTiming.enable(False)
@@ -299,7 +301,8 @@ def f16kv_decode(be, steps, warmup):
         be.free(p_)
     gbs = byts / (ms * 1e-3) / 1e9
     part_us = pm / pn * 1e3
-    part_gbs = 4 * KV * D * (ctx + warmup + steps + 1) / (part_us * 1e-6) / 1e9
+    part_rows = ctx + warmup + steps + (stamped + 1) / 2  # the stamped steps' mean context
+    part_gbs = 4 * KV * D * part_rows / (part_us * 1e-6) / 1e9
     log(f"fp16 KV decode: {ms:.4f} ms/step over {NL} layers -> {gbs:.0f} GB/s of fp16 rows ({gbs / HBM_PEAK_GBS:.1%}); "
         f"partial kernel {part_us:.2f} us -> {part_gbs:.0f} GB/s; 8k prefill over fp16 caches {pre_ms:.3f} ms for "
         f"{NL} layers -> {pre_tflops:.1f} TFLOP/s")
