@@ -801,11 +801,19 @@ void attn_prefill_kernel(
 // partials (shift, sum, weighted V for its 128 rows) to ws; the last unit of the tile to finish (an arrival
 // counter per entry, an agent-scope release before counting and an acquire after) merges them into out, reading
 // every range's shifts and sums at once, then the weighted rows range by range with all of a thread's columns in
-// flight together. The launch is persistent: workgroup b takes units b, b + grid, ..., range-major (the first range
-// of every entry, then the second, ...), so every entry's first range starts at once; with an empty list every
-// workgroup returns at once.
+// flight together. The launch is persistent: the units that exist are numbered densely (the kernel's schedule
+// below) and workgroup b takes units b, b + grid, ...; with a short list every unit starts at once, and with an
+// empty list every workgroup returns at once.
 constexpr int kPreciseMaxRanges = 16;
-constexpr int kPreciseMinTiles = 4;  // key tiles per range at least: shorter ranges cost more in merging
+#ifndef NBH_PRECISE_MIN_TILES
+#define NBH_PRECISE_MIN_TILES 4
+#endif
+#ifndef NBH_PRECISE_WG_PER_CU
+#define NBH_PRECISE_WG_PER_CU 1
+#endif
+constexpr int kPreciseMinTiles = NBH_PRECISE_MIN_TILES;  // key tiles per range at least: shorter ones merge more
+constexpr int kPreciseBatch = 32;    // a workgroup's units located per pass over the work list
+constexpr int kPreciseSlotRegs = 4;  // list entries per thread kept in registers between the schedule's passes
 
 __device__ __forceinline__ int precise_ranges(uint32_t count, int64_t ws_floats, int hd, int max_key_tiles) {
   const int64_t per_unit = int64_t(kRowsPerBlock) * (hd + 2);
@@ -829,6 +837,7 @@ __global__ __launch_bounds__(kWaves * 64) void attn_prefill_precise_kernel(
   __shared__ uint32_t arrival;
   __shared__ float merge_w[kPreciseMaxRanges][kRowsPerBlock];  // the merge's per-row range weights
   const uint32_t count = aux[0];
+  if (count == 0) return;  // nothing listed: most calls of a chunked prefill
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ql = lane & 31, hf = lane >> 5;
   const int64_t P = n * group, rows_valid = pos0 + n;
@@ -836,322 +845,409 @@ __global__ __launch_bounds__(kWaves * 64) void attn_prefill_precise_kernel(
   const int max_key_tiles = int((pos0 + n + kBN - 1) / kBN);
   const int ps = precise_ranges(count, ws_floats, HD, max_key_tiles);
   uint32_t* const arrivals = aux + kAuxHead + 2 * aux_cap;
-  for (int64_t u = blockIdx.x; u < int64_t(count) * ps; u += gridDim.x) {
-    const uint32_t it = uint32_t(u % count);
-    const int range = int(u / count);
-    const uint32_t slot = aux[kAuxHead + aux_cap + it];
-    const int tile = int(slot / uint32_t(n_kv)), g = int(slot % uint32_t(n_kv));
-    const int64_t pb0 = int64_t(tile) * kRowsPerBlock, wp0 = pb0 + wave * kRowsPerWave;
-    const int64_t p = wp0 + ql;
-    const bool active = p < P;
-    const int64_t t = active ? p / group : 0;
-    const int head = g * group + (active ? int(p % group) : 0);
-    const int64_t qpos = pos0 + t;
-    const int64_t kend = pos0 + (min(pb0 + kRowsPerBlock, P) - 1) / group + 1;
-    const int ntk = int((kend + kBN - 1) / kBN);
-    // this unit's key tiles: range `range` of the tile's ntk tiles in n_ranges contiguous ranges of at least
-    // kPreciseMinTiles tiles (a short tile is one range)
-    const int want = min(ps, max(1, ntk / kPreciseMinTiles));
-    const int per = (ntk + want - 1) / want, n_ranges = (ntk + per - 1) / per;
-    if (range >= n_ranges) continue;  // workgroup-uniform
-    const int kt0 = range * per, kt1 = min(ntk, kt0 + per);
-    const bool wave_active = wp0 < P;
-    const int64_t wave_kend = wave_active ? pos0 + (min(wp0 + kRowsPerWave, P) - 1) / group + 1 : 0;
-    const int64_t wave_kfull = wave_active ? pos0 + wp0 / group + 1 : 0;
+  const uint32_t* const list = aux + kAuxHead + aux_cap;
+  // key tiles of list entry e's row tile (its causal window)
+  auto slot_ntk = [&](uint32_t slot) -> int {
+    const int64_t pb = int64_t(slot / uint32_t(n_kv)) * kRowsPerBlock;
+    return int((pos0 + (min(pb + kRowsPerBlock, P) - 1) / group + 1 + kBN - 1) / kBN);
+  };
 
-    // Q (rotated on load when q_rope is given, as the prefill kernel does), scaled, split.
-    half8_t qh[DC], qlw[DC];
-    {
-      const float* qrow = q + (t * n_heads + head) * HD;
-      float x[DC][8];
+  // Schedule. T = the listed tiles' key tiles in all; an entry of ntk key tiles is cut into max(1, ntk / per_all)
+  // equal ranges (at most ps, the workspace's slots), per_all = max(kPreciseMinTiles, ceil(T / grid)): ranges of at
+  // least per_all tiles (a short entry stays whole, with no merge), and at most T / per_all <= grid units, one round
+  // when the list allows it. The units (entry e, range r) are numbered densely, entry after entry, through a
+  // block-wide prefix sum of the entries' range counts, and workgroup b takes units b, b + grid, ...: no workgroup
+  // waits on units that do not exist.
+  const uint32_t G = gridDim.x, b = blockIdx.x;
+  __shared__ uint32_t s_wsum[kWaves];
+  __shared__ uint32_t s_mine_e[kPreciseBatch], s_mine_r[kPreciseBatch], s_mine_slot[kPreciseBatch];
+  // the list's slots, read once: entries threadIdx.x + THREADS j for j < kPreciseSlotRegs in registers, the rest
+  // (lists longer than THREADS * kPreciseSlotRegs) read again where needed
+  uint32_t slot_reg[kPreciseSlotRegs];
+  uint32_t tsum = 0;
 #pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), bb = a;
-        if (active) {
-          a = *reinterpret_cast<const float4*>(qrow + 16 * c + 8 * hf);
-          bb = *reinterpret_cast<const float4*>(qrow + 16 * c + 8 * hf + 4);
-        }
-        x[c][0] = a.x, x[c][1] = a.y, x[c][2] = a.z, x[c][3] = a.w;
-        x[c][4] = bb.x, x[c][5] = bb.y, x[c][6] = bb.z, x[c][7] = bb.w;
-      }
-      if (q_rope && active) {
-        const float2* cs = q_rope + qpos * (HD / 2);
-        if (q_rope_neox) {
+  for (int j = 0; j < kPreciseSlotRegs; ++j) {
+    const uint32_t e = threadIdx.x + THREADS * j;
+    slot_reg[j] = e < count ? list[e] : 0u;
+    tsum += e < count ? uint32_t(slot_ntk(slot_reg[j])) : 0u;
+  }
+  for (uint32_t e = threadIdx.x + THREADS * kPreciseSlotRegs; e < count; e += THREADS)
+    tsum += uint32_t(slot_ntk(list[e]));
 #pragma unroll
-          for (int c = 0; c < DC / 2; ++c)
+  for (int m = 1; m < 64; m <<= 1) tsum += __shfl_xor(tsum, m, 64);
+  if (lane == 0) s_wsum[wave] = tsum;
+  __syncthreads();
+  uint32_t T = 0;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) rope_rotate(x[c][e], x[c + DC / 2][e], cs[16 * c + 8 * hf + e]);
-        } else {
-#pragma unroll
-          for (int c = 0; c < DC; ++c)
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) rope_rotate(x[c][e], x[c][e + 1], cs[(16 * c + 8 * hf + e) / 2]);
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < DC; ++c)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const half2_t hl = split_f16(x[c][e] * qscale);
-          qh[c][e] = hl[0];
-          qlw[c][e] = hl[1];
-        }
-    }
+  for (int w = 0; w < kWaves; ++w) T += s_wsum[w];
+  __syncthreads();
+  const int per_all = max(kPreciseMinTiles, int((T + G - 1) / G));
+  // key tiles per range of an entry of ntk key tiles; its ranges are ceil(ntk / per) <= ps
+  auto entry_per = [&](int ntk) {
+    const int nr = min(ps, max(1, ntk / per_all));
+    return (ntk + nr - 1) / nr;
+  };
 
-    floatx16 oacc[DT];
+  for (uint32_t done = 0;;) {
+    // this workgroup's units done .. done + kPreciseBatch - 1 (its k-th unit is unit b + k G)
+    uint32_t base = 0;  // units of the entries before this chunk
+    for (uint32_t c0 = 0, c = 0; c0 < count; c0 += THREADS, ++c) {
+      const uint32_t e = c0 + threadIdx.x;
+      uint32_t nr = 0, slot = 0;
+      if (e < count) {
+        slot = c < kPreciseSlotRegs ? slot_reg[0] : list[e];
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
-    float m = -INFINITY, l = 0.f;
-
-    // One key tile's fp32 K rows (float4 (key, 4 dims)) and V pairs (keys 2j, 2j+1 x 8 dims), held in registers one
-    // tile ahead of the compute; rows past the call's last valid row are zeros (and masked).
-    float4 kr[K_F4], va[V_U][2], vb[V_U][2];
-    auto fetch = [&](int kt) {
-      const int64_t r0 = int64_t(kt) * kBN;
-#pragma unroll
-      for (int i = 0; i < K_F4; ++i) {
-        const int f = threadIdx.x + THREADS * i, r = f / (HD / 4), c4 = f % (HD / 4);
-        kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (r0 + r < rows_valid) kr[i] = ld4(kc + (r0 + r) * row_stride + g * HD + 4 * c4);
+        for (int j = 1; j < kPreciseSlotRegs; ++j) slot = c == uint32_t(j) ? slot_reg[j] : slot;
+        const int ntk = slot_ntk(slot), per = entry_per(ntk);
+        nr = uint32_t((ntk + per - 1) / per);
       }
+      uint32_t x = nr;  // inclusive prefix sum over the chunk
 #pragma unroll
-      for (int i = 0; i < V_U; ++i) {
-        const int uu = threadIdx.x + THREADS * i, db = uu % (HD / 8), j = uu / (HD / 8);
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        va[i][0] = va[i][1] = vb[i][0] = vb[i][1] = z;
-        const int64_t ra = r0 + 2 * j;
-        if (ra < rows_valid) {
-          const KVT* src = vc + ra * row_stride + g * HD + 8 * db;
-          va[i][0] = ld4(src);
-          va[i][1] = ld4(src + 4);
-        }
-        if (ra + 1 < rows_valid) {
-          const KVT* src = vc + (ra + 1) * row_stride + g * HD + 8 * db;
-          vb[i][0] = ld4(src);
-          vb[i][1] = ld4(src + 4);
-        }
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
       }
-    };
-    // The fetched tile, split, into LDS: K rows at their swizzled chunks, V^T as key pairs in the vt_key order
-    // (vt_key is its own inverse: the position of key 2j, with 2j + 1 next to it).
-    auto stage = [&]() {
-#pragma unroll
-      for (int i = 0; i < K_F4; ++i) {
-        const int f = threadIdx.x + THREADS * i, r = f / (HD / 4), c4 = f % (HD / 4);
-        const half2_t sx = split_f16(kr[i].x), sy = split_f16(kr[i].y), sz = split_f16(kr[i].z), sw = split_f16(kr[i].w);
-        const int at = r * HD + 8 * ((c4 >> 1) ^ swz<KCPR>(r)) + 4 * (c4 & 1);
-        *reinterpret_cast<half4_t*>(&khi[at]) = half4_t{sx[0], sy[0], sz[0], sw[0]};
-        *reinterpret_cast<half4_t*>(&klo[at]) = half4_t{sx[1], sy[1], sz[1], sw[1]};
-      }
-#pragma unroll
-      for (int i = 0; i < V_U; ++i) {
-        const int uu = threadIdx.x + THREADS * i, db = uu % (HD / 8), j = uu / (HD / 8);
-        const int pos = vt_key(2 * j);
-        const float a8[8] = {va[i][0].x, va[i][0].y, va[i][0].z, va[i][0].w, va[i][1].x, va[i][1].y, va[i][1].z,
-                             va[i][1].w};
-        const float b8[8] = {vb[i][0].x, vb[i][0].y, vb[i][0].z, vb[i][0].w, vb[i][1].x, vb[i][1].y, vb[i][1].z,
-                             vb[i][1].w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int d = 8 * db + e;
-          const half2_t sa = split_f16(a8[e]), sb = split_f16(b8[e]);
-          const int at = d * kBN + 8 * ((pos >> 3) ^ swz<VCPR>(d)) + (pos & 7);
-          *reinterpret_cast<half2_t*>(&vhi[at]) = half2_t{sa[0], sb[0]};
-          *reinterpret_cast<half2_t*>(&vlo[at]) = half2_t{sa[1], sb[1]};
-        }
-      }
-    };
-    auto kfrag = [&](const _Float16* base, int r, int x) {
-      return *reinterpret_cast<const half8_t*>(&base[r * HD + 8 * (x ^ swz<KCPR>(r))]);
-    };
-    auto vfrag = [&](const _Float16* base, int d, int x) {
-      return *reinterpret_cast<const half8_t*>(&base[d * kBN + 8 * (x ^ swz<VCPR>(d))]);
-    };
-
-    fetch(kt0);
-    for (int kt = kt0; kt < kt1; ++kt) {
-      __syncthreads();  // every wave is done with the previous tile (or unit) in LDS
-      stage();
+      if (lane == 63) s_wsum[wave] = x;
       __syncthreads();
-      if (kt + 1 < kt1) fetch(kt + 1);  // in flight while this tile is computed
-      const int64_t r0 = int64_t(kt) * kBN;
-      if (!(wave_active && r0 < wave_kend)) continue;
-      floatx16 sacc[2];
+      uint32_t off = 0, total = 0;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[kk][r] = 0.f;
-      // consecutive MFMAs go to the two halves' independent accumulators
-#pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        half8_t ah[2], al[2];
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          ah[kk] = kfrag(khi, kk * 32 + ql, 2 * c + hf);
-          al[kk] = kfrag(klo, kk * 32 + ql, 2 * c + hf);
-        }
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[kk], qh[c], sacc[kk], 0, 0, 0);
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[kk], qlw[c], sacc[kk], 0, 0, 0);
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[kk], qh[c], sacc[kk], 0, 0, 0);
+      for (int w = 0; w < kWaves; ++w) {
+        off += w < wave ? s_wsum[w] : 0u;
+        total += s_wsum[w];
       }
-      if (r0 + kBN > wave_kfull) {
-        const int64_t rel64 = active ? qpos - r0 : -1;
-        const int rel = int(rel64 < kBN ? rel64 : kBN);
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (kk * 32 + 8 * (r / 4) + 4 * hf + (r % 4) > rel) sacc[kk][r] = -INFINITY;
-      }
-      float mt = -INFINITY;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kk][r]);
-      const float mn = fmaxf(m, fmaxf(mt, __shfl_xor(mt, 32, 64)));
-      const float ms = mn == -INFINITY ? 0.0f : mn;
-      if (__builtin_amdgcn_ballot_w64(mn > m) != 0) {
-        const float corr = exp2_raw(m - ms);  // m = -inf: 0, and o, l are still 0
-        l *= corr;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
-      }
-      m = mn;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sacc[kk][r] = exp2_raw(sacc[kk][r] - ms);
-          l += sacc[kk][r];
+      __syncthreads();
+      const uint32_t u0 = base + off + x - nr;  // entry e's first unit
+      for (uint32_t u = u0 + (b + G - u0 % G) % G; u < u0 + nr; u += G) {
+        const uint32_t k = (u - b) / G;
+        if (k >= done && k < done + kPreciseBatch) {
+          s_mine_e[k - done] = e;
+          s_mine_r[k - done] = u - u0;
+          s_mine_slot[k - done] = slot;
         }
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        half8_t ph, pl;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const half2_t hl = split_f16(sacc[kc >> 1][8 * (kc & 1) + e]);
-          ph[e] = hl[0];
-          pl[e] = hl[1];
-        }
-        half8_t ah[DT], al[DT];
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          ah[dt] = vfrag(vhi, 32 * dt + ql, 2 * kc + hf);
-          al[dt] = vfrag(vlo, 32 * dt + ql, 2 * kc + hf);
-        }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[dt], ph, oacc[dt], 0, 0, 0);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[dt], pl, oacc[dt], 0, 0, 0);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[dt], ph, oacc[dt], 0, 0, 0);
       }
+      base += total;
     }
-    const float l_tot = l + __shfl_xor(l, 32, 64);
-    if (n_ranges == 1) {  // the whole key range: the output directly
-      if (active) {
-        const float inv = 1.0f / l_tot;
-        float* orow = out + (t * n_heads + head) * HD;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int d = 32 * dt + 8 * i + 4 * hf;
-            *reinterpret_cast<float4*>(orow + d) = make_float4(oacc[dt][4 * i] * inv, oacc[dt][4 * i + 1] * inv,
-                                                               oacc[dt][4 * i + 2] * inv, oacc[dt][4 * i + 3] * inv);
+    __syncthreads();
+    const uint32_t mine = base > b ? (base - b + G - 1) / G : 0u;  // this workgroup's units in all
+    const uint32_t batch = mine > done ? min(mine - done, uint32_t(kPreciseBatch)) : 0u;
+    for (uint32_t kb = 0; kb < batch; ++kb) {
+      const uint32_t it = s_mine_e[kb];
+      const int range = int(s_mine_r[kb]);
+      const uint32_t slot = s_mine_slot[kb];
+      const int tile = int(slot / uint32_t(n_kv)), g = int(slot % uint32_t(n_kv));
+      const int64_t pb0 = int64_t(tile) * kRowsPerBlock, wp0 = pb0 + wave * kRowsPerWave;
+      const int64_t p = wp0 + ql;
+      const bool active = p < P;
+      const int64_t t = active ? p / group : 0;
+      const int head = g * group + (active ? int(p % group) : 0);
+      const int64_t qpos = pos0 + t;
+      const int64_t kend = pos0 + (min(pb0 + kRowsPerBlock, P) - 1) / group + 1;
+      const int ntk = int((kend + kBN - 1) / kBN);
+      // this unit's key tiles: range `range` of the tile's ntk tiles in n_ranges contiguous ranges of at least
+      // kPreciseMinTiles tiles (a short tile is one range)
+      const int per = entry_per(ntk), n_ranges = (ntk + per - 1) / per;
+      const int kt0 = range * per, kt1 = min(ntk, kt0 + per);
+      const bool wave_active = wp0 < P;
+      const int64_t wave_kend = wave_active ? pos0 + (min(wp0 + kRowsPerWave, P) - 1) / group + 1 : 0;
+      const int64_t wave_kfull = wave_active ? pos0 + wp0 / group + 1 : 0;
+
+      // Q (rotated on load when q_rope is given, as the prefill kernel does), scaled, split.
+      half8_t qh[DC], qlw[DC];
+      {
+        const float* qrow = q + (t * n_heads + head) * HD;
+        float x[DC][8];
+  #pragma unroll
+        for (int c = 0; c < DC; ++c) {
+          float4 a = make_float4(0.f, 0.f, 0.f, 0.f), bb = a;
+          if (active) {
+            a = *reinterpret_cast<const float4*>(qrow + 16 * c + 8 * hf);
+            bb = *reinterpret_cast<const float4*>(qrow + 16 * c + 8 * hf + 4);
+          }
+          x[c][0] = a.x, x[c][1] = a.y, x[c][2] = a.z, x[c][3] = a.w;
+          x[c][4] = bb.x, x[c][5] = bb.y, x[c][6] = bb.z, x[c][7] = bb.w;
+        }
+        if (q_rope && active) {
+          const float2* cs = q_rope + qpos * (HD / 2);
+          if (q_rope_neox) {
+  #pragma unroll
+            for (int c = 0; c < DC / 2; ++c)
+  #pragma unroll
+              for (int e = 0; e < 8; ++e) rope_rotate(x[c][e], x[c + DC / 2][e], cs[16 * c + 8 * hf + e]);
+          } else {
+  #pragma unroll
+            for (int c = 0; c < DC; ++c)
+  #pragma unroll
+              for (int e = 0; e < 8; e += 2) rope_rotate(x[c][e], x[c][e + 1], cs[(16 * c + 8 * hf + e) / 2]);
+          }
+        }
+  #pragma unroll
+        for (int c = 0; c < DC; ++c)
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const half2_t hl = split_f16(x[c][e] * qscale);
+            qh[c][e] = hl[0];
+            qlw[c][e] = hl[1];
           }
       }
-      continue;
-    }
-    // A partial: rows of the tile as [128][HD + 2] (weighted V, then shift and sum) in the unit's workspace slot.
-    float* part = ws + (int64_t(it) * ps + range) * kRowsPerBlock * (HD + 2);
-    {
-      float* prow = part + int64_t(wave * kRowsPerWave + ql) * (HD + 2);
-#pragma unroll
+
+      floatx16 oacc[DT];
+  #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d = 32 * dt + 8 * i + 4 * hf;
-          *reinterpret_cast<float4*>(prow + d) =
-              make_float4(oacc[dt][4 * i], oacc[dt][4 * i + 1], oacc[dt][4 * i + 2], oacc[dt][4 * i + 3]);
+  #pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+      float m = -INFINITY, l = 0.f;
+
+      // One key tile's fp32 K rows (float4 (key, 4 dims)) and V pairs (keys 2j, 2j+1 x 8 dims), held in registers one
+      // tile ahead of the compute; rows past the call's last valid row are zeros (and masked).
+      float4 kr[K_F4], va[V_U][2], vb[V_U][2];
+      auto fetch = [&](int kt) {
+        const int64_t r0 = int64_t(kt) * kBN;
+  #pragma unroll
+        for (int i = 0; i < K_F4; ++i) {
+          const int f = threadIdx.x + THREADS * i, r = f / (HD / 4), c4 = f % (HD / 4);
+          kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (r0 + r < rows_valid) kr[i] = ld4(kc + (r0 + r) * row_stride + g * HD + 4 * c4);
         }
-      if (hf == 0) {
-        prow[HD] = l_tot > 0.f ? m : -INFINITY;  // a range with no visible key must not raise the merged max
-        prow[HD + 1] = l_tot;
+  #pragma unroll
+        for (int i = 0; i < V_U; ++i) {
+          const int uu = threadIdx.x + THREADS * i, db = uu % (HD / 8), j = uu / (HD / 8);
+          const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+          va[i][0] = va[i][1] = vb[i][0] = vb[i][1] = z;
+          const int64_t ra = r0 + 2 * j;
+          if (ra < rows_valid) {
+            const KVT* src = vc + ra * row_stride + g * HD + 8 * db;
+            va[i][0] = ld4(src);
+            va[i][1] = ld4(src + 4);
+          }
+          if (ra + 1 < rows_valid) {
+            const KVT* src = vc + (ra + 1) * row_stride + g * HD + 8 * db;
+            vb[i][0] = ld4(src);
+            vb[i][1] = ld4(src + 4);
+          }
+        }
+      };
+      // The fetched tile, split, into LDS: K rows at their swizzled chunks, V^T as key pairs in the vt_key order
+      // (vt_key is its own inverse: the position of key 2j, with 2j + 1 next to it).
+      auto stage = [&]() {
+  #pragma unroll
+        for (int i = 0; i < K_F4; ++i) {
+          const int f = threadIdx.x + THREADS * i, r = f / (HD / 4), c4 = f % (HD / 4);
+          const half2_t sx = split_f16(kr[i].x), sy = split_f16(kr[i].y), sz = split_f16(kr[i].z), sw = split_f16(kr[i].w);
+          const int at = r * HD + 8 * ((c4 >> 1) ^ swz<KCPR>(r)) + 4 * (c4 & 1);
+          *reinterpret_cast<half4_t*>(&khi[at]) = half4_t{sx[0], sy[0], sz[0], sw[0]};
+          *reinterpret_cast<half4_t*>(&klo[at]) = half4_t{sx[1], sy[1], sz[1], sw[1]};
+        }
+  #pragma unroll
+        for (int i = 0; i < V_U; ++i) {
+          const int uu = threadIdx.x + THREADS * i, db = uu % (HD / 8), j = uu / (HD / 8);
+          const int pos = vt_key(2 * j);
+          const float a8[8] = {va[i][0].x, va[i][0].y, va[i][0].z, va[i][0].w, va[i][1].x, va[i][1].y, va[i][1].z,
+                               va[i][1].w};
+          const float b8[8] = {vb[i][0].x, vb[i][0].y, vb[i][0].z, vb[i][0].w, vb[i][1].x, vb[i][1].y, vb[i][1].z,
+                               vb[i][1].w};
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int d = 8 * db + e;
+            const half2_t sa = split_f16(a8[e]), sb = split_f16(b8[e]);
+            const int at = d * kBN + 8 * ((pos >> 3) ^ swz<VCPR>(d)) + (pos & 7);
+            *reinterpret_cast<half2_t*>(&vhi[at]) = half2_t{sa[0], sb[0]};
+            *reinterpret_cast<half2_t*>(&vlo[at]) = half2_t{sa[1], sb[1]};
+          }
+        }
+      };
+      auto kfrag = [&](const _Float16* base, int r, int x) {
+        return *reinterpret_cast<const half8_t*>(&base[r * HD + 8 * (x ^ swz<KCPR>(r))]);
+      };
+      auto vfrag = [&](const _Float16* base, int d, int x) {
+        return *reinterpret_cast<const half8_t*>(&base[d * kBN + 8 * (x ^ swz<VCPR>(d))]);
+      };
+
+      fetch(kt0);
+      for (int kt = kt0; kt < kt1; ++kt) {
+        __syncthreads();  // every wave is done with the previous tile (or unit) in LDS
+        stage();
+        __syncthreads();
+        if (kt + 1 < kt1) fetch(kt + 1);  // in flight while this tile is computed
+        const int64_t r0 = int64_t(kt) * kBN;
+        if (!(wave_active && r0 < wave_kend)) continue;
+        floatx16 sacc[2];
+  #pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) sacc[kk][r] = 0.f;
+        // consecutive MFMAs go to the two halves' independent accumulators
+  #pragma unroll
+        for (int c = 0; c < DC; ++c) {
+          half8_t ah[2], al[2];
+  #pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+            ah[kk] = kfrag(khi, kk * 32 + ql, 2 * c + hf);
+            al[kk] = kfrag(klo, kk * 32 + ql, 2 * c + hf);
+          }
+  #pragma unroll
+          for (int kk = 0; kk < 2; ++kk) sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[kk], qh[c], sacc[kk], 0, 0, 0);
+  #pragma unroll
+          for (int kk = 0; kk < 2; ++kk) sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[kk], qlw[c], sacc[kk], 0, 0, 0);
+  #pragma unroll
+          for (int kk = 0; kk < 2; ++kk) sacc[kk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[kk], qh[c], sacc[kk], 0, 0, 0);
+        }
+        if (r0 + kBN > wave_kfull) {
+          const int64_t rel64 = active ? qpos - r0 : -1;
+          const int rel = int(rel64 < kBN ? rel64 : kBN);
+  #pragma unroll
+          for (int kk = 0; kk < 2; ++kk)
+  #pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if (kk * 32 + 8 * (r / 4) + 4 * hf + (r % 4) > rel) sacc[kk][r] = -INFINITY;
+        }
+        float mt = -INFINITY;
+  #pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kk][r]);
+        const float mn = fmaxf(m, fmaxf(mt, __shfl_xor(mt, 32, 64)));
+        const float ms = mn == -INFINITY ? 0.0f : mn;
+        if (__builtin_amdgcn_ballot_w64(mn > m) != 0) {
+          const float corr = exp2_raw(m - ms);  // m = -inf: 0, and o, l are still 0
+          l *= corr;
+  #pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+  #pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
+        }
+        m = mn;
+  #pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            sacc[kk][r] = exp2_raw(sacc[kk][r] - ms);
+            l += sacc[kk][r];
+          }
+  #pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+          half8_t ph, pl;
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const half2_t hl = split_f16(sacc[kc >> 1][8 * (kc & 1) + e]);
+            ph[e] = hl[0];
+            pl[e] = hl[1];
+          }
+          half8_t ah[DT], al[DT];
+  #pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            ah[dt] = vfrag(vhi, 32 * dt + ql, 2 * kc + hf);
+            al[dt] = vfrag(vlo, 32 * dt + ql, 2 * kc + hf);
+          }
+  #pragma unroll
+          for (int dt = 0; dt < DT; ++dt) oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[dt], ph, oacc[dt], 0, 0, 0);
+  #pragma unroll
+          for (int dt = 0; dt < DT; ++dt) oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[dt], pl, oacc[dt], 0, 0, 0);
+  #pragma unroll
+          for (int dt = 0; dt < DT; ++dt) oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[dt], ph, oacc[dt], 0, 0, 0);
+        }
       }
-    }
-    // Arrive; the last range of the tile merges. Release the partial before counting, acquire the others after.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (threadIdx.x == 0) arrival = atomicAdd(&arrivals[it], 1u);
-    __syncthreads();
-    if (arrival != uint32_t(n_ranges - 1)) continue;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    const float* p0 = ws + int64_t(it) * ps * kRowsPerBlock * (HD + 2);
-    // Each row's weights 2^(m_r - M) / L over the ranges, every range's (m, l) loaded at once (one row per thread).
-    if (threadIdx.x < kRowsPerBlock) {
-      const int r = threadIdx.x;
-      float2 ml[kPreciseMaxRanges];
-#pragma unroll
-      for (int rg = 0; rg < kPreciseMaxRanges; ++rg)
-        ml[rg] = rg < n_ranges ? *reinterpret_cast<const float2*>(p0 + (int64_t(rg) * kRowsPerBlock + r) * (HD + 2) + HD)
-                               : make_float2(-INFINITY, 0.f);
-      float mx = -INFINITY;
-#pragma unroll
-      for (int rg = 0; rg < kPreciseMaxRanges; ++rg) mx = fmaxf(mx, ml[rg].x);
-      const float msh = mx == -INFINITY ? 0.0f : mx;
-      float lsum = 0.f;
-#pragma unroll
-      for (int rg = 0; rg < kPreciseMaxRanges; ++rg) {
-        ml[rg].x = exp2_raw(ml[rg].x - msh);
-        lsum += ml[rg].y * ml[rg].x;
+      const float l_tot = l + __shfl_xor(l, 32, 64);
+      if (n_ranges == 1) {  // the whole key range: the output directly
+        if (active) {
+          const float inv = 1.0f / l_tot;
+          float* orow = out + (t * n_heads + head) * HD;
+  #pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int d = 32 * dt + 8 * i + 4 * hf;
+              *reinterpret_cast<float4*>(orow + d) = make_float4(oacc[dt][4 * i] * inv, oacc[dt][4 * i + 1] * inv,
+                                                                 oacc[dt][4 * i + 2] * inv, oacc[dt][4 * i + 3] * inv);
+            }
+        }
+        continue;
       }
-      const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;  // 0: a row past the call's last (never written out)
-#pragma unroll
-      for (int rg = 0; rg < kPreciseMaxRanges; ++rg)
-        if (rg < n_ranges) merge_w[rg][r] = ml[rg].x * inv;
-    }
-    __syncthreads();
-    // The weighted rows: every thread's ITEMS (row, float4 column) pairs, one range after another, the items' loads
-    // of a range in flight together.
-    constexpr int V4 = HD / 4, ITEMS = kRowsPerBlock * V4 / THREADS;
-    static_assert(ITEMS * THREADS == kRowsPerBlock * V4, "merge items split evenly over the threads");
-    float4 acc[ITEMS];
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int rg = 0; rg < n_ranges; ++rg) {
-      float4 o[ITEMS];
-#pragma unroll
+      // A partial: rows of the tile as [128][HD + 2] (weighted V, then shift and sum) in the unit's workspace slot.
+      float* part = ws + (int64_t(it) * ps + range) * kRowsPerBlock * (HD + 2);
+      {
+        float* prow = part + int64_t(wave * kRowsPerWave + ql) * (HD + 2);
+  #pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int d = 32 * dt + 8 * i + 4 * hf;
+            *reinterpret_cast<float4*>(prow + d) =
+                make_float4(oacc[dt][4 * i], oacc[dt][4 * i + 1], oacc[dt][4 * i + 2], oacc[dt][4 * i + 3]);
+          }
+        if (hf == 0) {
+          prow[HD] = l_tot > 0.f ? m : -INFINITY;  // a range with no visible key must not raise the merged max
+          prow[HD + 1] = l_tot;
+        }
+      }
+      // Arrive; the last range of the tile merges. Release the partial before counting, acquire the others after.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __syncthreads();
+      if (threadIdx.x == 0) arrival = atomicAdd(&arrivals[it], 1u);
+      __syncthreads();
+      if (arrival != uint32_t(n_ranges - 1)) continue;
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      const float* p0 = ws + int64_t(it) * ps * kRowsPerBlock * (HD + 2);
+      // Each row's weights 2^(m_r - M) / L over the ranges, every range's (m, l) loaded at once (one row per thread).
+      if (threadIdx.x < kRowsPerBlock) {
+        const int r = threadIdx.x;
+        float2 ml[kPreciseMaxRanges];
+  #pragma unroll
+        for (int rg = 0; rg < kPreciseMaxRanges; ++rg)
+          ml[rg] = rg < n_ranges ? *reinterpret_cast<const float2*>(p0 + (int64_t(rg) * kRowsPerBlock + r) * (HD + 2) + HD)
+                                 : make_float2(-INFINITY, 0.f);
+        float mx = -INFINITY;
+  #pragma unroll
+        for (int rg = 0; rg < kPreciseMaxRanges; ++rg) mx = fmaxf(mx, ml[rg].x);
+        const float msh = mx == -INFINITY ? 0.0f : mx;
+        float lsum = 0.f;
+  #pragma unroll
+        for (int rg = 0; rg < kPreciseMaxRanges; ++rg) {
+          ml[rg].x = exp2_raw(ml[rg].x - msh);
+          lsum += ml[rg].y * ml[rg].x;
+        }
+        const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;  // 0: a row past the call's last (never written out)
+  #pragma unroll
+        for (int rg = 0; rg < kPreciseMaxRanges; ++rg)
+          if (rg < n_ranges) merge_w[rg][r] = ml[rg].x * inv;
+      }
+      __syncthreads();
+      // The weighted rows: every thread's ITEMS (row, float4 column) pairs, one range after another, the items' loads
+      // of a range in flight together.
+      constexpr int V4 = HD / 4, ITEMS = kRowsPerBlock * V4 / THREADS;
+      static_assert(ITEMS * THREADS == kRowsPerBlock * V4, "merge items split evenly over the threads");
+      float4 acc[ITEMS];
+  #pragma unroll
+      for (int j = 0; j < ITEMS; ++j) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int rg = 0; rg < n_ranges; ++rg) {
+        float4 o[ITEMS];
+  #pragma unroll
+        for (int j = 0; j < ITEMS; ++j) {
+          const int idx = int(threadIdx.x) + THREADS * j, r = idx / V4, c4 = idx % V4;
+          o[j] = *reinterpret_cast<const float4*>(p0 + (int64_t(rg) * kRowsPerBlock + r) * (HD + 2) + 4 * c4);
+        }
+  #pragma unroll
+        for (int j = 0; j < ITEMS; ++j) {
+          const int idx = int(threadIdx.x) + THREADS * j, r = idx / V4;
+          const float w = merge_w[rg][r];
+          acc[j].x += o[j].x * w;
+          acc[j].y += o[j].y * w;
+          acc[j].z += o[j].z * w;
+          acc[j].w += o[j].w * w;
+        }
+      }
+  #pragma unroll
       for (int j = 0; j < ITEMS; ++j) {
         const int idx = int(threadIdx.x) + THREADS * j, r = idx / V4, c4 = idx % V4;
-        o[j] = *reinterpret_cast<const float4*>(p0 + (int64_t(rg) * kRowsPerBlock + r) * (HD + 2) + 4 * c4);
-      }
-#pragma unroll
-      for (int j = 0; j < ITEMS; ++j) {
-        const int idx = int(threadIdx.x) + THREADS * j, r = idx / V4;
-        const float w = merge_w[rg][r];
-        acc[j].x += o[j].x * w;
-        acc[j].y += o[j].y * w;
-        acc[j].z += o[j].z * w;
-        acc[j].w += o[j].w * w;
+        const int64_t pp = pb0 + r;
+        if (pp >= P) continue;
+        const int64_t tt = pp / group;
+        const int hh = g * group + int(pp % group);
+        reinterpret_cast<float4*>(out + (tt * n_heads + hh) * HD)[c4] = acc[j];
       }
     }
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      const int idx = int(threadIdx.x) + THREADS * j, r = idx / V4, c4 = idx % V4;
-      const int64_t pp = pb0 + r;
-      if (pp >= P) continue;
-      const int64_t tt = pp / group;
-      const int hh = g * group + int(pp % group);
-      reinterpret_cast<float4*>(out + (tt * n_heads + hh) * HD)[c4] = acc[j];
-    }
+    __syncthreads();  // the batch's slots are read; the next batch may overwrite them
+    done += batch;
+    if (done >= mine) break;
   }
 }
 
@@ -1441,8 +1537,8 @@ int prefill_impl(const float* q, const void* k16, const void* vt16, float* out, 
   }
   // The listed row tiles, recomputed with split operands (a persistent launch; nothing to do when none was listed).
   // Key-range partials use the workspace, whose split partials the merge above has consumed.
-  // one workgroup per CU: at its register count (256 VGPRs) that is all that fits at once
-  const int64_t grid = std::min<int64_t>(tiles * n_kv_heads * kPreciseMaxRanges, int64_t(cu_count > 0 ? cu_count : 256));
+  const int64_t grid = std::min<int64_t>(tiles * n_kv_heads * kPreciseMaxRanges,
+                                         int64_t(cu_count > 0 ? cu_count : 256) * NBH_PRECISE_WG_PER_CU);
   return nbhs_timing::launch(NBHS_K_PREFILL_PRECISE,
                              head_dim == 64 ? attn_prefill_precise_kernel<64, KVT> : attn_prefill_precise_kernel<128, KVT>,
                              dim3(unsigned(grid)), dim3(kWaves * 64), s, q + off, k_cache, v_cache, out + off, n_mfma,
