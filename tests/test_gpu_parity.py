@@ -355,6 +355,25 @@ def test_causal_mask_poison(backend, n, pos0):
     assert_parity(clean, cpu_attention(q, k, v, pos0, KV), f"poison case n={n} pos0={pos0}")
 
 
+def test_long_recomputation_list(backend):
+    """A 4352-row prefill at q x 30 (scores ~30 log2) lists nearly every MFMA row tile (at most 1056 of the call's
+    1088: rows 0..127 run in fp32) - more than the precise kernel keeps in registers while it schedules (1024), and
+    more units than workgroups, so its schedule scans the list in several chunks and each workgroup takes several
+    units. Sampled row blocks across the call (the oracle over those rows alone: same keys, pos0 moved to the block)
+    are within the parity tolerance."""
+    H, KV, D, n = 32, 8, 64, 4352
+    rng = np.random.default_rng(4352)
+    q = (rng.standard_normal((n, H, D)) * 30).astype(np.float32)
+    k = rng.standard_normal((n, KV, D)).astype(np.float32)
+    v = rng.standard_normal((n, KV, D)).astype(np.float32)
+    got = gpu_attention(backend, q, k, v, 0, KV)
+    recomputed = backend.prefill_recomputed()
+    assert 1024 < recomputed <= (n - 128) * (H // KV) // 128 * KV, recomputed
+    for r0, r1 in ((128, 160), (1500, 1532), (3000, 3016), (4320, 4352)):
+        ref = cpu_attention(q[r0:r1], k[:r1], v[:r1], r0, KV)
+        assert_parity(got[r0:r1], ref, f"rows {r0}..{r1}")
+
+
 def test_prefill_chunks_match_one_call_and_repeat_bitwise(backend):
     """A prefill split into max_batch chunks (transformer.cpp:135-136) matches one call within tolerance: short
     chunks split each row's keys over several workgroups to fill the chip, and the merged rows differ from the
