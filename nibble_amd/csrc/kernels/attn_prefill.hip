@@ -98,7 +98,7 @@ constexpr int kSplitRec = 6;
 // the fp16 grid, where rounding to nearest erred by up to 1.97e-3 on rows this estimate keeps - it stayed within
 // 1.3 sqrt(var), so an accepted row errs by at most 1.3 / 1.5 of the bar. The model is statistical: values placed
 // on purpose at the largest stochastic-rounding variance in every dimension make sqrt(var) tight, and the largest
-// of a row's dimensions can then exceed 1.5 sqrt(var) (emulated: up to 1.07e-3 on 2 of 300 such rows kept);
+// of a row's dimensions can then exceed 1.5 sqrt(var) (emulated: up to 1.18e-3 on 4 of 300 such rows kept);
 // set_attention_fp32 routes every row through fp32 for callers that need the bar for any input.
 constexpr float kEstZ = 1.5f;
 constexpr float kEstBudget = 1e-3f;

@@ -553,3 +553,38 @@ def test_shared_outlier_channels():
     assert worst_small < 0.95, worst_small
     assert worst_kept <= 6e-4, worst_kept
     assert n_kept > 0
+
+
+def max_variance_rows(seed, count):
+    """Adversarial values: every V element 0.45-0.55 fp16 ulp above a grid point in [4, 5) (the largest
+    stochastic-rounding variance, ulp^2 / 4, in every dimension), with 8-200 keys aligned with the query carrying most
+    of the weight. sqrt(var), built from the largest |v| and a bound u^2 x^2 on each rounding's variance, is then
+    tight, and the largest of a row's dimensions can exceed 1.5 sqrt(var)."""
+    rng = np.random.default_rng(seed)
+    for i in range(count):
+        hd = (64, 128)[i % 2]
+        n = int(rng.choice([300, 1000, 2048]))
+        q = rng.standard_normal(hd)
+        k = rng.standard_normal((n, hd))
+        m = rng.integers(0, 256, (n, hd))
+        v = rng.choice([-1, 1], (n, hd)) * (4 + (m + 0.5 + rng.uniform(-0.05, 0.05, (n, hd))) / 256)
+        neff = int(rng.choice([8, 12, 16, 24, 32, 64, 200]))
+        hot = rng.choice(n, neff, replace=False)
+        k[hot] = q / np.linalg.norm(q) * np.sqrt(hd) * 1.5 + 0.3 * rng.standard_normal((neff, hd))
+        yield q, k, v
+
+
+def test_values_at_the_largest_rounding_variance_are_the_estimates_limit():
+    """The estimate's documented limit, pinned: on max_variance_rows rows the estimate keeps err by at most 1.25e-3
+    (measured: 4 of 300 kept rows over the bar, the worst 1.18e-3; rounding to nearest keeps 33 over it). Callers
+    that need the bar for such data use the fp32 route."""
+    worst_kept, over, over_rn = 0.0, 0, 0
+    for q, k, v in max_variance_rows(7, 300):
+        err, qh, p, l, o = emulate(q, k, v)
+        if kept(estimate(qh, k, v, p, l, o)):
+            worst_kept = max(worst_kept, err)
+            over += err > BUDGET
+        err0, qh, p, l, o = emulate(q, k, v, sr=False)
+        over_rn += kept(estimate(qh, k, v, p, l, o, sr=False)) and err0 > BUDGET
+    print(f"kept rows over the bar: {over} (worst {worst_kept:.2e}); rounding to nearest: {over_rn}")
+    assert worst_kept <= 1.25e-3 and over <= 6 and over_rn > over
