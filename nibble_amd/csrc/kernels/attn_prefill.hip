@@ -101,6 +101,11 @@ constexpr int kSplitRec = 6;
 // of a row's dimensions can then exceed 1.5 sqrt(var) (emulated: up to 1.18e-3 on 4 of 300 such rows kept);
 // set_attention_fp32 routes every row through fp32 for callers that need the bar for any input.
 constexpr float kEstZ = 1.5f;
+// A row whose weights are all (nearly) equal - keys * sum p^2 <= (sum p)^2 (1 + kFlatTol), equality exactly when
+// every weight is the same - has lost its scores' differences to the weights' rounding (a near-zero query: every
+// weight rounds to the same fp16 value), an error the variance model does not see and that does not shrink with the
+// output when the values cancel. Such rows are recomputed. Rows of ordinary scores sit far above the threshold.
+constexpr float kFlatTol = 1.0f / 4096.0f;
 constexpr float kEstBudget = 1e-3f;
 constexpr double kEstU = 1.0 / 2048.0;
 constexpr double kLn2 = 0.6931471805599453;
@@ -735,7 +740,8 @@ void attn_prefill_kernel(
     const float est =
         l2_tot / (l_tot * l_tot) * (est_c1 * qn2[qb] * kmx * (vg2 + om2) + est_cv * vg2 + est_co * om2);
     const float rk = est_c3 * sqrtf(qr2[qb] * kmx);  // the query residual's bound, per unit of (V + O)
-    flag = flag || (n_split == 1 && active[qb] && l_tot > 0.f && !(sqrtf(est) + rk * (vmx + om) <= 1.0f));
+    const bool flat = l2_tot * float(qpos[qb] + 1) <= l_tot * l_tot * (1.0f + kFlatTol);
+    flag = flag || (n_split == 1 && active[qb] && l_tot > 0.f && (flat || !(sqrtf(est) + rk * (vmx + om) <= 1.0f)));
     if (n_split > 1 && active[qb] && hf == 0) {
       // a key split judges nothing alone (few keys look sharp): its terms go to the merge, which estimates the row
       float* rec = ws_ml + ((t[qb] * n_heads + head[qb]) * n_split + split) * kSplitRec;
@@ -1262,7 +1268,7 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
                                                            const float* __restrict__ ws_ml, float* __restrict__ out,
                                                            int64_t rows_heads, int n_split, int n_heads, int group,
                                                            uint32_t* __restrict__ aux, int aux_cap, float est_cv,
-                                                           float est_co) {
+                                                           float est_co, int64_t row_pos0) {
   constexpr int V4 = HD / 4;
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i >= rows_heads * V4) return;  // whole rows only: rows_heads * V4 is a multiple of V4, and V4 divides 256
@@ -1316,8 +1322,9 @@ __global__ __launch_bounds__(256) void prefill_split_merge(const float* __restri
   for (int m = 1; m < V4; m <<= 1) om = fmaxf(om, __shfl_xor(om, m, 64));  // over the row's V4 lanes
   const float om2 = om * om;
   const float est = l2 * inv * inv * (a * (b + om2) + est_cv * b + est_co * om2);
-  if (c4 == 0 && l > 0.f && !(sqrtf(est) + rk * (sqrtf(b) + om) <= 1.0f)) {
-    const int64_t t = rh / n_heads;
+  const int64_t t = rh / n_heads;
+  const bool flat = l2 * float(row_pos0 + t + 1) <= l * l * (1.0f + kFlatTol);  // see kFlatTol
+  if (c4 == 0 && l > 0.f && (flat || !(sqrtf(est) + rk * (sqrtf(b) + om) <= 1.0f))) {
     const int head = int(rh % n_heads), g = head / group;
     const int64_t p = t * group + head % group;
     const uint32_t ep = aux[1], slot = uint32_t(p / kRowsPerBlock) * uint32_t(n_heads / group) + uint32_t(g);
@@ -1532,7 +1539,7 @@ int prefill_impl(const float* q, const void* k16, const void* vt16, float* out, 
     e = nbhs_timing::launch(NBHS_K_DECODE_COMBINE, head_dim == 64 ? split_merge_for<64>(sp) : split_merge_for<128>(sp),
                             dim3(unsigned((threads + 255) / 256)), dim3(256), s, ws_o, ws_ml, out + off,
                             n_mfma * n_heads, sp, int(n_heads), int(group), aux, int(aux_cap), est_cv,
-                            est_co);
+                            est_co, pos0 + fp32_rows);
     if (e != hipSuccess) return e;
   }
   // The listed row tiles, recomputed with split operands (a persistent launch; nothing to do when none was listed).

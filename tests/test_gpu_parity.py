@@ -256,6 +256,89 @@ def test_stochastic_staging_matches_its_restatement(backend):
     assert d_emu <= 3e-5 and d_ref > 4 * d_emu, (d_emu, d_ref)
 
 
+def layer0_prompt(seed, n_tok, vocab, KV, D, vmax):
+    """A first layer's K and V for a prompt over a small vocabulary (Zipf-distributed token ids): each token's
+    hidden state is its embedding, so K rows (before RoPE) and V rows repeat exactly wherever the token recurs. V is
+    scaled so that its largest element is vmax."""
+    rng = np.random.default_rng(seed)
+    dm = 4 * D
+    emb = rng.standard_normal((vocab, dm))
+    toks = np.minimum(rng.zipf(1.3, n_tok) - 1, vocab - 1)
+    wk = rng.standard_normal((dm, KV * D)) / np.sqrt(dm)
+    wv = 0.5 * wk + 0.5 * rng.standard_normal((dm, KV * D)) / np.sqrt(dm)
+    k = (emb[toks] @ wk).reshape(n_tok, KV, D)
+    v = (emb[toks] @ wv).reshape(n_tok, KV, D)
+    v *= vmax / np.abs(v).max()
+    return toks, k.astype(np.float32), v.astype(np.float32)
+
+
+@pytest.mark.parametrize("vmax", [2.0, 6.0])
+def test_repeated_tokens_of_a_first_layer(backend, vmax):
+    """A 2048-token prompt over a 40-token vocabulary through append_rope_attention in four 512-row chunks (Llama-3
+    RoPE on q and the new keys): every V row of a token is the same wherever it recurs, the keys differ only by
+    their rotation, and the query of a row is its own token's projection. Rounded to nearest, such values would
+    carry one error per token into the weighted mean; the stochastic staging keeps each chunk within the parity
+    tolerance of the reference over the rotated rows."""
+    H, KV, D, n, c = 32, 8, 64, 2048, 512
+    base, ff = 5e5, synth.llama3_freq_factors(D, 5e5)
+    toks, kn, vn = layer0_prompt(int(vmax * 10), n, 40, KV, D, vmax)
+    rng = np.random.default_rng(5)
+    dm = 4 * D
+    emb = np.random.default_rng(int(vmax * 10)).standard_normal((40, dm))
+    wq = rng.standard_normal((dm, H * D)) / np.sqrt(dm)
+    q = (emb[toks] @ wq).reshape(n, H, D).astype(np.float32)
+    with Buffers(backend) as B:
+        dq, dkn, dvn = B.upload(q), B.upload(kn), B.upload(vn)
+        dk, dv, do = B.alloc(n * KV * D), B.alloc(n * KV * D), B.alloc(q.size)
+        for p0 in range(0, n, c):
+            print(f"chunk pos0={p0}", flush=True)
+            backend.append_rope_attention(dq.at(p0 * H * D), dk, dv, dkn.at(p0 * KV * D), dvn.at(p0 * KV * D),
+                                          do.at(p0 * H * D), c, p0, H, KV, D, base, False, ff)
+        got = backend.download(do, q.shape)
+        gk, gv = backend.download(dk, kn.shape), backend.download(dv, vn.shape)
+    assert np.array_equal(bits(gk), bits(oracle.rope(kn.copy(), 0, base, False, ff))), "appended K rows"
+    assert np.array_equal(bits(gv), bits(vn)), "appended V rows"
+    qr = oracle.rope(q.copy(), 0, base, False, ff)
+    for p0 in range(0, n, c):
+        ref = cpu_attention(qr[p0:p0 + c], gk[:p0 + c], gv[:p0 + c], p0, KV)
+        assert_parity(got[p0:p0 + c], ref, f"vmax={vmax} chunk {p0}")
+
+
+@pytest.mark.parametrize("mag", [10.0, 20.0, 40.0])
+def test_keys_with_outlier_channels(backend, mag):
+    """Keys sharing two channels of magnitude `mag` (+-20 %) that the query also weights (channels LLM keys carry),
+    512 rows deep in a 2048-row cache: within the parity tolerance of the reference."""
+    H, KV, D, n, pos0 = 32, 8, 64, 512, 1536
+    rng = np.random.default_rng(int(mag))
+    q = rng.standard_normal((n, H, D)).astype(np.float32)
+    k = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+    v = rng.standard_normal((pos0 + n, KV, D)).astype(np.float32)
+    dims = [5, 37]
+    k[:, :, dims] = (mag * (1 + 0.2 * rng.standard_normal((pos0 + n, KV, 2)))).astype(np.float32)
+    q[:, :, dims] = (mag / 8 * rng.choice([-1, 1], (n, H, 2))).astype(np.float32)
+    got = gpu_attention(backend, q, k, v, pos0, KV)
+    assert_parity(got, cpu_attention(q, k, v, pos0, KV), f"outlier channels x{mag}")
+
+
+@pytest.mark.parametrize("qscale", [1e-4, 1e-2])
+def test_flat_scores_with_correlated_values(backend, qscale):
+    """A near-zero query (nearly uniform attention, scores spanning less than one fp16 step of the weights) over K
+    and V projected from shared rank-1 hidden states with values up to 10: the weights' rounding correlates with V;
+    within the parity tolerance of the reference."""
+    H, KV, D, n, pos0 = 32, 8, 64, 512, 1536
+    rng = np.random.default_rng(int(1 / qscale))
+    ctx, dm = pos0 + n, 4 * D
+    h = np.outer(rng.standard_normal(ctx), rng.standard_normal(dm)) + 0.01 * rng.standard_normal((ctx, dm))
+    wk = rng.standard_normal((dm, KV * D)) / np.sqrt(dm)
+    k = (h @ wk).reshape(ctx, KV, D)
+    v = (h @ wk).reshape(ctx, KV, D)
+    v = (v * (10.0 / np.abs(v).max())).astype(np.float32)
+    k = k.astype(np.float32)
+    q = (rng.standard_normal((n, H, D)) * qscale).astype(np.float32)
+    got = gpu_attention(backend, q, k, v, pos0, KV)
+    assert_parity(got, cpu_attention(q, k, v, pos0, KV), f"flat scores q x {qscale}")
+
+
 @pytest.mark.parametrize("case", make_golden.REPEAT_CASES, ids=[c[0] for c in make_golden.REPEAT_CASES])
 def test_attention_golden_repeated_values_through_fused_append(backend, case):
     """The repeated-value cases through append_rope_attention (Llama-3 RoPE on q and the new keys; V rows are
