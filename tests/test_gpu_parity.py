@@ -339,6 +339,52 @@ def test_flat_scores_with_correlated_values(backend, qscale):
     assert_parity(got, cpu_attention(q, k, v, pos0, KV), f"flat scores q x {qscale}")
 
 
+def structured_case(seed):
+    """One seeded mix of the structures the prefill route's error estimate must cover: query scale 1e-3 .. 10, keys
+    N(0,1) / from shared low-rank hidden states / with two outlier channels, values N(0,1) / correlated with the keys
+    / repeated in runs / offset by 3 / scaled by 8, at several depths, head groupings and head sizes."""
+    rng = np.random.default_rng(1000 + seed)
+    H, KV = [(32, 8), (14, 2), (8, 2)][seed % 3]
+    D = (64, 128)[(seed // 3) % 2]
+    n = int(rng.choice([160, 256, 512]))
+    pos0 = int(rng.choice([0, 384, 1536]))
+    ctx, dm = pos0 + n, 4 * D
+    qs = float(rng.choice([1e-3, 0.3, 1.0, 3.0, 10.0]))
+    kkind = rng.choice(["n01", "lowrank", "outlier"])
+    vkind = rng.choice(["n01", "corr", "runs", "offset", "big"])
+    h = rng.standard_normal((ctx, 2)) @ rng.standard_normal((2, dm)) + 0.1 * rng.standard_normal((ctx, dm))
+    wk = rng.standard_normal((dm, KV * D)) / np.sqrt(dm)
+    k = (h @ wk if kkind == "lowrank" else rng.standard_normal((ctx, KV * D))).reshape(ctx, KV, D)
+    if kkind == "outlier":
+        k[:, :, [3, 17]] += 12.0
+    if vkind == "corr":
+        v = (h @ (0.8 * wk + 0.2 * rng.standard_normal((dm, KV * D)) / np.sqrt(dm))).reshape(ctx, KV, D)
+    else:
+        v = rng.standard_normal((ctx, KV, D))
+    if vkind == "runs":
+        for s0 in rng.integers(0, ctx - 32, 8):
+            v[s0:s0 + 32] = v[s0]
+    elif vkind == "offset":
+        v = v + 3.0
+    elif vkind == "big":
+        v = v * 8.0
+    q = rng.standard_normal((n, H, D)) * qs
+    if kkind == "outlier":
+        q[:, :, [3, 17]] += 1.5 * np.sign(rng.standard_normal((n, H, 2)))
+    name = f"seed{seed}: H{H}/KV{KV} D{D} n{n} pos0 {pos0} q x {qs} K {kkind} V {vkind}"
+    return name, q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), pos0, KV
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_structured_inputs_sweep(backend, seed):
+    """Seeded mixes of query scale, key and value structure, depth and head shape (structured_case) through
+    Backend::attention on the default route: within the parity tolerance of the reference."""
+    name, q, k, v, pos0, KV = structured_case(seed)
+    print(name, flush=True)
+    got = gpu_attention(backend, q, k, v, pos0, KV)
+    assert_parity(got, cpu_attention(q, k, v, pos0, KV), name)
+
+
 @pytest.mark.parametrize("case", make_golden.REPEAT_CASES, ids=[c[0] for c in make_golden.REPEAT_CASES])
 def test_attention_golden_repeated_values_through_fused_append(backend, case):
     """The repeated-value cases through append_rope_attention (Llama-3 RoPE on q and the new keys; V rows are
