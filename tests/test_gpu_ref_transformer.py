@@ -150,3 +150,23 @@ def test_reference_transformer_head_dim_64(tmp_path):
     d = float(np.max(np.abs(inv["b512"] - cpu)))
     print(f"hd64 batch-invariant: |hip-cpu| {d:.2e}", flush=True)
     assert d <= 1e-4 * scale
+
+
+@needs_driver
+@pytest.mark.gpu
+def test_reference_transformer_repeated_phrase(tmp_path):
+    """The head_dim-64 model (n_embd 256, llama with rope freqs, F16 weights) on a 600-token prompt that repeats one
+    20-token phrase 30 times: a first layer's value rows repeat exactly wherever a token recurs, and rows 128..599
+    take the MFMA prefill route (one call of 600 rows, and 512-row chunks as the Transformer cuts a prompt). Logits
+    within 1e-3 of the logits' scale of the same forward over the reference's CpuBackend."""
+    m = model_util.tiny_model(11, np.float16, "llama", True, E=256, FF=512, scale=0.25)
+    phrase = np.random.default_rng(8).integers(0, 261, 20).tolist()
+    toks = phrase * 30
+    cpu = run(m, tmp_path, "cpu", toks, ["b1024"], n_ctx=640)["b1024"]
+    scale = max(1.0, float(np.max(np.abs(cpu))))
+    hip = run(m, tmp_path, "hip", toks, ["b1024", "b512"], n_ctx=640)
+    for name, o in hip.items():
+        d = float(np.max(np.abs(o - cpu)))
+        print(f"repeated phrase {name}: |hip-cpu| {d:.2e} (max |logit| {scale:.2f})", flush=True)
+        assert np.all(np.isfinite(o))
+        assert d <= 1e-3 * scale
