@@ -257,8 +257,9 @@ int nbhs_sgemm_xwt(nbhs_blas h, const float* x, const float* w, float* y, int64_
  * row is scaled by a power of two and split into fp16 hi + lo parts (x s = hi + lo to ~2^-22 relative); both are
  * multiplied by the exact fp16 weights with fp32 accumulation, so the result is fp32-grade (within the float
  * summation bound of the reference's sum). ws: device scratch of nbhs_gemm_f16w_workspace(n, in) bytes, 256-byte
- * aligned (the split rows). Requires in % 8 == 0 and 16-byte aligned weights. Deterministic; each weight's tile
- * configuration follows from its own shape, so its outputs do not depend on the other weights of the call. */
+ * aligned (the split rows and a fixed 64 MB area for K-range partial sums). Requires in % 8 == 0 and 16-byte aligned
+ * weights. Deterministic; each weight's tile configuration and K ranges follow from its own shape, so its outputs do
+ * not depend on the other weights of the call. */
 #define NBHS_GEMM_MAX_WEIGHTS 8
 int64_t nbhs_gemm_f16w_workspace(int64_t n, int64_t in);
 int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const int64_t* rows, int64_t in,
@@ -327,7 +328,8 @@ enum nbhs_kernel_id {
   NBHS_K_CALIBRATION = 16,     /* nbhs_mfma_loop_f16 */
   NBHS_K_SPLIT_ACTS = 17,      /* activation rows split into fp16 hi + lo for the F16-weight GEMM */
   NBHS_K_GEMM = 18,            /* F16-weight GEMM (nbhs_gemm_f16w_multi) */
-  NBHS_K_COUNT = 19
+  NBHS_K_GEMM_REDUCE = 19,     /* the F16-weight GEMM's sum of K-range partials */
+  NBHS_K_COUNT = 20
 };
 int nbhs_kernel_timing_enable(int on); /* on != 0: time every kernel; 0: none (clears what was recorded) */
 int nbhs_kernel_timing_select(uint32_t kernel_mask); /* time the kernels whose bit (1 << id) is set; clears */

@@ -415,7 +415,7 @@ class KernelTiming:
     include/nibble_hip_shim.h). Used by the benchmark for roofline figures."""
 
     (ROPE, APPEND_ROPE, DECODE_PARTIAL, DECODE_COMBINE, GENERIC, STAGE_KV, PREFILL_MFMA, GEMV, CONVERT, ADD_BIAS, RMSNORM,
-     ELEMENTWISE, QUANTIZE, QGEMV, QGEMM, PREFILL_PRECISE, CALIBRATION, SPLIT_ACTS, GEMM) = range(19)
+     ELEMENTWISE, QUANTIZE, QGEMV, QGEMM, PREFILL_PRECISE, CALIBRATION, SPLIT_ACTS, GEMM, GEMM_REDUCE) = range(20)
 
     @staticmethod
     def enable(on: bool = True, only: int | None = None):

@@ -37,7 +37,9 @@ struct GemmWeight {
   const _Float16* w;  // [rows, in]
   float* y;           // [n, rows]
   int64_t rows;
-  int tile0;          // first output tile (blockIdx.x) of this weight
+  int tile0;          // first workgroup (blockIdx.x) of this weight
+  int split;          // K ranges (1: the whole K; > 1: partial sums into part, merged by gemm_split_reduce_kernel)
+  float* part;        // [split][n][rows] partial sums when split > 1
 };
 struct GemmBatch {
   GemmWeight w[kMaxWeights];
@@ -152,6 +154,12 @@ constexpr int kSmallBM = 64, kSmallBN = 64, kSmallBK = 64, kSmallStages = 3;
 constexpr int kWideBM = 128, kWideBN = 128, kWideBK = 32, kWideStages = 3;
 constexpr int kPadK = 64;  // K padding of the split activation rows (a multiple of both slice depths)
 constexpr int64_t kWideMinTiles = 256;
+// K ranges of a weight with few 128 x 128 tiles: up to kMaxSplit, each at least kSplitMinKTiles 32-deep slices
+// (1536 elements; measured at 512 rows: an FFN-down projection, K = 8192, 108 -> 80 us in 4 ranges; a QKV one, K =
+// 2048, 38 -> 40 us in 4 ranges of 512, whose partial sums cost more than the halved operand traffic saves, so it is
+// not cut); the partial sums live in a fixed area of the workspace (64 MB), which bounds a split weight's outputs.
+constexpr int kMaxSplit = 4, kSplitMinKTiles = 48;
+constexpr int64_t kSplitPartFloats = int64_t(1) << 24;
 
 template <int BM, int BN, int BK, int STAGES>
 __global__ __launch_bounds__(kThreads) void gemm_f16w_kernel(GemmBatch b, const _Float16* __restrict__ xh,
@@ -168,7 +176,10 @@ __global__ __launch_bounds__(kThreads) void gemm_f16w_kernel(GemmBatch b, const 
   for (int j = 1; j < b.n_w; ++j)
     if (int(blockIdx.x) >= b.w[j].tile0) wi = j;
   const GemmWeight& d = b.w[wi];
-  const int64_t n0 = int64_t(int(blockIdx.x) - d.tile0) * BN, m0 = int64_t(blockIdx.y) * BM;
+  // this workgroup's output tile and K range: workgroups of a split weight are tile-major within each range
+  const int local = int(blockIdx.x) - d.tile0, tiles = int((d.rows + BN - 1) / BN);
+  const int ks = local / tiles;
+  const int64_t n0 = int64_t(local % tiles) * BN, m0 = int64_t(blockIdx.y) * BM;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;  // this wave's rows wm*BM/2.. and weight rows wn*BN/2..
 
@@ -205,8 +216,10 @@ __global__ __launch_bounds__(kThreads) void gemm_f16w_kernel(GemmBatch b, const 
     woff[i] = uint32_t((r * int(in) + 8 * x) * 2);
   }
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int nk_all = int(in_pad / BK), per = (nk_all + d.split - 1) / d.split;
+  const int kb = ks * per;  // this range's first K tile
   auto fetch = [&](int kt, int st) {
-    const uint32_t k0 = uint32_t(kt) * BK;
+    const uint32_t k0 = uint32_t(kb + kt) * BK;
 #pragma unroll
     for (int i = 0; i < XLD; ++i) {
       buffer_load_lds16(rh, &lds[st][(i * 4 + wave_u) * 512], xoff[i] + k0 * 2);
@@ -247,7 +260,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f16w_kernel(GemmBatch b, const 
     for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  const int nk = int(in_pad / BK);
+  const int nk = max(0, min(per, nk_all - kb));  // K tiles of this range
 #pragma unroll
   for (int i = 0; i < STAGES - 1; ++i)
     if (i < nk) fetch(i, i);
@@ -307,7 +320,8 @@ __global__ __launch_bounds__(kThreads) void gemm_f16w_kernel(GemmBatch b, const 
   }
 
   // acc[i][j][r] holds activation row 8 (r / 4) + 4 hf + r % 4 of the wave's block i and weight row lane % 32 of
-  // its block j.
+  // its block j. A K range's partial sums go unscaled to its slice of part.
+  float* const dst = d.split > 1 ? d.part + int64_t(ks) * n * d.rows : d.y;
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int64_t col = n0 + wn * (BN / 2) + 32 * j + (lane & 31);
@@ -317,9 +331,30 @@ __global__ __launch_bounds__(kThreads) void gemm_f16w_kernel(GemmBatch b, const 
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int64_t t = m0 + wm * (BM / 2) + 32 * i + 8 * (r / 4) + 4 * hf + (r % 4);
-          if (t < n) d.y[t * d.rows + col] = acc[i][j][r] * inv_scale[t];
+          if (t < n) dst[t * d.rows + col] = d.split > 1 ? acc[i][j][r] : acc[i][j][r] * inv_scale[t];
         }
     }
+  }
+}
+
+// y = (sum of a split weight's K-range partials, in range order) * 1 / s_t, for every weight of the batch with
+// split > 1: one thread per output, the weights' outputs laid end to end (`first` output of each, in weight order).
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmBatch b, const float* __restrict__ inv_scale,
+                                                                int64_t n, int64_t total) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  int64_t off = 0;
+  for (int j = 0; j < b.n_w; ++j) {
+    const GemmWeight& d = b.w[j];
+    const int64_t cnt = n * d.rows;
+    if (i < off + cnt) {
+      const int64_t o = i - off;
+      float acc = 0.f;
+      for (int s = 0; s < d.split; ++s) acc += d.part[int64_t(s) * cnt + o];
+      d.y[o] = acc * inv_scale[o / d.rows];
+      return;
+    }
+    off += cnt;
   }
 }
 
@@ -332,7 +367,7 @@ extern "C" {
 int64_t nbhs_gemm_f16w_workspace(int64_t n, int64_t in) {
   if (n <= 0 || in <= 0 || n > (int64_t(1) << 31) || in > (int64_t(1) << 30)) return -1;
   const int64_t in_pad = round_up(in, kPadK);
-  return round_up(2 * n * in_pad * 2, 256) + round_up(n * 4, 256);
+  return round_up(2 * n * in_pad * 2, 256) + round_up(n * 4, 256) + kSplitPartFloats * 4;
 }
 
 int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const int64_t* rows, int64_t in,
@@ -344,37 +379,70 @@ int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const i
   const int64_t in_pad = round_up(in, kPadK);
   // every operand a buffer resource addresses must fit 32-bit offsets
   if (kWideBM * in_pad * 2 > INT32_MAX || n > 65535 * int64_t(kSmallBM)) return NBHS_EINVAL;
-  // Each weight's tile configuration follows from its own shape (so its results do not depend on the other weights
-  // of the call: matmul_multi equals separate calls); the weights of each configuration share one launch.
-  GemmBatch wide{}, small{};
-  int64_t wide_tiles = 0, small_tiles = 0;
-  for (int i = 0; i < n_w; ++i) {
-    if (!w[i] || !y[i] || rows[i] <= 0 || reinterpret_cast<uintptr_t>(w[i]) % 16 != 0 ||
-        kWideBN * in * 2 > INT32_MAX)
-      return NBHS_EINVAL;
-    const bool is_wide = (rows[i] + kWideBN - 1) / kWideBN * ((n + kWideBM - 1) / kWideBM) >= kWideMinTiles;
-    GemmBatch& b = is_wide ? wide : small;
-    int64_t& t = is_wide ? wide_tiles : small_tiles;
-    b.w[b.n_w++] = GemmWeight{static_cast<const _Float16*>(w[i]), y[i], rows[i], int(t)};
-    t += (rows[i] + (is_wide ? kWideBN : kSmallBN) - 1) / (is_wide ? kWideBN : kSmallBN);
-    if (t > INT32_MAX) return NBHS_EINVAL;
-  }
   char* base = static_cast<char*>(ws);
   _Float16* xh = reinterpret_cast<_Float16*>(base);
   _Float16* xl = xh + n * in_pad;
   float* inv = reinterpret_cast<float*>(base + round_up(2 * n * in_pad * 2, 256));
+  float* part = reinterpret_cast<float*>(base + round_up(2 * n * in_pad * 2, 256) + round_up(n * 4, 256));
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 ? 1 : 0;
+  const unsigned wide_rows = unsigned((n + kWideBM - 1) / kWideBM), small_rows = unsigned((n + kSmallBM - 1) / kSmallBM);
+  // Each weight's configuration follows from its own shape (so its results do not depend on the other weights of
+  // the call: matmul_multi equals separate calls): 128 x 128 tiles when they alone are many; otherwise, when K is
+  // long and the output fits the partial-sum area, 128 x 128 tiles over 2 or 4 K ranges (each range's workgroup
+  // fetches half the operand bytes per product of a 64 x 64 tile's, and the ranges restore the workgroup count;
+  // the partials are summed in range order); otherwise 64 x 64 tiles. The weights of each configuration share a
+  // launch; split weights share one while their partials fit the area, then the next group starts.
+  GemmBatch wide{}, small{}, split{};
+  int64_t wide_tiles = 0, small_tiles = 0, split_wgs = 0, split_out = 0, part_used = 0;
   hipError_t e = nbhs_timing::launch(NBHS_K_SPLIT_ACTS, split_acts_kernel, dim3(unsigned(n)), dim3(64), s, x, in,
                                      in_pad, xh, xl, inv, vec);
+  auto flush_split = [&]() {
+    if (e != hipSuccess || split.n_w == 0) return;
+    e = nbhs_timing::launch(NBHS_K_GEMM, gemm_f16w_kernel<kWideBM, kWideBN, kWideBK, kWideStages>,
+                            dim3(unsigned(split_wgs), wide_rows), dim3(kThreads), s, split, xh, xl, inv, n, in,
+                            in_pad);
+    if (e == hipSuccess)
+      e = nbhs_timing::launch(NBHS_K_GEMM_REDUCE, gemm_split_reduce_kernel, dim3(unsigned((split_out + 255) / 256)),
+                              dim3(256), s, split, inv, n, split_out);
+    split = GemmBatch{};
+    split_wgs = split_out = part_used = 0;
+  };
+  for (int i = 0; i < n_w && e == hipSuccess; ++i) {
+    if (!w[i] || !y[i] || rows[i] <= 0 || reinterpret_cast<uintptr_t>(w[i]) % 16 != 0 ||
+        kWideBN * in * 2 > INT32_MAX)
+      return NBHS_EINVAL;
+    const int64_t wt = (rows[i] + kWideBN - 1) / kWideBN * wide_rows;
+    int sp = 1;
+    if (wt < kWideMinTiles && n * rows[i] * kMaxSplit <= kSplitPartFloats) {
+      const int64_t nkt = in_pad / kWideBK;
+      while (sp < kMaxSplit && wt * sp < kWideMinTiles && nkt / (2 * sp) >= kSplitMinKTiles) sp *= 2;
+    }
+    const _Float16* wd = static_cast<const _Float16*>(w[i]);
+    if (wt >= kWideMinTiles) {
+      wide.w[wide.n_w++] = GemmWeight{wd, y[i], rows[i], int(wide_tiles), 1, nullptr};
+      wide_tiles += (rows[i] + kWideBN - 1) / kWideBN;
+    } else if (sp > 1) {
+      const int64_t cnt = n * rows[i] * sp;
+      if (part_used + cnt > kSplitPartFloats) flush_split();
+      split.w[split.n_w++] = GemmWeight{wd, y[i], rows[i], int(split_wgs), sp, part + part_used};
+      split_wgs += (rows[i] + kWideBN - 1) / kWideBN * sp;
+      split_out += n * rows[i];
+      part_used += cnt;
+    } else {
+      small.w[small.n_w++] = GemmWeight{wd, y[i], rows[i], int(small_tiles), 1, nullptr};
+      small_tiles += (rows[i] + kSmallBN - 1) / kSmallBN;
+    }
+    if (wide_tiles > INT32_MAX || small_tiles > INT32_MAX || split_wgs > INT32_MAX) return NBHS_EINVAL;
+  }
+  flush_split();
   if (e == hipSuccess && wide.n_w > 0)
     e = nbhs_timing::launch(NBHS_K_GEMM, gemm_f16w_kernel<kWideBM, kWideBN, kWideBK, kWideStages>,
-                            dim3(unsigned(wide_tiles), unsigned((n + kWideBM - 1) / kWideBM)), dim3(kThreads), s,
-                            wide, xh, xl, inv, n, in, in_pad);
+                            dim3(unsigned(wide_tiles), wide_rows), dim3(kThreads), s, wide, xh, xl, inv, n, in, in_pad);
   if (e == hipSuccess && small.n_w > 0)
     e = nbhs_timing::launch(NBHS_K_GEMM, gemm_f16w_kernel<kSmallBM, kSmallBN, kSmallBK, kSmallStages>,
-                            dim3(unsigned(small_tiles), unsigned((n + kSmallBM - 1) / kSmallBM)), dim3(kThreads), s,
-                            small, xh, xl, inv, n, in, in_pad);
+                            dim3(unsigned(small_tiles), small_rows), dim3(kThreads), s, small, xh, xl, inv, n, in,
+                            in_pad);
   return e;
 }
 

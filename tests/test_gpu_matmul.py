@@ -272,3 +272,64 @@ def test_f16_gemm_wide_tiles(backend):
         assert_matmul_close(g, w, x, f"weight {i} ({w.shape[0]} rows)")
         assert np.array_equal(bits(g), bits(sep[i])), f"weight {i}: matmul_multi differs from a separate call"
     backend.release_weights()
+
+
+def multi_vs_separate(backend, ws, x, n):
+    with Buffers(backend) as B:
+        dx = B.upload(x)
+        ys = [B.alloc(n * w.shape[0]) for w in ws]
+        backend.matmul_multi(ws, dx, ys, n)
+        got = [backend.download(y, (n, w.shape[0])) for y, w in zip(ys, ws)]
+        sep = []
+        for w in ws:
+            y1 = B.alloc(n * w.shape[0])
+            backend.matmul(w, dx, y1, n)
+            sep.append(backend.download(y1, (n, w.shape[0])))
+    return got, sep
+
+
+def assert_within_bound(got, w, x, what=""):
+    """got [n, out] within the float-summation bound of the exact product (float64 reference only: for weights too
+    large for the restated reference's scalar loop to run in a test)."""
+    in_ = w.shape[1]
+    x2 = np.asarray(x, np.float64).reshape(-1, in_)
+    w64 = np.asarray(w, np.float64)
+    bound = in_ * U * (np.abs(x2) @ np.abs(w64).T) + 1e-37
+    err = np.abs(got.astype(np.float64) - x2 @ w64.T)
+    print(f"matmul {what}: max |gpu-exact|/bound = {float(np.max(err / bound)):.3f}", flush=True)
+    assert np.all(np.isfinite(got)) and np.all(err <= bound), what
+
+
+def test_f16_gemm_split_k(backend):
+    """Weights with few 128 x 128 tiles and a long K take K ranges (partials summed in range order): 700 and 90 rows at
+    n = 300, in = 8200 (4 ranges of 65, 65, 65 and 63 slices; partial activation, weight and K tiles), in one call
+    with a 12000-row weight (128 x 128 tiles, no ranges). Within the summation bound (the split weights also against
+    the restated reference), and matmul_multi equals separate calls bit for bit (each weight's configuration follows
+    from its own shape, backend.h:57)."""
+    rng = np.random.default_rng(29)
+    n, in_ = 300, 8200
+    ws = [rand(rng, (r, in_), np.float16, 0.3) for r in (700, 90, 12000)]
+    x = rand(rng, (n, in_))
+    got, sep = multi_vs_separate(backend, ws, x, n)
+    for i, (g, w) in enumerate(zip(got, ws)):
+        if w.shape[0] < 1000:
+            assert_matmul_close(g, w, x, f"weight {i} ({w.shape[0]} rows)")
+        else:
+            assert_within_bound(g, w, x, f"weight {i} ({w.shape[0]} rows)")
+        assert np.array_equal(bits(g), bits(sep[i])), f"weight {i}: matmul_multi differs from a separate call"
+    backend.release_weights()
+
+
+def test_f16_gemm_split_k_groups(backend):
+    """Three 9000-row weights at n = 300, in = 4160, each in 2 K ranges: their partial sums (5.4M floats each) exceed
+    the 16M-float partial area together, so the call runs them as two groups (two weights, then one). Within the
+    summation bound, and equal to separate calls bit for bit."""
+    rng = np.random.default_rng(31)
+    n, in_ = 300, 4160
+    ws = [rand(rng, (9000, in_), np.float16, 0.3) for _ in range(3)]
+    x = rand(rng, (n, in_))
+    got, sep = multi_vs_separate(backend, ws, x, n)
+    for i, (g, w) in enumerate(zip(got, ws)):
+        assert_within_bound(g, w, x, f"weight {i}")
+        assert np.array_equal(bits(g), bits(sep[i])), f"weight {i}: matmul_multi differs from a separate call"
+    backend.release_weights()
