@@ -378,7 +378,12 @@ int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const i
   if (need < 0 || ws_bytes < need || reinterpret_cast<uintptr_t>(ws) % 256 != 0) return NBHS_EINVAL;
   const int64_t in_pad = round_up(in, kPadK);
   // every operand a buffer resource addresses must fit 32-bit offsets
-  if (kWideBM * in_pad * 2 > INT32_MAX || n > 65535 * int64_t(kSmallBM)) return NBHS_EINVAL;
+  if (kWideBM * in_pad * 2 > INT32_MAX || kWideBN * in * 2 > INT32_MAX || n > 65535 * int64_t(kSmallBM))
+    return NBHS_EINVAL;
+  // every weight is checked before anything is launched, so a rejected call writes no output
+  for (int i = 0; i < n_w; ++i)
+    if (!w[i] || !y[i] || rows[i] <= 0 || rows[i] > INT32_MAX || reinterpret_cast<uintptr_t>(w[i]) % 16 != 0)
+      return NBHS_EINVAL;
   char* base = static_cast<char*>(ws);
   _Float16* xh = reinterpret_cast<_Float16*>(base);
   _Float16* xl = xh + n * in_pad;
@@ -409,9 +414,6 @@ int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const i
     split_wgs = split_out = part_used = 0;
   };
   for (int i = 0; i < n_w && e == hipSuccess; ++i) {
-    if (!w[i] || !y[i] || rows[i] <= 0 || reinterpret_cast<uintptr_t>(w[i]) % 16 != 0 ||
-        kWideBN * in * 2 > INT32_MAX)
-      return NBHS_EINVAL;
     const int64_t wt = (rows[i] + kWideBN - 1) / kWideBN * wide_rows;
     int sp = 1;
     if (wt < kWideMinTiles && n * rows[i] * kMaxSplit <= kSplitPartFloats) {
