@@ -613,12 +613,15 @@ __global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* 
 
 // ---- the tiled matmul for longer calls (prefill chunks) ----
 //
-// qgemm_legacy_kernel: a 256-thread workgroup computes 64 weight rows x 64 activation rows; thread (ri, ti) owns rows
-// ri + 16i and activation rows ti + 16j (i, j < 4). Chunks of 8 blocks of both operands are staged in LDS; each
-// thread walks the chunk's blocks in order and adds each block's term to its 16 sums, so every output is the
-// reference's ordered sum (the same terms as qgemv_kernel, the same bits). One launch covers the weights of one
-// type that share the input (a layer's Q, K and V): grid x runs over the row tiles of all of them, so small
-// weights do not leave most CUs idle.
+// qgemm_legacy_kernel: a 256-thread workgroup computes 64 weight rows x 16 TJ activation rows; thread (ri, ti) owns
+// rows ri + 16i and activation rows ti + 16j (i < 4, j < TJ). Chunks of 8 blocks of both operands are staged in LDS;
+// each thread walks the chunk's blocks in order and adds each block's term to its sums, so every output is the
+// reference's ordered sum (the same terms as qgemv_kernel, the same bits). The next chunk's share of each thread is
+// loaded into registers while the current one is computed, and an activation block's quant sum (the Q4_0 / Q5_0
+// offset term) is taken once at staging. One launch covers the weights of one type that share the input (a layer's
+// Q, K and V): grid x runs over the row tiles of all of them, so small weights do not leave most CUs idle; TJ = 2
+// (32 activation rows per workgroup) doubles the workgroups of a launch that would otherwise leave most SIMDs with
+// one wave.
 constexpr int kGemmCB = 8;  // blocks per staged chunk
 
 struct QGemmBatch {  // weights of one type sharing one input; tile0[i]: first row tile of weight i
@@ -628,7 +631,10 @@ struct QGemmBatch {  // weights of one type sharing one input; tile0[i]: first r
   int n_w;
 };
 
-template <int T>
+// Staged quant words as a native vector type (a uint4 copy is a memcpy that keeps the staging share in scratch).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <int T, int TJ>
 __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, int64_t n) {
   int wi = 0;
   for (int i = 1; i < B.n_w; ++i)
@@ -636,67 +642,130 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
   const QW W = B.w[wi];
   float* __restrict__ y = B.y[wi];
   constexpr int QB = T == kQ8_0 ? 32 : 16;           // quant bytes per block
-  constexpr int QW4 = QB / 16;                        // uint4 per block
-  constexpr int WROW = kGemmCB * QW4 + 1;             // uint4 per staged weight row (one of padding: spreads banks)
-  __shared__ uint4 wq[64 * WROW];
+  constexpr int QW4 = QB / 16;                        // u32x4_t per block
+  constexpr int WROW = kGemmCB * QW4 + 1;             // u32x4_t per staged weight row (one of padding: spreads banks)
+  constexpr int AR = 16 * TJ;                         // activation rows per workgroup
+  constexpr int NWQ = 64 * kGemmCB * QW4 / 256;       // weight u32x4_t a thread stages per chunk
+  constexpr int NWM = 64 * kGemmCB / 256;             // weight block headers a thread stages per chunk
+  constexpr int NA = (AR * kGemmCB + 255) / 256;      // activation blocks a thread stages per chunk (at most)
+  static_assert(NWQ * 256 == 64 * kGemmCB * QW4 && NWM * 256 == 64 * kGemmCB, "chunks split evenly");
+  __shared__ u32x4_t wq[64 * WROW];
   __shared__ uint16_t wd[64][kGemmCB], wm[64][kGemmCB];
   __shared__ uint32_t wh[64][kGemmCB];
-  __shared__ uint4 aq[64][kGemmCB][2];
-  __shared__ float ad[64][kGemmCB], as_[64][kGemmCB];
+  __shared__ u32x4_t aq[AR][kGemmCB][2];
+  __shared__ float ad[AR][kGemmCB], as_[AR][kGemmCB];
+  __shared__ int asum[AR][kGemmCB];
   const int tid = threadIdx.x, ri = tid & 15, ti = tid >> 4;
-  const int64_t row0 = int64_t(int(blockIdx.x) - B.tile0[wi]) * 64, t0 = int64_t(blockIdx.y) * 64;
-  float acc[4][4];
+  const int64_t row0 = int64_t(int(blockIdx.x) - B.tile0[wi]) * 64, t0 = int64_t(blockIdx.y) * AR;
+  float acc[4][TJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-  for (int64_t c0 = 0; c0 < W.nb; c0 += kGemmCB) {
+    for (int j = 0; j < TJ; ++j) acc[i][j] = 0.f;
+  // A thread's share of one chunk, in registers: rows and activation rows past the ends, and blocks past the
+  // chunk's end, load clamped (staged but never used).
+  struct Share {
+    u32x4_t q[NWQ];
+    uint32_t d[NWM], m[NWM], h[NWM];
+    u32x4_t a0[NA], a1[NA];
+    float ad[NA], as[NA];
+  };
+  auto load_share = [&](int64_t c0, Share& sh) __attribute__((always_inline)) {
     const int nc = int(W.nb - c0 < kGemmCB ? W.nb - c0 : kGemmCB);
-    // stage: rows and activation rows past the ends, and blocks past the chunk's end, load clamped (unused)
-    for (int e = tid; e < 64 * kGemmCB * QW4; e += 256) {
+#pragma unroll
+    for (int u = 0; u < NWQ; ++u) {
+      const int e = tid + 256 * u;
       const int r = e / (kGemmCB * QW4), rem = e % (kGemmCB * QW4), b = rem / QW4, part = rem % QW4;
       const int64_t rr = min(row0 + r, W.rows - 1), bb = c0 + min(b, nc - 1);
-      wq[r * WROW + b * QW4 + part] = reinterpret_cast<const uint4*>(W.q + (rr * W.nb + bb) * QB)[part];
+      sh.q[u] = reinterpret_cast<const u32x4_t*>(W.q + (rr * W.nb + bb) * QB)[part];
     }
-    for (int e = tid; e < 64 * kGemmCB; e += 256) {
+#pragma unroll
+    for (int u = 0; u < NWM; ++u) {
+      const int e = tid + 256 * u;
       const int r = e / kGemmCB, b = e % kGemmCB;
       const int64_t wb = min(row0 + r, W.rows - 1) * W.nb + c0 + min(b, nc - 1);
-      wd[r][b] = W.d[wb];
-      if constexpr (T == kQ5_1) wm[r][b] = W.m[wb];
-      if constexpr (T == kQ5_0 || T == kQ5_1) wh[r][b] = reinterpret_cast<const uint32_t*>(W.h)[wb];
-      const int64_t ab = min(t0 + r, n - 1) * A.nb + c0 + min(b, nc - 1);
-      ad[r][b] = A.d[ab];
-      if constexpr (T == kQ5_1) as_[r][b] = A.s[ab];
-      const uint4* ap = reinterpret_cast<const uint4*>(A.qs + ab * 32);
-      aq[r][b][0] = ap[0];
-      aq[r][b][1] = ap[1];
+      sh.d[u] = W.d[wb];
+      if constexpr (T == kQ5_1) sh.m[u] = W.m[wb];
+      if constexpr (T == kQ5_0 || T == kQ5_1) sh.h[u] = reinterpret_cast<const uint32_t*>(W.h)[wb];
     }
-    __syncthreads();
-    for (int b = 0; b < nc; ++b) {
-      ActL act[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+    for (int u = 0; u < NA; ++u) {
+      const int e = tid + 256 * u;
+      if (e < AR * kGemmCB) {
+        const int r = e / kGemmCB, b = e % kGemmCB;
+        const int64_t ab = min(t0 + r, n - 1) * A.nb + c0 + min(b, nc - 1);
+        sh.ad[u] = A.d[ab];
+        if constexpr (T == kQ5_1) sh.as[u] = A.s[ab];
+        const u32x4_t* ap = reinterpret_cast<const u32x4_t*>(A.qs + ab * 32);
+        sh.a0[u] = ap[0];
+        sh.a1[u] = ap[1];
+      }
+    }
+  };
+  auto store_share = [&](const Share& sh) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < NWQ; ++u) {
+      const int e = tid + 256 * u;
+      const int r = e / (kGemmCB * QW4), rem = e % (kGemmCB * QW4);
+      wq[r * WROW + rem] = sh.q[u];
+    }
+#pragma unroll
+    for (int u = 0; u < NWM; ++u) {
+      const int e = tid + 256 * u;
+      const int r = e / kGemmCB, b = e % kGemmCB;
+      wd[r][b] = uint16_t(sh.d[u]);
+      if constexpr (T == kQ5_1) wm[r][b] = uint16_t(sh.m[u]);
+      if constexpr (T == kQ5_0 || T == kQ5_1) wh[r][b] = sh.h[u];
+    }
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+      const int e = tid + 256 * u;
+      if (e < AR * kGemmCB) {
+        const int r = e / kGemmCB, b = e % kGemmCB;
+        ad[r][b] = sh.ad[u];
+        if constexpr (T == kQ5_1) as_[r][b] = sh.as[u];
+        aq[r][b][0] = sh.a0[u];
+        aq[r][b][1] = sh.a1[u];
+        if constexpr (T == kQ4_0 || T == kQ5_0) {
+          const uint32_t w8[8] = {sh.a0[u].x, sh.a0[u].y, sh.a0[u].z, sh.a0[u].w,
+                                  sh.a1[u].x, sh.a1[u].y, sh.a1[u].z, sh.a1[u].w};
+          int sum = 0;
+#pragma unroll
+          for (int w = 0; w < 8; ++w) sum = sdot4(w8[w], 0x01010101u, sum);
+          asum[r][b] = sum;
+        }
+      }
+    }
+  };
+  Share cur;
+  load_share(0, cur);
+  for (int64_t c0 = 0; c0 < W.nb; c0 += kGemmCB) {
+    const int nc = int(W.nb - c0 < kGemmCB ? W.nb - c0 : kGemmCB);
+    store_share(cur);
+    __syncthreads();
+    // the next chunk's share, in flight while this one is computed (the last chunk loads itself again, unused)
+    load_share(c0 + kGemmCB < W.nb ? c0 + kGemmCB : c0, cur);
+    for (int b = 0; b < nc; ++b) {
+      ActL act[TJ];
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
         const int t = ti + 16 * j;
-        const uint4 a0 = aq[t][b][0], a1 = aq[t][b][1];
+        const u32x4_t a0 = aq[t][b][0], a1 = aq[t][b][1];
         ActL& a = act[j];
         a.a[0] = a0.x, a.a[1] = a0.y, a.a[2] = a0.z, a.a[3] = a0.w, a.a[4] = a1.x, a.a[5] = a1.y, a.a[6] = a1.z,
         a.a[7] = a1.w;
         a.d = ad[t][b];
         a.s = T == kQ5_1 ? as_[t][b] : 0.f;
-        a.sum = 0;
-        if constexpr (T == kQ4_0 || T == kQ5_0) {
-#pragma unroll
-          for (int w = 0; w < 8; ++w) a.sum = sdot4(a.a[w], 0x01010101u, a.sum);
-        }
+        a.sum = T == kQ4_0 || T == kQ5_0 ? asum[t][b] : 0;
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = ri + 16 * i;
         const float dw = h2f(wd[r][b]);
         if constexpr (T == kQ8_0) {
-          const uint4 w0 = wq[r * WROW + 2 * b], w1 = wq[r * WROW + 2 * b + 1];
+          const u32x4_t w0 = wq[r * WROW + 2 * b], w1 = wq[r * WROW + 2 * b + 1];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < TJ; ++j) {
             const ActL& a = act[j];
             int s = sdot4(w0.x, a.a[0], 0);
             s = sdot4(w0.y, a.a[1], s), s = sdot4(w0.z, a.a[2], s), s = sdot4(w0.w, a.a[3], s);
@@ -705,7 +774,7 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
             acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(float(s), __fmul_rn(dw, a.d)));
           }
         } else {
-          const uint4 wv = wq[r * WROW + b];
+          const u32x4_t wv = wq[r * WROW + b];
           const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
           uint32_t lo[4], hi[4];
 #pragma unroll
@@ -723,7 +792,7 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
           }
           const float mw = T == kQ5_1 ? h2f(wm[r][b]) : 0.f;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < TJ; ++j) {
             const ActL& a = act[j];
             int s = 0;
 #pragma unroll
@@ -742,10 +811,19 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < TJ; ++j) {
       const int64_t r = row0 + ri + 16 * i, t = t0 + ti + 16 * j;
       if (r < W.rows && t < n) y[t * W.rows + r] = acc[i][j];
     }
+}
+
+// Workgroups below which a legacy-type launch takes 32-row activation tiles (two per CU on 256 CUs).
+constexpr int64_t kLegacyMinWgs = 512;
+template <int T>
+hipError_t launch_legacy(bool half, dim3 grid, dim3 grid2, hipStream_t s, const QGemmBatch& B, const QA& A,
+                         int64_t n) {
+  if (half) return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<T, 2>, grid2, dim3(256), s, B, A, n);
+  return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<T, 4>, grid, dim3(256), s, B, A, n);
 }
 
 // qgemm_k_kernel: the tiled matmul for the K types on the int8 matrix cores (v_mfma_i32_16x16x32_i8).
@@ -1166,14 +1244,17 @@ int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* row
              act == kActQ8_K ? reinterpret_cast<const int16_t*>(base + l.bsums_off) : nullptr, B.w[0].nb};
   const dim3 grid{unsigned(tiles), unsigned((n + 63) / 64), 1}, block{256, 1, 1};
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // legacy types: 32-row activation tiles when 64-row ones would give fewer than kLegacyMinWgs workgroups
+  const bool half = int64_t(tiles) * ((n + 63) / 64) < kLegacyMinWgs && n > 32;
+  const dim3 grid2{unsigned(tiles), unsigned((n + 31) / 32), 1};
   switch (type) {
     case kQ4_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ4_K>, grid, block, s, B, A, n);
     case kQ5_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ5_K>, grid, block, s, B, A, n);
     case kQ6_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ6_K>, grid, block, s, B, A, n);
-    case kQ4_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ4_0>, grid, block, s, B, A, n);
-    case kQ5_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_0>, grid, block, s, B, A, n);
-    case kQ5_1: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ5_1>, grid, block, s, B, A, n);
-    case kQ8_0: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<kQ8_0>, grid, block, s, B, A, n);
+    case kQ4_0: return launch_legacy<kQ4_0>(half, grid, grid2, s, B, A, n);
+    case kQ5_0: return launch_legacy<kQ5_0>(half, grid, grid2, s, B, A, n);
+    case kQ5_1: return launch_legacy<kQ5_1>(half, grid, grid2, s, B, A, n);
+    case kQ8_0: return launch_legacy<kQ8_0>(half, grid, grid2, s, B, A, n);
     default: return NBHS_EINVAL;
   }
 }

@@ -134,6 +134,32 @@ def test_quant_tiled_many_weights_one_type(backend, t):
     backend.release_weights()
 
 
+@pytest.mark.parametrize("t", LEGACY, ids=[U.NAMES[t] for t in LEGACY])
+def test_quant_tiled_legacy_both_tile_heights(backend, t):
+    """The legacy tiled kernel in both activation-tile heights: a launch of at least 512 workgroups keeps 64-row
+    activation tiles (4100 rows = 65 row tiles x 9 activation tiles at n = 520, rows and activation rows ending
+    inside a tile), a smaller one takes 32-row tiles (the same weight's first 70 rows at n = 100). Three blocks per
+    row: a partial chunk. Both bit-exact."""
+    in_ = 96
+    w_big = U.random_qmat(t, 4100, in_, seed=700 + t)
+    w_small = U.random_qmat(t, 70, in_, seed=800 + t)
+    rng = np.random.default_rng(31 + t)
+    x_big = (rng.standard_normal((520, in_)) * 2).astype(np.float32)
+    x_small = x_big[:100].copy()
+    with Buffers(backend) as B:
+        dxb, dyb = B.upload(x_big), B.alloc(520 * 4100)
+        dxs, dys = B.upload(x_small), B.alloc(100 * 70)
+        backend.matmul(w_big, dxb, dyb, 520)
+        backend.matmul(w_small, dxs, dys, 100)
+        got_big = backend.download(dyb, (520, 4100))
+        got_small = backend.download(dys, (100, 70))
+    for g, w, x in ((got_big, w_big, x_big), (got_small, w_small, x_small)):
+        ref = oracle.matmul_q(t, w.raw, in_, w.rows, x)
+        diff = int(np.sum(bits(g) != bits(ref)))
+        assert diff == 0, (U.NAMES[t], w.rows, diff)
+    backend.release_weights()
+
+
 @pytest.mark.parametrize("n", [17, 80, 130])
 def test_quant_tiled_k_types_mixed(backend, n):
     """Prefill-sized calls over K-type weights, which run the int8 matrix-core kernel on residue-major Q8_K
