@@ -613,15 +613,18 @@ __global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* 
 
 // ---- the tiled matmul for longer calls (prefill chunks) ----
 //
-// qgemm_legacy_kernel: a 256-thread workgroup computes 64 weight rows x 16 TJ activation rows; thread (ri, ti) owns
-// rows ri + 16i and activation rows ti + 16j (i < 4, j < TJ). Chunks of 8 blocks of both operands are staged in LDS;
-// each thread walks the chunk's blocks in order and adds each block's term to its sums, so every output is the
-// reference's ordered sum (the same terms as qgemv_kernel, the same bits). The next chunk's share of each thread is
-// loaded into registers while the current one is computed, and an activation block's quant sum (the Q4_0 / Q5_0
-// offset term) is taken once at staging. One launch covers the weights of one type that share the input (a layer's
-// Q, K and V): grid x runs over the row tiles of all of them, so small weights do not leave most CUs idle; TJ = 2
-// (32 activation rows per workgroup) doubles the workgroups of a launch that would otherwise leave most SIMDs with
-// one wave.
+// qgemm_legacy_kernel: a 256-thread workgroup computes 64 weight rows x 16 TJ activation rows on the int8 matrix
+// cores. A legacy block is 32 elements, exactly the contraction of one v_mfma_i32_16x16x32_i8, so each (16 weight
+// rows, 16 activation rows, block) is one MFMA from zero: the block's exact integer dots (Q4_0 / Q5_0 as
+// sum q_w q_a, the offset term -8 or -16 times the activation block's quant sum applied after, exactly). Every output
+// then adds its block's float term - the reference's expression, in block order - so the outputs are bit-exact with
+// the v_dot4 path and with quant.cpp. Waves: 2 x 2 over 64 x 64 (TJ = 4) or 4 x 1 over 64 x 32 (TJ = 2), each lane
+// holding the MFMA result layout's 4 weight rows of one activation row per 16 x 16 pair. Chunks of 8 blocks of
+// both operands are staged in LDS (one 16-byte pad per row: conflict-free fragment reads); the next chunk's share of
+// each thread is loaded into registers while the current one is computed, the weight scales are widened to float
+// and an activation block's quant sum taken once at staging. One launch covers the weights of one type that share
+// the input (a layer's Q, K and V): grid x runs over the row tiles of all of them, so small weights do not leave
+// most CUs idle; TJ = 2 doubles the workgroups of a launch that would otherwise leave most SIMDs with one wave.
 constexpr int kGemmCB = 8;  // blocks per staged chunk
 
 struct QGemmBatch {  // weights of one type sharing one input; tile0[i]: first row tile of weight i
@@ -633,6 +636,7 @@ struct QGemmBatch {  // weights of one type sharing one input; tile0[i]: first r
 
 // Staged quant words as a native vector type (a uint4 copy is a memcpy that keeps the staging share in scratch).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));  // an integer MFMA result
 
 template <int T, int TJ>
 __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, int64_t n) {
@@ -644,24 +648,34 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
   constexpr int QB = T == kQ8_0 ? 32 : 16;           // quant bytes per block
   constexpr int QW4 = QB / 16;                        // u32x4_t per block
   constexpr int WROW = kGemmCB * QW4 + 1;             // u32x4_t per staged weight row (one of padding: spreads banks)
+  constexpr int AROW = 2 * kGemmCB + 1;               // u32x4_t per staged activation row (likewise)
   constexpr int AR = 16 * TJ;                         // activation rows per workgroup
   constexpr int NWQ = 64 * kGemmCB * QW4 / 256;       // weight u32x4_t a thread stages per chunk
   constexpr int NWM = 64 * kGemmCB / 256;             // weight block headers a thread stages per chunk
   constexpr int NA = (AR * kGemmCB + 255) / 256;      // activation blocks a thread stages per chunk (at most)
   static_assert(NWQ * 256 == 64 * kGemmCB * QW4 && NWM * 256 == 64 * kGemmCB, "chunks split evenly");
+  // Per wave: WM 16-row weight groups x 2 16-row activation groups, one v_mfma_i32_16x16x32_i8 per pair and block
+  // (a legacy block is exactly the MFMA's 32-deep contraction). TJ = 4: waves 2 x 2 over 64 x 64; TJ = 2: waves
+  // 4 x 1 over 64 x 32.
+  constexpr int WM = TJ == 4 ? 2 : 1;
   __shared__ u32x4_t wq[64 * WROW];
-  __shared__ uint16_t wd[64][kGemmCB], wm[64][kGemmCB];
+  __shared__ float wdf[kGemmCB][64], wmf[kGemmCB][64];
   __shared__ uint32_t wh[64][kGemmCB];
-  __shared__ u32x4_t aq[AR][kGemmCB][2];
-  __shared__ float ad[AR][kGemmCB], as_[AR][kGemmCB];
-  __shared__ int asum[AR][kGemmCB];
-  const int tid = threadIdx.x, ri = tid & 15, ti = tid >> 4;
+  __shared__ u32x4_t aq[AR * AROW];
+  __shared__ float ad[kGemmCB][AR], as_[kGemmCB][AR];
+  __shared__ int asum[kGemmCB][AR];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ml = lane & 15, kg = lane >> 4;  // operand row / column of the lane and its 8-deep k group
+  const int wr0 = TJ == 4 ? 32 * (wave & 1) : 16 * wave, ac0 = TJ == 4 ? 32 * (wave >> 1) : 0;
   const int64_t row0 = int64_t(int(blockIdx.x) - B.tile0[wi]) * 64, t0 = int64_t(blockIdx.y) * AR;
-  float acc[4][TJ];
+  // acc[i][j][v]: weight row wr0 + 16 i + 4 kg + v, activation row ac0 + 16 j + ml (the MFMA's result layout)
+  float acc[WM][2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) acc[i][j] = 0.f;
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
   // A thread's share of one chunk, in registers: rows and activation rows past the ends, and blocks past the
   // chunk's end, load clamped (staged but never used).
   struct Share {
@@ -713,8 +727,8 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
     for (int u = 0; u < NWM; ++u) {
       const int e = tid + 256 * u;
       const int r = e / kGemmCB, b = e % kGemmCB;
-      wd[r][b] = uint16_t(sh.d[u]);
-      if constexpr (T == kQ5_1) wm[r][b] = uint16_t(sh.m[u]);
+      wdf[b][r] = h2f(uint16_t(sh.d[u]));
+      if constexpr (T == kQ5_1) wmf[b][r] = h2f(uint16_t(sh.m[u]));
       if constexpr (T == kQ5_0 || T == kQ5_1) wh[r][b] = sh.h[u];
     }
 #pragma unroll
@@ -722,20 +736,43 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
       const int e = tid + 256 * u;
       if (e < AR * kGemmCB) {
         const int r = e / kGemmCB, b = e % kGemmCB;
-        ad[r][b] = sh.ad[u];
-        if constexpr (T == kQ5_1) as_[r][b] = sh.as[u];
-        aq[r][b][0] = sh.a0[u];
-        aq[r][b][1] = sh.a1[u];
+        ad[b][r] = sh.ad[u];
+        if constexpr (T == kQ5_1) as_[b][r] = sh.as[u];
+        aq[r * AROW + 2 * b] = sh.a0[u];
+        aq[r * AROW + 2 * b + 1] = sh.a1[u];
         if constexpr (T == kQ4_0 || T == kQ5_0) {
-          const uint32_t w8[8] = {sh.a0[u].x, sh.a0[u].y, sh.a0[u].z, sh.a0[u].w,
-                                  sh.a1[u].x, sh.a1[u].y, sh.a1[u].z, sh.a1[u].w};
           int sum = 0;
 #pragma unroll
-          for (int w = 0; w < 8; ++w) sum = sdot4(w8[w], 0x01010101u, sum);
-          asum[r][b] = sum;
+          for (int w = 0; w < 4; ++w) sum = sdot4(sh.a0[u][w], 0x01010101u, sum);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) sum = sdot4(sh.a1[u][w], 0x01010101u, sum);
+          asum[b][r] = sum;
         }
       }
     }
+  };
+  // The lane's A operand (weight row wr0 + 16 i + ml, block elements 8 kg .. 8 kg + 7) as int8 values: element e of
+  // a 4/5-bit block is the low nibble of byte e (e < 16) or the high nibble of byte e - 16, plus bit e of qh as
+  // bit 4 for the 5-bit types; Q8_0 bytes are the values.
+  auto a_operand = [&](int r, int b) __attribute__((always_inline)) {
+    const uint32_t* wr = reinterpret_cast<const uint32_t*>(&wq[r * WROW + QW4 * b]);
+    uint32_t lo, hi;
+    if constexpr (T == kQ8_0) {
+      lo = wr[2 * kg], hi = wr[2 * kg + 1];
+    } else {
+      const int sh = 4 * (kg >> 1);
+      lo = (wr[2 * (kg & 1)] >> sh) & 0x0F0F0F0Fu;
+      hi = (wr[2 * (kg & 1) + 1] >> sh) & 0x0F0F0F0Fu;
+      if constexpr (T == kQ5_0 || T == kQ5_1) {
+        const uint32_t bits = (wh[r][b] >> (8 * kg)) & 0xFFu;  // qh bits of elements 8 kg .. 8 kg + 7
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo |= ((bits >> e) & 1u) << (8 * e + 4);
+          hi |= ((bits >> (e + 4)) & 1u) << (8 * e + 4);
+        }
+      }
+    }
+    return long((uint64_t(hi) << 32) | uint64_t(lo));
   };
   Share cur;
   load_share(0, cur);
@@ -746,62 +783,39 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
     // the next chunk's share, in flight while this one is computed (the last chunk loads itself again, unused)
     load_share(c0 + kGemmCB < W.nb ? c0 + kGemmCB : c0, cur);
     for (int b = 0; b < nc; ++b) {
-      ActL act[TJ];
+      long bop[2];
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        const int t = ti + 16 * j;
-        const u32x4_t a0 = aq[t][b][0], a1 = aq[t][b][1];
-        ActL& a = act[j];
-        a.a[0] = a0.x, a.a[1] = a0.y, a.a[2] = a0.z, a.a[3] = a0.w, a.a[4] = a1.x, a.a[5] = a1.y, a.a[6] = a1.z,
-        a.a[7] = a1.w;
-        a.d = ad[t][b];
-        a.s = T == kQ5_1 ? as_[t][b] : 0.f;
-        a.sum = T == kQ4_0 || T == kQ5_0 ? asum[t][b] : 0;
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t* ar = reinterpret_cast<const uint32_t*>(&aq[(ac0 + 16 * j + ml) * AROW + 2 * b]);
+        bop[j] = long((uint64_t(ar[2 * kg + 1]) << 32) | uint64_t(ar[2 * kg]));
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = ri + 16 * i;
-        const float dw = h2f(wd[r][b]);
-        if constexpr (T == kQ8_0) {
-          const u32x4_t w0 = wq[r * WROW + 2 * b], w1 = wq[r * WROW + 2 * b + 1];
+      for (int i = 0; i < WM; ++i) {
+        const int rb = wr0 + 16 * i;
+        const long aop = a_operand(rb + ml, b);
+        const float4 dw4 = *reinterpret_cast<const float4*>(&wdf[b][rb + 4 * kg]);
+        const float dw[4] = {dw4.x, dw4.y, dw4.z, dw4.w};
+        float mw[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (T == kQ5_1) {
+          const float4 m4 = *reinterpret_cast<const float4*>(&wmf[b][rb + 4 * kg]);
+          mw[0] = m4.x, mw[1] = m4.y, mw[2] = m4.z, mw[3] = m4.w;
+        }
 #pragma unroll
-          for (int j = 0; j < TJ; ++j) {
-            const ActL& a = act[j];
-            int s = sdot4(w0.x, a.a[0], 0);
-            s = sdot4(w0.y, a.a[1], s), s = sdot4(w0.z, a.a[2], s), s = sdot4(w0.w, a.a[3], s);
-            s = sdot4(w1.x, a.a[4], s), s = sdot4(w1.y, a.a[5], s), s = sdot4(w1.z, a.a[6], s);
-            s = sdot4(w1.w, a.a[7], s);
-            acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(float(s), __fmul_rn(dw, a.d)));
-          }
-        } else {
-          const u32x4_t wv = wq[r * WROW + b];
-          const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
-          uint32_t lo[4], hi[4];
+        for (int j = 0; j < 2; ++j) {
+          const i32x4_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop[j], i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+          const int t = ac0 + 16 * j + ml;
+          const float da = ad[b][t];
+          const int sum = T == kQ4_0 || T == kQ5_0 ? asum[b][t] : 0;
+          const float sa = T == kQ5_1 ? as_[b][t] : 0.f;
 #pragma unroll
-          for (int k = 0; k < 4; ++k) lo[k] = w4[k] & 0x0F0F0F0Fu, hi[k] = (w4[k] >> 4) & 0x0F0F0F0Fu;
-          if constexpr (T == kQ5_0 || T == kQ5_1) {
-            const uint32_t qh = wh[r][b];
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int jj = 4 * k + e;
-                lo[k] |= ((qh >> jj) & 1u) << (8 * e + 4);
-                hi[k] |= ((qh >> (jj + 16)) & 1u) << (8 * e + 4);
-              }
-          }
-          const float mw = T == kQ5_1 ? h2f(wm[r][b]) : 0.f;
-#pragma unroll
-          for (int j = 0; j < TJ; ++j) {
-            const ActL& a = act[j];
-            int s = 0;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) s = sdot4(lo[k], a.a[k], s), s = sdot4(hi[k], a.a[k + 4], s);
+          for (int v = 0; v < 4; ++v) {
+            const int s = c[v];
             float term;
-            if constexpr (T == kQ4_0) term = __fmul_rn(__fmul_rn(float(s - 8 * a.sum), dw), a.d);
-            if constexpr (T == kQ5_0) term = __fmul_rn(__fmul_rn(dw, a.d), float(s - 16 * a.sum));
-            if constexpr (T == kQ5_1) term = __fadd_rn(__fmul_rn(__fmul_rn(dw, a.d), float(s)), __fmul_rn(mw, a.s));
-            acc[i][j] = __fadd_rn(acc[i][j], term);
+            if constexpr (T == kQ8_0) term = __fmul_rn(float(s), __fmul_rn(dw[v], da));
+            if constexpr (T == kQ4_0) term = __fmul_rn(__fmul_rn(float(s - 8 * sum), dw[v]), da);
+            if constexpr (T == kQ5_0) term = __fmul_rn(__fmul_rn(dw[v], da), float(s - 16 * sum));
+            if constexpr (T == kQ5_1) term = __fadd_rn(__fmul_rn(__fmul_rn(dw[v], da), float(s)), __fmul_rn(mw[v], sa));
+            acc[i][j][v] = __fadd_rn(acc[i][j][v], term);
           }
         }
       }
@@ -809,12 +823,14 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int64_t r = row0 + ri + 16 * i, t = t0 + ti + 16 * j;
-      if (r < W.rows && t < n) y[t * W.rows + r] = acc[i][j];
-    }
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t r = row0 + wr0 + 16 * i + 4 * kg + v, t = t0 + ac0 + 16 * j + ml;
+        if (r < W.rows && t < n) y[t * W.rows + r] = acc[i][j][v];
+      }
 }
 
 // Workgroups below which a legacy-type launch takes 32-row activation tiles (two per CU on 256 CUs).
@@ -848,7 +864,6 @@ constexpr int kKTileRows = 16;
 template <int T>
 constexpr int k_slices() { return T == kQ4_K ? 2 : T == kQ5_K ? 3 : 4; }
 
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
 
 // Bytes b of the result hold lo16(x_b * y_b) & 0xFF for the four bytes of a word, with x_b, y_b small signed
