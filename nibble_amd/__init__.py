@@ -143,7 +143,9 @@ def weight(w, shape=None, dtype=None) -> NbhTensor:
     if isinstance(w, np.ndarray) and dtype is not None:
         assert w.flags.c_contiguous and shape is not None
         ne = [int(shape[-1]), int(shape[0]) if len(shape) > 1 else 1, 1, 1]
-        return NbhTensor(dtype, len(shape), (c_int64 * 4)(*ne), c_void_p(w.ctypes.data))
+        t = NbhTensor(dtype, len(shape), (c_int64 * 4)(*ne), c_void_p(w.ctypes.data))
+        t._host = w  # the view points into w: the array lives as long as the tensor (uploads happen at first use)
+        return t
     if isinstance(w, np.ndarray):
         if w.dtype == np.float32:
             t = F32
@@ -158,7 +160,10 @@ def weight(w, shape=None, dtype=None) -> NbhTensor:
             raise BackendError("a device weight needs its shape and type")
         t, data = dtype, int(w)
     ne = [int(shape[-1]), int(shape[0]) if len(shape) > 1 else 1, 1, 1]
-    return NbhTensor(t, len(shape), (c_int64 * 4)(*ne), c_void_p(data))
+    out = NbhTensor(t, len(shape), (c_int64 * 4)(*ne), c_void_p(data))
+    if isinstance(w, np.ndarray):
+        out._host = w  # as above: a host view keeps its array alive
+    return out
 
 
 class HipBackend:

@@ -75,3 +75,23 @@ def test_backend_creation_without_gpu_raises():
         pytest.skip("a GPU driver is present")
     with pytest.raises(nibble_amd.BackendError):
         nibble_amd.HipBackend(0)
+
+
+def test_weight_views_keep_their_host_arrays_alive():
+    """A weight made from a temporary host array (float or raw quantized blocks) still points at intact data after
+    the caller's reference is gone: the backend uploads a weight at its first use, possibly much later."""
+    import ctypes
+    import gc
+
+    import numpy as np
+
+    import nibble_amd
+
+    wf = nibble_amd.weight(np.arange(16, dtype=np.float32).reshape(4, 4))
+    wq = nibble_amd.weight(np.arange(144 * 2, dtype=np.uint8) % 251, shape=(2, 256), dtype=12)
+    gc.collect()
+    _ = [np.ones(1 << 20, dtype=np.uint8) for _ in range(4)]  # allocations that would reuse freed memory
+    got_f = np.ctypeslib.as_array((ctypes.c_float * 16).from_address(wf.data))
+    got_q = np.ctypeslib.as_array((ctypes.c_uint8 * (144 * 2)).from_address(wq.data))
+    assert np.array_equal(got_f, np.arange(16, dtype=np.float32))
+    assert np.array_equal(got_q, np.arange(144 * 2, dtype=np.uint8) % 251)
