@@ -26,7 +26,6 @@ constexpr int64_t kFp32PrefixRows = 128;
 // matmul calls with at most this many rows take the weight-streaming gemv kernel; longer ones are GEMMs.
 constexpr int64_t kGemvMaxRows = NBHS_GEMV_MAX_ROWS;
 constexpr size_t kGemvMaxWeights = NBHS_GEMV_MAX_WEIGHTS;
-constexpr int64_t kLegacyTiledMinRows = 80;  // measured crossover (Q8_0, 3072 x 2048): 16-row launches ~10 us each
 
 std::string str(int64_t v) { return std::to_string(v); }
 
@@ -478,9 +477,9 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
   const bool fuse = n <= 4 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && in % 4 == 0;
   int done_act = -1;
   for (const int t : types) {
-    // prefill chunks: the tiled kernels, whose K-type activations are in residue-major order. The legacy types'
-    // tiled kernel (64 x 64 tiles) has too few workgroups below ~80 rows; there the 16-row launches are faster.
-    const bool tiled = nbh_quant::is_k(t) ? n > kGemvMaxRows : n > kLegacyTiledMinRows;
+    // more than 16 rows: the tiled kernels (measured faster from 17 rows on at the QKV shape), whose K-type
+    // activations are in residue-major order
+    const bool tiled = n > kGemvMaxRows;
     const bool rm = tiled && nbh_quant::is_k(t);
     const int act_key = 2 * nbh_quant::act_of(t) + (rm ? 1 : 0);
     if (!fuse && act_key != done_act) {

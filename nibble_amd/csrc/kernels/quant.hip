@@ -1259,8 +1259,9 @@ int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* row
              act == kActQ8_K ? reinterpret_cast<const int16_t*>(base + l.bsums_off) : nullptr, B.w[0].nb};
   const dim3 grid{unsigned(tiles), unsigned((n + 63) / 64), 1}, block{256, 1, 1};
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // legacy types: 32-row activation tiles when 64-row ones would give fewer than kLegacyMinWgs workgroups
-  const bool half = int64_t(tiles) * ((n + 63) / 64) < kLegacyMinWgs && n > 32;
+  // legacy types: 32-row activation tiles when 64-row ones would give fewer than kLegacyMinWgs workgroups (and for
+  // at most 32 rows, where a 64-row tile would compute half of it for nothing)
+  const bool half = int64_t(tiles) * ((n + 63) / 64) < kLegacyMinWgs || n <= 32;
   const dim3 grid2{unsigned(tiles), unsigned((n + 31) / 32), 1};
   switch (type) {
     case kQ4_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ4_K>, grid, block, s, B, A, n);

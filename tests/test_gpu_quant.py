@@ -21,7 +21,7 @@ TYPES = list(U.NAMES)
 @pytest.mark.parametrize("n", [1, 3, 16, 17, 40, 96])
 def test_quant_matmul_bit_exact(backend, t, n):
     """Activation quantization and the block dots, every activation-row chunking: n <= 16 (one row-chunked
-    launch), 17 and 40 (row-chunked launches for the legacy types, tiled for the K types), 96 (tiled)."""
+    launch), 17, 40 and 96 (the tiled kernels; the legacy types' 32-row activation tiles, one or two of them)."""
     be_ = oracle.block_elems(t)
     in_ = 2 * 256 if be_ == 256 else 7 * 32 + 32 * 64  # two super-blocks / 71 legacy blocks (a partial chunk)
     rows = 37  # not a multiple of the 4 rows per wave
