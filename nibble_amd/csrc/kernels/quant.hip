@@ -854,15 +854,17 @@ hipError_t launch_legacy(bool half, dim3 grid, dim3 grid2, hipStream_t s, const 
 // The float arithmetic that follows is the reference's per output and block: d = fp16(d_w) * d_a, sums[w] +=
 // d * aux[w], for Q4_K / Q5_K acc -= (fp16(dmin_w) * d_a) * sumi, result acc + sums[0] + ... + sums[7] - the same
 // operations in the same order as qgemv_kernel, so the same bits.
-// A workgroup (4 waves) takes 16 weight rows and 64 activation rows (16 per wave). Per super-block its threads
-// expand the 16 rows into slice * quant bytes in LDS (residue-major, 40-byte rows: conflict-free 8-byte reads),
-// two super-blocks per stage;
-// each wave then runs 8 residues x slices MFMAs of 16 x 16 x 32, its activation operands read straight from the
-// residue-major Q8_K planes (quantize_q8k_kernel<true>). The accumulator layout gives lane l activation row
-// t0 + l % 16 and weight rows 4 (l / 16) + v, v < 4: 4 outputs and their 9 float accumulators per lane.
-constexpr int kKTileRows = 16;
+// A workgroup (4 waves) takes 64 weight rows and 32 activation rows; each wave 16 weight rows against both 16-row
+// activation groups. Per super-block the raw weight words (quants, high bits), the sub-block scales and minimums
+// (taken out of their packing once, at staging), d / dmin widened, and the activation rows (residue-major Q8_K
+// quants, d, the sub-block sums of the 16-sums) are staged in LDS with 16-byte loads, the next super-block's share
+// of each thread loaded into registers while the current one is computed. A lane (weight row ml, k group kg of the
+// MFMA operand layout) builds its slice operands for residue w from its row's quant word 8 kg + w (the elements of
+// residue w in sub-blocks 2 kg and 2 kg + 1) and the two sub-blocks' scales; the result layout gives it weight rows
+// 4 kg + v (v < 4) of activation row ml of each group: 8 outputs and their 9 float accumulators per lane.
 template <int T>
 constexpr int k_slices() { return T == kQ4_K ? 2 : T == kQ5_K ? 3 : 4; }
+constexpr int kKTileRows = 64, kKTileActs = 32;
 
 typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
 
@@ -875,176 +877,257 @@ __device__ __forceinline__ uint32_t byte_products(u16x2_t ex, u16x2_t ox, u16x2_
 }
 
 template <int T>
-__global__ __launch_bounds__(256) void qgemm_k_kernel(QGemmBatch B, QA A, int64_t n) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void qgemm_k_kernel(QGemmBatch B, QA A,
+                                                                                             int64_t n) {
   static_assert(T == kQ4_K || T == kQ5_K || T == kQ6_K, "K types");
   constexpr int NS = k_slices<T>();
-  constexpr int RW = 10;   // words per expanded (slice, residue, row) entry: 8 and 2 of padding
-  constexpr int SBS = 2;   // super-blocks staged per barrier pair: one global round trip for both
-  __shared__ __align__(16) uint32_t ew[SBS][NS][8][kKTileRows][RW];
-  __shared__ int mins[SBS][kKTileRows][8];
-  __shared__ float wdm[SBS][kKTileRows][2];
+  constexpr int WR = kKTileRows, AR = kKTileActs;
+  constexpr int QS = 33;                                 // words per staged quant row (32 and one of padding)
+  constexpr int HW = T == kQ5_K ? 8 : T == kQ6_K ? 16 : 0;  // high-bit words per row
+  constexpr int HS = HW + 1;
+  constexpr int AS = 68;                                 // words per staged activation row (64 and 4 of padding)
+  __shared__ uint32_t wq[WR * QS];
+  __shared__ uint32_t wh[HW > 0 ? WR * HS : 1];
+  __shared__ int wsc[WR][8], wmn[WR][8];                 // Q4_K / Q5_K: 6-bit scale and minimum per sub-block
+  __shared__ uint32_t wsq[WR][4];                        // Q6_K: the 16 int8 scales
+  __shared__ float wdm[WR][2];
+  __shared__ __align__(16) uint32_t aq[AR * AS];
+  __shared__ float ad[AR];
+  __shared__ int abs_[AR][8];                            // sum of the 16-sums of each sub-block (Q4_K / Q5_K)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ml = lane & 15, kg = lane >> 4;
   int wi = 0;
   for (int i = 1; i < B.n_w; ++i)
     if (int(blockIdx.x) >= B.tile0[i]) wi = i;
   const QW W = B.w[wi];
   float* __restrict__ y = B.y[wi];
-  const int64_t row0 = int64_t(int(blockIdx.x) - B.tile0[wi]) * kKTileRows;
-  const int tl = lane & 15, g = lane >> 4;
-  const int64_t t = int64_t(blockIdx.y) * 64 + 16 * wave + tl, tc = t < n ? t : n - 1;
-  // expansion share: row er, residue rr, sub-blocks 4 hh .. 4 hh + 3
-  const int er = tid >> 4, rr = (tid >> 1) & 7, hh = tid & 1;
-  const int64_t erow = row0 + er < W.rows ? row0 + er : W.rows - 1;
-  float sums[8][4], acc[4];
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    acc[v] = 0.f;
-#pragma unroll
-    for (int w = 0; w < 8; ++w) sums[w][v] = 0.f;
-  }
-  // Raw words of this thread's expansion share: Q4_K / Q5_K qs groups 2 hh, 2 hh + 1 (low nibbles: sub-block 2c,
-  // high: 2c + 1); Q6_K the ql groups of half hh (low nibbles: sub-blocks 4 hh + lg, high: 4 hh + lg + 2); the high
-  // bits; the 16 scale bytes; d and dmin.
-  struct Raw {
-    uint32_t q[2], h;
-    uint4 sc;
-    uint16_t d, m;
+  const int64_t row0 = int64_t(int(blockIdx.x) - B.tile0[wi]) * WR, t0 = int64_t(blockIdx.y) * AR;
+  // A thread's share of one super-block: 2 quant u32x4 (64 rows x 128 bytes), its high-bit part, the scales and
+  // d / dmin of one row (threads < 64), 2 activation u32x4 (32 rows x 256 bytes) and one row's d and 16-sums
+  // (threads < 32). Rows and activation rows past the ends load clamped (staged, never stored).
+  struct Share {
+    u32x4_t q[2], h, sc, a[2], bs[2];
+    uint32_t d, m;
+    float da;
   };
-  auto load_raw = [&](int64_t sb, Raw& r) {
-    const int64_t wb = erow * W.nb + sb;
-    const uint32_t* qw = reinterpret_cast<const uint32_t*>(W.q + wb * 128);
-    r.q[0] = qw[8 * (2 * hh) + rr];
-    r.q[1] = qw[8 * (2 * hh + 1) + rr];
-    r.h = 0;
-    if constexpr (T == kQ5_K) r.h = reinterpret_cast<const uint32_t*>(W.h + wb * 32)[rr];
-    if constexpr (T == kQ6_K) r.h = reinterpret_cast<const uint32_t*>(W.h + wb * 64 + 32 * hh)[rr];
-    r.sc = *reinterpret_cast<const uint4*>(W.s + wb * 16);
-    r.d = W.d[wb];
-    r.m = T == kQ6_K ? uint16_t(0) : W.m[wb];
+  auto load_share = [&](int64_t sb, Share& sh) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = tid + 256 * u, r = e >> 3, part = e & 7;
+      const int64_t rr = min(row0 + r, W.rows - 1);
+      sh.q[u] = reinterpret_cast<const u32x4_t*>(W.q + (rr * W.nb + sb) * 128)[part];
+    }
+    if constexpr (T == kQ5_K) {
+      if (tid < WR * 2) {
+        const int64_t rr = min(row0 + (tid >> 1), W.rows - 1);
+        sh.h = reinterpret_cast<const u32x4_t*>(W.h + (rr * W.nb + sb) * 32)[tid & 1];
+      }
+    }
+    if constexpr (T == kQ6_K) {
+      const int64_t rr = min(row0 + (tid >> 2), W.rows - 1);
+      sh.h = reinterpret_cast<const u32x4_t*>(W.h + (rr * W.nb + sb) * 64)[tid & 3];
+    }
+    if (tid < WR) {
+      const int64_t wb = min(row0 + tid, W.rows - 1) * W.nb + sb;
+      sh.sc = *reinterpret_cast<const u32x4_t*>(W.s + wb * 16);
+      sh.d = W.d[wb];
+      sh.m = T == kQ6_K ? 0u : uint32_t(W.m[wb]);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = tid + 256 * u, r = e >> 4, part = e & 15;
+      const int64_t ab = min(t0 + r, n - 1) * A.nb + sb;
+      sh.a[u] = reinterpret_cast<const u32x4_t*>(A.qs + ab * 256)[part];
+    }
+    if (tid < AR) {
+      const int64_t ab = min(t0 + tid, n - 1) * A.nb + sb;
+      sh.da = A.d[ab];
+      if constexpr (T != kQ6_K) {
+        const u32x4_t* bp = reinterpret_cast<const u32x4_t*>(A.bsums + ab * 16);
+        sh.bs[0] = bp[0];
+        sh.bs[1] = bp[1];
+      }
+    }
   };
-  auto expand = [&](const Raw& raw, int j) {
-    // scale bytes by compile-time index (a register array indexed by hh would go to scratch)
-    const uint32_t scw[4] = {raw.sc.x, raw.sc.y, raw.sc.z, raw.sc.w};
-    auto sbyte = [&](int i) { return int((scw[i >> 2] >> (8 * (i & 3))) & 0xFFu); };
+  auto store_share = [&](const Share& sh) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = tid + 256 * u, r = e >> 3, part = e & 7;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) wq[r * QS + 4 * part + c] = sh.q[u][c];
+    }
+    if constexpr (T == kQ5_K) {
+      if (tid < WR * 2) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) wh[(tid >> 1) * HS + 4 * (tid & 1) + c] = sh.h[c];
+      }
+    }
     if constexpr (T == kQ6_K) {
 #pragma unroll
-      for (int gg = 0; gg < 4; ++gg) {
-        const int k = 4 * hh + gg;
-        const uint32_t v =
-            ((raw.q[gg & 1] >> (4 * (gg >> 1))) & 0x0F0F0F0Fu) | (((raw.h >> (2 * gg)) & 0x03030303u) << 4);
-        // 16-bit lanes: even bytes (0, 2) and odd bytes (1, 3) of u0 = v & 7 and u1 = (v >> 3) - 4
-        const u16x2_t u0e = __builtin_bit_cast(u16x2_t, v & 0x00070007u);
-        const u16x2_t u0o = __builtin_bit_cast(u16x2_t, (v >> 8) & 0x00070007u);
-        const u16x2_t four = {4, 4};
-        const u16x2_t u1e = __builtin_bit_cast(u16x2_t, (v >> 3) & 0x00070007u) - four;
-        const u16x2_t u1o = __builtin_bit_cast(u16x2_t, (v >> 11) & 0x00070007u) - four;
-        // the signed scales of bytes 0, 1 and of bytes 2, 3 of the residue word: scale bytes 2k, 2k + 1
-        const int slo = int(int8_t(hh ? sbyte(8 + 2 * gg) : sbyte(2 * gg)));
-        const int shi = int(int8_t(hh ? sbyte(9 + 2 * gg) : sbyte(2 * gg + 1)));
-        const u16x2_t s0 = {uint16_t(slo & 15), uint16_t(shi & 15)};
-        const u16x2_t s1 = {uint16_t(slo >> 4), uint16_t(shi >> 4)};
-        ew[j][0][rr][er][k] = byte_products(u1e, u1o, s1);
-        ew[j][1][rr][er][k] = byte_products(u0e, u0o, s1);
-        ew[j][2][rr][er][k] = byte_products(u1e, u1o, s0);
-        ew[j][3][rr][er][k] = byte_products(u0e, u0o, s0);
-      }
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int k = 4 * hh + kk;
-        // scale_min_k4 (quant.cpp:55-64) on the register copy of the packed scales, k = 4 hh + kk
-        const int sk = hh ? (sbyte(8 + kk) & 0xF) | ((sbyte(kk) >> 6) << 4) : sbyte(kk) & 63;
-        const int mk = hh ? (sbyte(8 + kk) >> 4) | ((sbyte(4 + kk) >> 6) << 4) : sbyte(kk + 4) & 63;
-        uint32_t q = (raw.q[kk >> 1] >> (4 * (kk & 1))) & 0x0F0F0F0Fu;
-        if constexpr (T == kQ5_K) {
-          q |= ((raw.h >> k) & 0x01010101u) << 4;
-          ew[j][0][rr][er][k] = q * uint32_t(sk & 3);
-          ew[j][1][rr][er][k] = q * uint32_t((sk >> 2) & 3);
-          ew[j][2][rr][er][k] = q * uint32_t(sk >> 4);
-        } else {
-          ew[j][0][rr][er][k] = q * uint32_t(sk & 7);
-          ew[j][1][rr][er][k] = q * uint32_t(sk >> 3);
-        }
-        if (rr == 0) mins[j][er][k] = mk;
-      }
+      for (int c = 0; c < 4; ++c) wh[(tid >> 2) * HS + 4 * (tid & 3) + c] = sh.h[c];
     }
-    if (rr == 0 && hh == 0) {
-      wdm[j][er][0] = h2f(raw.d);
-      wdm[j][er][1] = h2f(raw.m);
+    if (tid < WR) {
+      const uint32_t scw[4] = {sh.sc[0], sh.sc[1], sh.sc[2], sh.sc[3]};
+      auto sbyte = [&](int i) { return int((scw[i >> 2] >> (8 * (i & 3))) & 0xFFu); };
+      if constexpr (T == kQ6_K) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) wsq[tid][c] = scw[c];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {  // ggml get_scale_min_k4 (quant.cpp:52-61), compile-time byte indices
+          int sk, mk;
+          if (k < 4) {
+            sk = sbyte(k) & 63;
+            mk = sbyte(k + 4) & 63;
+          } else {
+            sk = (sbyte(k + 4) & 0xF) | ((sbyte(k - 4) >> 6) << 4);
+            mk = (sbyte(k + 4) >> 4) | ((sbyte(k) >> 6) << 4);
+          }
+          wsc[tid][k] = sk;
+          wmn[tid][k] = mk;
+        }
+      }
+      wdm[tid][0] = h2f(uint16_t(sh.d));
+      wdm[tid][1] = h2f(uint16_t(sh.m));
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = tid + 256 * u, r = e >> 4, part = e & 15;
+      *reinterpret_cast<u32x4_t*>(&aq[r * AS + 4 * part]) = sh.a[u];
+    }
+    if (tid < AR) {
+      ad[tid] = sh.da;
+      if constexpr (T != kQ6_K) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {  // 16-sums 2k and 2k + 1: the two int16 halves of word k
+          const uint32_t wk = sh.bs[k >> 2][k & 3];
+          abs_[tid][k] = int(int16_t(wk & 0xFFFFu)) + int(int16_t(wk >> 16));
+        }
+      }
     }
   };
-  // one super-block of this lane's outputs from stage j
-  auto compute = [&](int64_t sb, int j) {
-    const int64_t ab = tc * A.nb + sb;
-    const uint8_t* aq = reinterpret_cast<const uint8_t*>(A.qs) + ab * 256;
-    uint2 bw[8];
+  // acc[j][v], sums[w][j][v]: weight row 16 wave + 4 kg + v, activation row 16 j + ml
+  float sums[8][2][4], acc[2][4];
 #pragma unroll
-    for (int w = 0; w < 8; ++w) bw[w] = *reinterpret_cast<const uint2*>(aq + 32 * w + 8 * g);
-    const float da = A.d[ab];
-    int bsk[8];
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int k = 0; k < 8; ++k) bsk[k] = 0;
-    if constexpr (T != kQ6_K) {
-      const int16_t* bsp = A.bsums + ab * 16;
+    for (int v = 0; v < 4; ++v) {
+      acc[j][v] = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) bsk[k] = int(bsp[2 * k]) + int(bsp[2 * k + 1]);
+      for (int w = 0; w < 8; ++w) sums[w][j][v] = 0.f;
     }
-    float dv[4];
+  const int ra = 16 * wave + ml;  // this lane's operand row
+  Share cur;
+  load_share(0, cur);
+  for (int64_t sb = 0; sb < W.nb; ++sb) {
+    store_share(cur);
+    __syncthreads();
+    load_share(sb + 1 < W.nb ? sb + 1 : sb, cur);  // in flight while this super-block is computed
+    float dv[2][4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) dv[v] = __fmul_rn(wdm[j][4 * g + v][0], da);
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dv[j][v] = __fmul_rn(wdm[16 * wave + 4 * kg + v][0], ad[16 * j + ml]);
+    // the lane's two sub-blocks' scales: 2 kg and 2 kg + 1 (Q4_K / Q5_K), or their int8 pairs (Q6_K)
+    int s_a = 0, s_b = 0;
+    uint32_t s6 = 0;
+    if constexpr (T == kQ6_K)
+      s6 = wsq[ra][kg];  // bytes 4 kg .. 4 kg + 3: scales 2k, 2k + 1 of sub-blocks k = 2 kg, 2 kg + 1
+    else
+      s_a = wsc[ra][2 * kg], s_b = wsc[ra][2 * kg + 1];
 #pragma unroll
     for (int w = 0; w < 8; ++w) {
-      const long bop = (long(bw[w].y) << 32) | long(bw[w].x);
-      i32x4_t c[NS];
+      long aop[NS];
+      if constexpr (T == kQ6_K) {
+        // sub-block k = 2 kg + b: half h = kg >> 1, g = 2 (kg & 1) + b; ql group lg = b at word 16 h + 8 lg + w,
+        // nibble 4 (kg & 1); qh word 8 h + w at bits 2 g
+        const int h = kg >> 1, sel = kg & 1;
+        const uint32_t hq = wh[ra * HS + 8 * h + w];
+        uint32_t sl[4][2];
 #pragma unroll
-      for (int sl = 0; sl < NS; ++sl) {
-        const uint2 aw = *reinterpret_cast<const uint2*>(&ew[j][sl][w][tl][2 * g]);
-        const long aop = (long(aw.y) << 32) | long(aw.x);
-        c[sl] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+        for (int b = 0; b < 2; ++b) {
+          const int g = 2 * sel + b;
+          const uint32_t lw = wq[ra * QS + 16 * h + 8 * b + w];
+          const uint32_t v = ((lw >> (4 * sel)) & 0x0F0F0F0Fu) | (((hq >> (2 * g)) & 0x03030303u) << 4);
+          const u16x2_t u0e = __builtin_bit_cast(u16x2_t, v & 0x00070007u);
+          const u16x2_t u0o = __builtin_bit_cast(u16x2_t, (v >> 8) & 0x00070007u);
+          const u16x2_t four = {4, 4};
+          const u16x2_t u1e = __builtin_bit_cast(u16x2_t, (v >> 3) & 0x00070007u) - four;
+          const u16x2_t u1o = __builtin_bit_cast(u16x2_t, (v >> 11) & 0x00070007u) - four;
+          const int slo = int(int8_t((s6 >> (16 * b)) & 0xFFu)), shi = int(int8_t((s6 >> (16 * b + 8)) & 0xFFu));
+          const u16x2_t s0 = {uint16_t(slo & 15), uint16_t(shi & 15)};
+          const u16x2_t s1 = {uint16_t(slo >> 4), uint16_t(shi >> 4)};
+          sl[0][b] = byte_products(u1e, u1o, s1);
+          sl[1][b] = byte_products(u0e, u0o, s1);
+          sl[2][b] = byte_products(u1e, u1o, s0);
+          sl[3][b] = byte_products(u0e, u0o, s0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) aop[i] = long((uint64_t(sl[i][1]) << 32) | uint64_t(sl[i][0]));
+      } else {
+        const uint32_t qw = wq[ra * QS + 8 * kg + w];
+        uint32_t qa = qw & 0x0F0F0F0Fu, qb = (qw >> 4) & 0x0F0F0F0Fu;  // sub-blocks 2 kg and 2 kg + 1
+        if constexpr (T == kQ5_K) {
+          const uint32_t hb = wh[ra * HS + w];
+          qa |= ((hb >> (2 * kg)) & 0x01010101u) << 4;
+          qb |= ((hb >> (2 * kg + 1)) & 0x01010101u) << 4;
+        }
+        if constexpr (T == kQ4_K) {
+          aop[0] = long((uint64_t(qb * uint32_t(s_b & 7)) << 32) | uint64_t(qa * uint32_t(s_a & 7)));
+          aop[1] = long((uint64_t(qb * uint32_t(s_b >> 3)) << 32) | uint64_t(qa * uint32_t(s_a >> 3)));
+        } else {
+          aop[0] = long((uint64_t(qb * uint32_t(s_b & 3)) << 32) | uint64_t(qa * uint32_t(s_a & 3)));
+          aop[1] = long((uint64_t(qb * uint32_t((s_b >> 2) & 3)) << 32) | uint64_t(qa * uint32_t((s_a >> 2) & 3)));
+          aop[2] = long((uint64_t(qb * uint32_t(s_b >> 4)) << 32) | uint64_t(qa * uint32_t(s_a >> 4)));
+        }
       }
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        int aux;
-        if constexpr (T == kQ6_K)
-          aux = 128 * c[0][v] + 16 * c[1][v] + 8 * c[2][v] + c[3][v];
-        else if constexpr (T == kQ5_K)
-          aux = c[0][v] + 4 * c[1][v] + 16 * c[2][v];
-        else
-          aux = c[0][v] + 8 * c[1][v];
-        sums[w][v] = __fadd_rn(sums[w][v], __fmul_rn(dv[v], float(aux)));
+      for (int j = 0; j < 2; ++j) {
+        const uint2 bw = *reinterpret_cast<const uint2*>(&aq[(16 * j + ml) * AS + 8 * w + 2 * kg]);
+        const long bop = long((uint64_t(bw.y) << 32) | uint64_t(bw.x));
+        i32x4_t c[NS];
+#pragma unroll
+        for (int sl = 0; sl < NS; ++sl)
+          c[sl] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[sl], bop, i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          int aux;
+          if constexpr (T == kQ6_K)
+            aux = 128 * c[0][v] + 16 * c[1][v] + 8 * c[2][v] + c[3][v];
+          else if constexpr (T == kQ5_K)
+            aux = c[0][v] + 4 * c[1][v] + 16 * c[2][v];
+          else
+            aux = c[0][v] + 8 * c[1][v];
+          sums[w][j][v] = __fadd_rn(sums[w][j][v], __fmul_rn(dv[j][v], float(aux)));
+        }
       }
     }
     if constexpr (T != kQ6_K) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int rv = 4 * g + v;
-        int sumi = 0;
+      for (int j = 0; j < 2; ++j) {
+        const int t = 16 * j + ml;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) sumi += bsk[k] * mins[j][rv][k];
-        acc[v] = __fsub_rn(acc[v], __fmul_rn(__fmul_rn(wdm[j][rv][1], da), float(sumi)));
+        for (int v = 0; v < 4; ++v) {
+          const int rv = 16 * wave + 4 * kg + v;
+          int sumi = 0;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) sumi += abs_[t][k] * wmn[rv][k];
+          acc[j][v] = __fsub_rn(acc[j][v], __fmul_rn(__fmul_rn(wdm[rv][1], ad[t]), float(sumi)));
+        }
       }
     }
-  };
-  for (int64_t sb = 0; sb < W.nb; sb += SBS) {
-    const bool two = sb + 1 < W.nb;
-    Raw r0, r1;
-    load_raw(sb, r0);
-    if (two) load_raw(sb + 1, r1);
-    expand(r0, 0);
-    if (two) expand(r1, 1);
-    __syncthreads();
-    compute(sb, 0);  // block order: sb, then sb + 1
-    if (two) compute(sb + 1, 1);
     __syncthreads();
   }
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    float o = acc[v];
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int w = 0; w < 8; ++w) o = __fadd_rn(o, sums[w][v]);
-    const int64_t r = row0 + 4 * g + v;
-    if (r < W.rows && t < n) y[t * W.rows + r] = o;
-  }
+    for (int v = 0; v < 4; ++v) {
+      float o = acc[j][v];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) o = __fadd_rn(o, sums[w][j][v]);
+      const int64_t r = row0 + 16 * wave + 4 * kg + v, t = t0 + 16 * j + ml;
+      if (r < W.rows && t < n) y[t * W.rows + r] = o;
+    }
 }
 
 // ---- dequantization (quant.cpp:157-242), one thread per block of one output row ----
@@ -1237,9 +1320,9 @@ int nbhs_qgemv_multi(int type, int n_w, const void* const* w, const int64_t* row
 int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* rows, float* const* y, int64_t in,
                      const void* acts, int64_t n, nbhs_stream stream) {
   if (!is_quant(type) || n_w <= 0 || n_w > kMaxQWeights || !w || !rows || !y || !acts ||
-      in <= 0 || in % block_elems(type) || n <= 0 || (n + 63) / 64 > 65535)
+      in <= 0 || in % block_elems(type) || n <= 0 || (n + 31) / 32 > 65535)
     return NBHS_EINVAL;
-  const int64_t tile_rows = is_k(type) ? kKTileRows : 64;
+  const int64_t tile_rows = 64;  // weight rows per workgroup, every type
   QGemmBatch B{};
   int64_t tiles = 0;
   for (int i = 0; i < n_w; ++i) {
@@ -1264,9 +1347,9 @@ int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* row
   const bool half = int64_t(tiles) * ((n + 63) / 64) < kLegacyMinWgs || n <= 32;
   const dim3 grid2{unsigned(tiles), unsigned((n + 31) / 32), 1};
   switch (type) {
-    case kQ4_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ4_K>, grid, block, s, B, A, n);
-    case kQ5_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ5_K>, grid, block, s, B, A, n);
-    case kQ6_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ6_K>, grid, block, s, B, A, n);
+    case kQ4_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ4_K>, grid2, block, s, B, A, n);
+    case kQ5_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ5_K>, grid2, block, s, B, A, n);
+    case kQ6_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ6_K>, grid2, block, s, B, A, n);
     case kQ4_0: return launch_legacy<kQ4_0>(half, grid, grid2, s, B, A, n);
     case kQ5_0: return launch_legacy<kQ5_0>(half, grid, grid2, s, B, A, n);
     case kQ5_1: return launch_legacy<kQ5_1>(half, grid, grid2, s, B, A, n);
