@@ -618,8 +618,9 @@ __global__ __launch_bounds__(64) void qgemv_kernel(QBatch B, QA A, const float* 
 // rows, 16 activation rows, block) is one MFMA from zero: the block's exact integer dots (Q4_0 / Q5_0 as
 // sum q_w q_a, the offset term -8 or -16 times the activation block's quant sum applied after, exactly). Every output
 // then adds its block's float term - the reference's expression, in block order - so the outputs are bit-exact with
-// the v_dot4 path and with quant.cpp. Waves: 2 x 2 over 64 x 64 (TJ = 4) or 4 x 1 over 64 x 32 (TJ = 2), each lane
-// holding the MFMA result layout's 4 weight rows of one activation row per 16 x 16 pair. Chunks of 8 blocks of
+// the v_dot4 path and with quant.cpp. Waves: 2 x 2 over 64 x 64 (TJ = 4), 4 x 1 over 64 x 32 (TJ = 2) or, with
+// WRT = 32 weight rows, 2 x 2 over 32 x 32; each lane holds the MFMA result layout's 4 weight rows of one
+// activation row per 16 x 16 pair. Chunks of 8 blocks of
 // both operands are staged in LDS (one 16-byte pad per row: conflict-free fragment reads); the next chunk's share of
 // each thread is loaded into registers while the current one is computed, the weight scales are widened to float
 // and an activation block's quant sum taken once at staging. One launch covers the weights of one type that share
@@ -638,7 +639,7 @@ struct QGemmBatch {  // weights of one type sharing one input; tile0[i]: first r
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));  // an integer MFMA result
 
-template <int T, int TJ>
+template <int T, int TJ, int WRT = 64>
 __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, int64_t n) {
   int wi = 0;
   for (int i = 1; i < B.n_w; ++i)
@@ -650,30 +651,32 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
   constexpr int WROW = kGemmCB * QW4 + 1;             // u32x4_t per staged weight row (one of padding: spreads banks)
   constexpr int AROW = 2 * kGemmCB + 1;               // u32x4_t per staged activation row (likewise)
   constexpr int AR = 16 * TJ;                         // activation rows per workgroup
-  constexpr int NWQ = 64 * kGemmCB * QW4 / 256;       // weight u32x4_t a thread stages per chunk
-  constexpr int NWM = 64 * kGemmCB / 256;             // weight block headers a thread stages per chunk
+  constexpr int NWQ = WRT * kGemmCB * QW4 / 256;       // weight u32x4_t a thread stages per chunk
+  constexpr int NWM = WRT * kGemmCB / 256;             // weight block headers a thread stages per chunk
   constexpr int NA = (AR * kGemmCB + 255) / 256;      // activation blocks a thread stages per chunk (at most)
-  static_assert(NWQ * 256 == 64 * kGemmCB * QW4 && NWM * 256 == 64 * kGemmCB, "chunks split evenly");
+  static_assert(NWQ * 256 == WRT * kGemmCB * QW4 && NWM * 256 == WRT * kGemmCB, "chunks split evenly");
   // Per wave: WM 16-row weight groups x 2 16-row activation groups, one v_mfma_i32_16x16x32_i8 per pair and block
   // (a legacy block is exactly the MFMA's 32-deep contraction). TJ = 4: waves 2 x 2 over 64 x 64; TJ = 2: waves
   // 4 x 1 over 64 x 32.
-  constexpr int WM = TJ == 4 ? 2 : 1;
-  __shared__ u32x4_t wq[64 * WROW];
-  __shared__ float wdf[kGemmCB][64], wmf[kGemmCB][64];
-  __shared__ uint32_t wh[64][kGemmCB];
+  constexpr int WM = TJ == 4 && WRT == 64 ? 2 : 1;
+  constexpr int WN = WRT == 64 ? 2 : 1;  // 16-row activation groups per wave (32 x 32 tiles: waves 2 x 2 of 16 x 16)
+  __shared__ u32x4_t wq[WRT * WROW];
+  __shared__ float wdf[kGemmCB][WRT], wmf[kGemmCB][WRT];
+  __shared__ uint32_t wh[WRT][kGemmCB];
   __shared__ u32x4_t aq[AR * AROW];
   __shared__ float ad[kGemmCB][AR], as_[kGemmCB][AR];
   __shared__ int asum[kGemmCB][AR];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ml = lane & 15, kg = lane >> 4;  // operand row / column of the lane and its 8-deep k group
-  const int wr0 = TJ == 4 ? 32 * (wave & 1) : 16 * wave, ac0 = TJ == 4 ? 32 * (wave >> 1) : 0;
-  const int64_t row0 = int64_t(int(blockIdx.x) - B.tile0[wi]) * 64, t0 = int64_t(blockIdx.y) * AR;
+  const int wr0 = WRT == 32 ? 16 * (wave & 1) : TJ == 4 ? 32 * (wave & 1) : 16 * wave;
+  const int ac0 = WRT == 32 ? 16 * (wave >> 1) : TJ == 4 ? 32 * (wave >> 1) : 0;
+  const int64_t row0 = int64_t(int(blockIdx.x) - B.tile0[wi]) * WRT, t0 = int64_t(blockIdx.y) * AR;
   // acc[i][j][v]: weight row wr0 + 16 i + 4 kg + v, activation row ac0 + 16 j + ml (the MFMA's result layout)
-  float acc[WM][2][4];
+  float acc[WM][WN][4];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < WN; ++j)
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
   // A thread's share of one chunk, in registers: rows and activation rows past the ends, and blocks past the
@@ -783,9 +786,9 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
     // the next chunk's share, in flight while this one is computed (the last chunk loads itself again, unused)
     load_share(c0 + kGemmCB < W.nb ? c0 + kGemmCB : c0, cur);
     for (int b = 0; b < nc; ++b) {
-      long bop[2];
+      long bop[WN];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < WN; ++j) {
         const uint32_t* ar = reinterpret_cast<const uint32_t*>(&aq[(ac0 + 16 * j + ml) * AROW + 2 * b]);
         bop[j] = long((uint64_t(ar[2 * kg + 1]) << 32) | uint64_t(ar[2 * kg]));
       }
@@ -801,7 +804,7 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
           mw[0] = m4.x, mw[1] = m4.y, mw[2] = m4.z, mw[3] = m4.w;
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < WN; ++j) {
           const i32x4_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop[j], i32x4_t{0, 0, 0, 0}, 0, 0, 0);
           const int t = ac0 + 16 * j + ml;
           const float da = ad[b][t];
@@ -825,7 +828,7 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < WN; ++j)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int64_t r = row0 + wr0 + 16 * i + 4 * kg + v, t = t0 + ac0 + 16 * j + ml;
@@ -833,13 +836,21 @@ __global__ __launch_bounds__(256) void qgemm_legacy_kernel(QGemmBatch B, QA A, i
       }
 }
 
-// Workgroups below which a legacy-type launch takes 32-row activation tiles (two per CU on 256 CUs).
+// The legacy kernel's tile for a launch: 64 x 64 while 64 x 64 tiles give at least kLegacyMinWgs workgroups
+// (two per CU); else 64 x 32 while those do; else 32 x 32 (more, smaller workgroups: at the QKV shape 16-80 rows
+// run 10-20 % faster than with 64 x 32, and 512 rows 3-5 % slower).
 constexpr int64_t kLegacyMinWgs = 512;
+enum LegacyTile { kTile64x64, kTile64x32, kTile32x32 };
 template <int T>
-hipError_t launch_legacy(bool half, dim3 grid, dim3 grid2, hipStream_t s, const QGemmBatch& B, const QA& A,
-                         int64_t n) {
-  if (half) return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<T, 2>, grid2, dim3(256), s, B, A, n);
-  return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<T, 4>, grid, dim3(256), s, B, A, n);
+hipError_t launch_legacy(LegacyTile tile, unsigned tiles, int64_t n, hipStream_t s, const QGemmBatch& B,
+                         const QA& A) {
+  if (tile == kTile64x64)
+    return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<T, 4>, dim3(tiles, unsigned((n + 63) / 64)),
+                               dim3(256), s, B, A, n);
+  const dim3 grid{tiles, unsigned((n + 31) / 32)};
+  if (tile == kTile64x32)
+    return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<T, 2>, grid, dim3(256), s, B, A, n);
+  return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_legacy_kernel<T, 2, 32>, grid, dim3(256), s, B, A, n);
 }
 
 // qgemm_k_kernel: the tiled matmul for the K types on the int8 matrix cores (v_mfma_i32_16x16x32_i8).
@@ -1322,38 +1333,50 @@ int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* row
   if (!is_quant(type) || n_w <= 0 || n_w > kMaxQWeights || !w || !rows || !y || !acts ||
       in <= 0 || in % block_elems(type) || n <= 0 || (n + 31) / 32 > 65535)
     return NBHS_EINVAL;
-  const int64_t tile_rows = 64;  // weight rows per workgroup, every type
+  // weight-row tiles of every weight at 64 rows (each weight's tiles start at its tile0 in grid x) and, for the
+  // legacy types' smallest launches, at 32
   QGemmBatch B{};
-  int64_t tiles = 0;
+  int64_t tiles64 = 0, tiles32 = 0;
   for (int i = 0; i < n_w; ++i) {
     if (!w[i] || !y[i] || rows[i] <= 0) return NBHS_EINVAL;
     B.w[i] = weight_of(type, w[i], rows[i], in);
     B.y[i] = y[i];
-    B.tile0[i] = int(tiles);
-    tiles += (rows[i] + tile_rows - 1) / tile_rows;
-    if (tiles >= (int64_t(1) << 31)) return NBHS_EINVAL;
+    tiles64 += (rows[i] + 63) / 64;
+    tiles32 += (rows[i] + 31) / 32;
+    if (tiles32 >= (int64_t(1) << 31)) return NBHS_EINVAL;
   }
   B.n_w = n_w;
+  LegacyTile tile = kTile64x64;
+  if (!is_k(type)) {
+    if (tiles64 * ((n + 63) / 64) >= kLegacyMinWgs && n > 32)
+      tile = kTile64x64;
+    else if (tiles64 * ((n + 31) / 32) >= kLegacyMinWgs)
+      tile = kTile64x32;
+    else
+      tile = kTile32x32;
+  }
+  const int64_t tile_rows = tile == kTile32x32 ? 32 : 64;
+  int64_t tiles = 0;
+  for (int i = 0; i < n_w; ++i) {
+    B.tile0[i] = int(tiles);
+    tiles += (rows[i] + tile_rows - 1) / tile_rows;
+  }
   const int act = act_of(type);
   const ActLayout l = act_layout(act, n, B.w[0].nb);
   const uint8_t* base = static_cast<const uint8_t*>(acts);
   const QA A{reinterpret_cast<const int8_t*>(base + l.qs_off), reinterpret_cast<const float*>(base + l.d_off),
              act == kActQ8_1 ? reinterpret_cast<const float*>(base + l.s_off) : nullptr,
              act == kActQ8_K ? reinterpret_cast<const int16_t*>(base + l.bsums_off) : nullptr, B.w[0].nb};
-  const dim3 grid{unsigned(tiles), unsigned((n + 63) / 64), 1}, block{256, 1, 1};
+  const dim3 grid32{unsigned(tiles), unsigned((n + 31) / 32), 1}, block{256, 1, 1};
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // legacy types: 32-row activation tiles when 64-row ones would give fewer than kLegacyMinWgs workgroups (and for
-  // at most 32 rows, where a 64-row tile would compute half of it for nothing)
-  const bool half = int64_t(tiles) * ((n + 63) / 64) < kLegacyMinWgs || n <= 32;
-  const dim3 grid2{unsigned(tiles), unsigned((n + 31) / 32), 1};
   switch (type) {
-    case kQ4_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ4_K>, grid2, block, s, B, A, n);
-    case kQ5_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ5_K>, grid2, block, s, B, A, n);
-    case kQ6_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ6_K>, grid2, block, s, B, A, n);
-    case kQ4_0: return launch_legacy<kQ4_0>(half, grid, grid2, s, B, A, n);
-    case kQ5_0: return launch_legacy<kQ5_0>(half, grid, grid2, s, B, A, n);
-    case kQ5_1: return launch_legacy<kQ5_1>(half, grid, grid2, s, B, A, n);
-    case kQ8_0: return launch_legacy<kQ8_0>(half, grid, grid2, s, B, A, n);
+    case kQ4_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ4_K>, grid32, block, s, B, A, n);
+    case kQ5_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ5_K>, grid32, block, s, B, A, n);
+    case kQ6_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ6_K>, grid32, block, s, B, A, n);
+    case kQ4_0: return launch_legacy<kQ4_0>(tile, unsigned(tiles), n, s, B, A);
+    case kQ5_0: return launch_legacy<kQ5_0>(tile, unsigned(tiles), n, s, B, A);
+    case kQ5_1: return launch_legacy<kQ5_1>(tile, unsigned(tiles), n, s, B, A);
+    case kQ8_0: return launch_legacy<kQ8_0>(tile, unsigned(tiles), n, s, B, A);
     default: return NBHS_EINVAL;
   }
 }

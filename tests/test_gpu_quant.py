@@ -135,28 +135,28 @@ def test_quant_tiled_many_weights_one_type(backend, t):
 
 
 @pytest.mark.parametrize("t", LEGACY, ids=[U.NAMES[t] for t in LEGACY])
-def test_quant_tiled_legacy_both_tile_heights(backend, t):
-    """The legacy tiled kernel in both activation-tile heights: a launch of at least 512 workgroups keeps 64-row
-    activation tiles (4100 rows = 65 row tiles x 9 activation tiles at n = 520, rows and activation rows ending
-    inside a tile), a smaller one takes 32-row tiles (the same weight's first 70 rows at n = 100). Three blocks per
-    row: a partial chunk. Both bit-exact."""
+def test_quant_tiled_legacy_every_tile_shape(backend, t):
+    """The legacy tiled kernel in each of its tile shapes, chosen by the launch's size: 64 x 64 tiles when those
+    give at least 512 workgroups (4100 rows = 65 row tiles x 9 activation tiles at n = 520), 64 x 32 when those do
+    (n = 250: 65 x 8), 32 x 32 below (the same weight at n = 100, and a 70-row weight at n = 100). Rows and
+    activation rows end inside a tile; three blocks per row: a partial chunk. Every output bit-exact."""
     in_ = 96
     w_big = U.random_qmat(t, 4100, in_, seed=700 + t)
     w_small = U.random_qmat(t, 70, in_, seed=800 + t)
     rng = np.random.default_rng(31 + t)
     x_big = (rng.standard_normal((520, in_)) * 2).astype(np.float32)
-    x_small = x_big[:100].copy()
+    cases = [(w_big, 520), (w_big, 250), (w_big, 100), (w_small, 100)]
     with Buffers(backend) as B:
-        dxb, dyb = B.upload(x_big), B.alloc(520 * 4100)
-        dxs, dys = B.upload(x_small), B.alloc(100 * 70)
-        backend.matmul(w_big, dxb, dyb, 520)
-        backend.matmul(w_small, dxs, dys, 100)
-        got_big = backend.download(dyb, (520, 4100))
-        got_small = backend.download(dys, (100, 70))
-    for g, w, x in ((got_big, w_big, x_big), (got_small, w_small, x_small)):
-        ref = oracle.matmul_q(t, w.raw, in_, w.rows, x)
+        dx = B.upload(x_big)
+        outs = []
+        for w, n in cases:
+            dy = B.alloc(n * w.rows)
+            backend.matmul(w, dx, dy, n)
+            outs.append(backend.download(dy, (n, w.rows)))
+    for (w, n), g in zip(cases, outs):
+        ref = oracle.matmul_q(t, w.raw, in_, w.rows, x_big[:n])
         diff = int(np.sum(bits(g) != bits(ref)))
-        assert diff == 0, (U.NAMES[t], w.rows, diff)
+        assert diff == 0, (U.NAMES[t], w.rows, n, diff)
     backend.release_weights()
 
 
