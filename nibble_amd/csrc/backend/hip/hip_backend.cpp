@@ -14,7 +14,9 @@ namespace nibble::hip {
 namespace {
 
 // Calls with at most this many query rows take the fp32 split-context kernel (decode, short appends).
-constexpr int64_t kQ6KTiledMinRows = 10;  // Q6_K calls of more rows take the tiled GEMM
+// K-type calls of more rows than these take the tiled kernels (the small-call one first): measured faster from
+// there on at the QKV shape than the 16-row gemv launches
+constexpr int64_t kKTiledMinRows = 8, kQ6KTiledMinRows = 4;
 constexpr int64_t kDecodeMaxRows = NBHS_DECODE_MAX_ROWS;
 constexpr size_t kGemmMaxWeights = NBHS_GEMM_MAX_WEIGHTS;
 // Rows per launch of the ordered route (its grid holds one z index per row; a row's result is the same in any launch).
@@ -478,10 +480,11 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
   const bool fuse = n <= 4 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && in % 4 == 0;
   int done_act = -1;
   for (const int t : types) {
-    // more than 16 rows (Q6_K: more than 10): the tiled kernels, measured faster from there on at the QKV shape (Q6_K's
-    // 16-row launches grow ~2.6 us per row, past the tiled kernel's ~35 us from 11 rows); their K-type activations
-    // are in residue-major order
-    const bool tiled = n > (t == nbh_quant::kQ6_K ? kQ6KTiledMinRows : kGemvMaxRows);
+    // the tiled kernels from more than 16 rows on (K types: 8, Q6_K: 4), whose K-type activations are in
+    // residue-major order
+    const int64_t min_rows =
+        t == nbh_quant::kQ6_K ? kQ6KTiledMinRows : nbh_quant::is_k(t) ? kKTiledMinRows : kGemvMaxRows;
+    const bool tiled = n > min_rows;
     const bool rm = tiled && nbh_quant::is_k(t);
     const int act_key = 2 * nbh_quant::act_of(t) + (rm ? 1 : 0);
     if (!fuse && act_key != done_act) {

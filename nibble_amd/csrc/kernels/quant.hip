@@ -1141,6 +1141,239 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void q
     }
 }
 
+// qgemm_k_small_kernel: the K types for calls of few activation rows, where 64-row weight tiles leave most CUs
+// idle and each workgroup would walk every super-block alone. A workgroup takes 16 weight rows x 32 activation
+// rows and its 4 waves split the super-blocks (wave w: w, w + 4, ...): each computes its super-block's float terms
+// - d * aux[l] for the eight lanes and, for Q4_K / Q5_K, the minimum term, with the operands, slices and
+// expressions of qgemm_k_kernel, its operands read straight from global memory - and writes them to LDS; per round
+// of four super-blocks the 256 threads, two outputs each, add them to their running sums in super-block order:
+// the reference's order, so the same bits.
+template <int T>
+__global__ __launch_bounds__(256) void qgemm_k_small_kernel(QGemmBatch B, QA A, int64_t n) {
+  static_assert(T == kQ4_K || T == kQ5_K || T == kQ6_K, "K types");
+  constexpr int NS = k_slices<T>();
+  constexpr int NTM = T == kQ6_K ? 8 : 9;  // float terms per output and super-block
+  __shared__ float terms[4][NTM][16][33];  // [wave][term][weight row][activation row], one column of padding
+  __shared__ float rowd[4][16][2];         // per wave: d, dmin of its super-block's 16 rows
+  __shared__ int rowm[4][16][8], rows6[4][16][8];  // minimums and 6-bit scales (Q4_K / Q5_K)
+  __shared__ uint32_t rowq6[4][16][4];     // Q6_K: the 16 int8 scales
+  __shared__ float actd[4][32];
+  __shared__ int actb[4][32][8];           // sums of the 16-sums per sub-block (Q4_K / Q5_K)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ml = lane & 15, kg = lane >> 4;
+  int wi = 0;
+  for (int i = 1; i < B.n_w; ++i)
+    if (int(blockIdx.x) >= B.tile0[i]) wi = i;
+  const QW W = B.w[wi];
+  float* __restrict__ y = B.y[wi];
+  const int64_t row0 = int64_t(int(blockIdx.x) - B.tile0[wi]) * 16, t0 = int64_t(blockIdx.y) * 32;
+  // owner sums: outputs (weight row tid & 15, activation rows (tid >> 4) and (tid >> 4) + 16)
+  float sums[2][8], acc[2];
+#pragma unroll
+  for (int o = 0; o < 2; ++o) {
+    acc[o] = 0.f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) sums[o][l] = 0.f;
+  }
+  const int64_t ra = min(row0 + ml, W.rows - 1);  // this lane's operand row
+  for (int64_t s0 = 0; s0 < W.nb; s0 += 4) {
+    const int64_t sb = s0 + wave;
+    const bool has = sb < W.nb;
+    const int64_t sbc = has ? sb : W.nb - 1;
+    // this wave's super-block: per-row and per-activation-row values into its LDS slices
+    if (lane < 16) {
+      const int64_t wb = min(row0 + lane, W.rows - 1) * W.nb + sbc;
+      const u32x4_t sc = *reinterpret_cast<const u32x4_t*>(W.s + wb * 16);
+      const uint32_t scw[4] = {sc[0], sc[1], sc[2], sc[3]};
+      auto sbyte = [&](int i) { return int((scw[i >> 2] >> (8 * (i & 3))) & 0xFFu); };
+      rowd[wave][lane][0] = h2f(W.d[wb]);
+      if constexpr (T == kQ6_K) {
+        rowd[wave][lane][1] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rowq6[wave][lane][c] = scw[c];
+      } else {
+        rowd[wave][lane][1] = h2f(W.m[wb]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {  // ggml get_scale_min_k4 (quant.cpp:52-61), compile-time byte indices
+          int sk, mk;
+          if (k < 4) {
+            sk = sbyte(k) & 63;
+            mk = sbyte(k + 4) & 63;
+          } else {
+            sk = (sbyte(k + 4) & 0xF) | ((sbyte(k - 4) >> 6) << 4);
+            mk = (sbyte(k + 4) >> 4) | ((sbyte(k) >> 6) << 4);
+          }
+          rows6[wave][lane][k] = sk;
+          rowm[wave][lane][k] = mk;
+        }
+      }
+    } else if (lane < 48) {
+      const int a = lane - 16;
+      const int64_t ab = min(t0 + a, n - 1) * A.nb + sbc;
+      actd[wave][a] = A.d[ab];
+      if constexpr (T != kQ6_K) {
+        const u32x4_t* bp = reinterpret_cast<const u32x4_t*>(A.bsums + ab * 16);
+        const u32x4_t b0 = bp[0], b1 = bp[1];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {  // 16-sums 2k and 2k + 1: the two int16 halves of word k
+          const uint32_t wk = k < 4 ? b0[k] : b1[k - 4];
+          actb[wave][a][k] = int(int16_t(wk & 0xFFFFu)) + int(int16_t(wk >> 16));
+        }
+      }
+    }
+    // the lane's operand words: its row's quant words of its k group (and their high bits), every residue
+    const int64_t wb = ra * W.nb + sbc;
+    u32x4_t qv[T == kQ6_K ? 4 : 2], hv[2];
+    if constexpr (T == kQ6_K) {
+      const u32x4_t* q = reinterpret_cast<const u32x4_t*>(W.q + wb * 128 + 64 * (kg >> 1));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qv[i] = q[i];
+      const u32x4_t* h = reinterpret_cast<const u32x4_t*>(W.h + wb * 64 + 32 * (kg >> 1));
+      hv[0] = h[0], hv[1] = h[1];
+    } else {
+      const u32x4_t* q = reinterpret_cast<const u32x4_t*>(W.q + wb * 128 + 32 * kg);
+      qv[0] = q[0], qv[1] = q[1];
+      if constexpr (T == kQ5_K) {
+        const u32x4_t* h = reinterpret_cast<const u32x4_t*>(W.h + wb * 32);
+        hv[0] = h[0], hv[1] = h[1];
+      }
+    }
+    uint2 bw[2][8];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t ab = min(t0 + 16 * j + ml, n - 1) * A.nb + sbc;
+      const uint8_t* aq = reinterpret_cast<const uint8_t*>(A.qs) + ab * 256;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) bw[j][w] = *reinterpret_cast<const uint2*>(aq + 32 * w + 8 * kg);
+    }
+    __syncthreads();  // this round's row and activation values are in LDS
+    if (has) {
+      float dv[2][4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) dv[j][v] = __fmul_rn(rowd[wave][4 * kg + v][0], actd[wave][16 * j + ml]);
+      int s_a = 0, s_b = 0;
+      uint32_t s6 = 0;
+      if constexpr (T == kQ6_K)
+        s6 = rowq6[wave][ml][kg];
+      else
+        s_a = rows6[wave][ml][2 * kg], s_b = rows6[wave][ml][2 * kg + 1];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        long aop[NS];
+        if constexpr (T == kQ6_K) {
+          const int sel = kg & 1;
+          const uint32_t hq = hv[w >> 2][w & 3];
+          uint32_t sl[4][2];
+#pragma unroll
+          for (int b = 0; b < 2; ++b) {
+            const int g = 2 * sel + b;
+            const uint32_t lw = qv[(8 * b + w) >> 2][(8 * b + w) & 3];
+            const uint32_t v = ((lw >> (4 * sel)) & 0x0F0F0F0Fu) | (((hq >> (2 * g)) & 0x03030303u) << 4);
+            const u16x2_t u0e = __builtin_bit_cast(u16x2_t, v & 0x00070007u);
+            const u16x2_t u0o = __builtin_bit_cast(u16x2_t, (v >> 8) & 0x00070007u);
+            const u16x2_t four = {4, 4};
+            const u16x2_t u1e = __builtin_bit_cast(u16x2_t, (v >> 3) & 0x00070007u) - four;
+            const u16x2_t u1o = __builtin_bit_cast(u16x2_t, (v >> 11) & 0x00070007u) - four;
+            const int slo = int(int8_t((s6 >> (16 * b)) & 0xFFu)), shi = int(int8_t((s6 >> (16 * b + 8)) & 0xFFu));
+            const u16x2_t s0 = {uint16_t(slo & 15), uint16_t(shi & 15)};
+            const u16x2_t s1 = {uint16_t(slo >> 4), uint16_t(shi >> 4)};
+            sl[0][b] = byte_products(u1e, u1o, s1);
+            sl[1][b] = byte_products(u0e, u0o, s1);
+            sl[2][b] = byte_products(u1e, u1o, s0);
+            sl[3][b] = byte_products(u0e, u0o, s0);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) aop[i] = long((uint64_t(sl[i][1]) << 32) | uint64_t(sl[i][0]));
+        } else {
+          const uint32_t qw = qv[w >> 2][w & 3];
+          uint32_t qa = qw & 0x0F0F0F0Fu, qb = (qw >> 4) & 0x0F0F0F0Fu;  // sub-blocks 2 kg and 2 kg + 1
+          if constexpr (T == kQ5_K) {
+            const uint32_t hb = hv[w >> 2][w & 3];
+            qa |= ((hb >> (2 * kg)) & 0x01010101u) << 4;
+            qb |= ((hb >> (2 * kg + 1)) & 0x01010101u) << 4;
+          }
+          if constexpr (T == kQ4_K) {
+            aop[0] = long((uint64_t(qb * uint32_t(s_b & 7)) << 32) | uint64_t(qa * uint32_t(s_a & 7)));
+            aop[1] = long((uint64_t(qb * uint32_t(s_b >> 3)) << 32) | uint64_t(qa * uint32_t(s_a >> 3)));
+          } else {
+            aop[0] = long((uint64_t(qb * uint32_t(s_b & 3)) << 32) | uint64_t(qa * uint32_t(s_a & 3)));
+            aop[1] = long((uint64_t(qb * uint32_t((s_b >> 2) & 3)) << 32) | uint64_t(qa * uint32_t((s_a >> 2) & 3)));
+            aop[2] = long((uint64_t(qb * uint32_t(s_b >> 4)) << 32) | uint64_t(qa * uint32_t(s_a >> 4)));
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const long bop = long((uint64_t(bw[j][w].y) << 32) | uint64_t(bw[j][w].x));
+          i32x4_t c[NS];
+#pragma unroll
+          for (int sl = 0; sl < NS; ++sl)
+            c[sl] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[sl], bop, i32x4_t{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            int aux;
+            if constexpr (T == kQ6_K)
+              aux = 128 * c[0][v] + 16 * c[1][v] + 8 * c[2][v] + c[3][v];
+            else if constexpr (T == kQ5_K)
+              aux = c[0][v] + 4 * c[1][v] + 16 * c[2][v];
+            else
+              aux = c[0][v] + 8 * c[1][v];
+            terms[wave][w][4 * kg + v][16 * j + ml] = __fmul_rn(dv[j][v], float(aux));
+          }
+        }
+      }
+      if constexpr (T != kQ6_K) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int t = 16 * j + ml;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int rv = 4 * kg + v;
+            int sumi = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) sumi += actb[wave][t][k] * rowm[wave][rv][k];
+            terms[wave][8][rv][t] = __fmul_rn(__fmul_rn(rowd[wave][rv][1], actd[wave][t]), float(sumi));
+          }
+        }
+      }
+    }
+    __syncthreads();  // every wave's terms are in LDS
+    const int orow = tid & 15;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (s0 + s < W.nb) {
+#pragma unroll
+        for (int o = 0; o < 2; ++o) {
+          const int ot = (tid >> 4) + 16 * o;
+#pragma unroll
+          for (int l = 0; l < 8; ++l) sums[o][l] = __fadd_rn(sums[o][l], terms[s][l][orow][ot]);
+          if constexpr (T != kQ6_K) acc[o] = __fsub_rn(acc[o], terms[s][8][orow][ot]);
+        }
+      }
+    }
+    __syncthreads();  // the terms are consumed before the next round overwrites them
+  }
+#pragma unroll
+  for (int o = 0; o < 2; ++o) {
+    float r = acc[o];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) r = __fadd_rn(r, sums[o][l]);
+    const int64_t row = row0 + (tid & 15), t = t0 + (tid >> 4) + 16 * o;
+    if (row < W.rows && t < n) y[t * W.rows + row] = r;
+  }
+}
+
+// The small-call K kernel runs while 64 x 32 tiles would give fewer than this many workgroups (measured at the QKV
+// shape, 48 such row tiles: Q4_K faster up to 64 rows, Q5_K / Q6_K up to 128-160; beyond, the 64 x 32 kernel).
+template <int T>
+constexpr int64_t k_small_max_wgs() { return T == kQ4_K ? 128 : 256; }
+template <int T>
+hipError_t launch_k(bool small, dim3 grid32, hipStream_t s, const QGemmBatch& B, const QA& A, int64_t n) {
+  if (small) return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_small_kernel<T>, grid32, dim3(256), s, B, A, n);
+  return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<T>, grid32, dim3(256), s, B, A, n);
+}
+
 // ---- dequantization (quant.cpp:157-242), one thread per block of one output row ----
 
 template <int T>
@@ -1343,7 +1576,7 @@ int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* row
     B.y[i] = y[i];
     tiles64 += (rows[i] + 63) / 64;
     tiles32 += (rows[i] + 31) / 32;
-    if (tiles32 >= (int64_t(1) << 31)) return NBHS_EINVAL;
+    if ((tiles32 + 1) * 2 >= (int64_t(1) << 31)) return NBHS_EINVAL;  // 16-row tiles fit too
   }
   B.n_w = n_w;
   LegacyTile tile = kTile64x64;
@@ -1355,7 +1588,11 @@ int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* row
     else
       tile = kTile32x32;
   }
-  const int64_t tile_rows = tile == kTile32x32 ? 32 : 64;
+  // K types: the small-call kernel (16-row weight tiles, super-blocks split over the waves) when 64-row tiles
+  // would give fewer than kKSmallMaxWgs workgroups
+  const bool small = is_k(type) && tiles64 * ((n + 31) / 32) < (type == kQ4_K ? k_small_max_wgs<kQ4_K>()
+                                                                                 : k_small_max_wgs<kQ6_K>());
+  const int64_t tile_rows = small ? 16 : tile == kTile32x32 ? 32 : 64;
   int64_t tiles = 0;
   for (int i = 0; i < n_w; ++i) {
     B.tile0[i] = int(tiles);
@@ -1370,9 +1607,9 @@ int nbhs_qgemm_multi(int type, int n_w, const void* const* w, const int64_t* row
   const dim3 grid32{unsigned(tiles), unsigned((n + 31) / 32), 1}, block{256, 1, 1};
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (type) {
-    case kQ4_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ4_K>, grid32, block, s, B, A, n);
-    case kQ5_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ5_K>, grid32, block, s, B, A, n);
-    case kQ6_K: return nbhs_timing::launch(NBHS_K_QGEMM, qgemm_k_kernel<kQ6_K>, grid32, block, s, B, A, n);
+    case kQ4_K: return launch_k<kQ4_K>(small, grid32, s, B, A, n);
+    case kQ5_K: return launch_k<kQ5_K>(small, grid32, s, B, A, n);
+    case kQ6_K: return launch_k<kQ6_K>(small, grid32, s, B, A, n);
     case kQ4_0: return launch_legacy<kQ4_0>(tile, unsigned(tiles), n, s, B, A);
     case kQ5_0: return launch_legacy<kQ5_0>(tile, unsigned(tiles), n, s, B, A);
     case kQ5_1: return launch_legacy<kQ5_1>(tile, unsigned(tiles), n, s, B, A);

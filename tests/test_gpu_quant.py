@@ -21,7 +21,8 @@ TYPES = list(U.NAMES)
 @pytest.mark.parametrize("n", [1, 3, 16, 17, 40, 96])
 def test_quant_matmul_bit_exact(backend, t, n):
     """Activation quantization and the block dots, every activation-row chunking: n <= 16 (one row-chunked
-    launch), 17, 40 and 96 (the tiled kernels; the legacy types' 32-row activation tiles, one or two of them)."""
+    launch; K types above 8 rows, Q6_K above 4, take the small-call tiled kernel), 17, 40 and 96 (the tiled
+    kernels: the legacy types' 32-row activation tiles, the K types' small-call kernel)."""
     be_ = oracle.block_elems(t)
     in_ = 2 * 256 if be_ == 256 else 7 * 32 + 32 * 64  # two super-blocks / 71 legacy blocks (a partial chunk)
     rows = 37  # not a multiple of the 4 rows per wave
@@ -156,6 +157,30 @@ def test_quant_tiled_legacy_every_tile_shape(backend, t):
     for (w, n), g in zip(cases, outs):
         ref = oracle.matmul_q(t, w.raw, in_, w.rows, x_big[:n])
         diff = int(np.sum(bits(g) != bits(ref)))
+        assert diff == 0, (U.NAMES[t], w.rows, n, diff)
+    backend.release_weights()
+
+
+KTYPES = [oracle.Q4_K, oracle.Q5_K, oracle.Q6_K]
+
+
+@pytest.mark.parametrize("t", KTYPES, ids=[U.NAMES[t] for t in KTYPES])
+def test_quant_tiled_k_both_kernels(backend, t):
+    """The K types' two tiled kernels, chosen by the launch's size: a large call (4100 rows = 65 row tiles of 64 x
+    17 activation tiles of 32 at n = 520) takes the 64 x 32 kernel; a small one (40 rows, n = 24) takes the
+    small-call kernel, whose waves split the super-blocks - six of them here, so two rounds, the second one partial.
+    Rows and activation rows end inside a tile. Every output bit-exact."""
+    cases = [(U.random_qmat(t, 4100, 256, seed=900 + t), 256, 520),
+             (U.random_qmat(t, 40, 1536, seed=950 + t), 1536, 24)]
+    rng = np.random.default_rng(77 + t)
+    for w, in_, n in cases:
+        x = (rng.standard_normal((n, in_)) * 2).astype(np.float32)
+        with Buffers(backend) as B:
+            dx, dy = B.upload(x), B.alloc(n * w.rows)
+            backend.matmul(w, dx, dy, n)
+            got = backend.download(dy, (n, w.rows))
+        ref = oracle.matmul_q(t, w.raw, in_, w.rows, x)
+        diff = int(np.sum(bits(got) != bits(ref)))
         assert diff == 0, (U.NAMES[t], w.rows, n, diff)
     backend.release_weights()
 
