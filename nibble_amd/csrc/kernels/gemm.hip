@@ -159,6 +159,12 @@ constexpr int64_t kWideMinTiles = 256;
 // 2048, 38 -> 40 us in 4 ranges of 512, whose partial sums cost more than the halved operand traffic saves, so it is
 // not cut); the partial sums live in a fixed area of the workspace (64 MB), which bounds a split weight's outputs.
 constexpr int kMaxSplit = 4, kSplitMinKTiles = 48;
+// K ranges of a weight's 64 x 64 tiles in calls of few rows, where the tiles are too few to fill the CUs and each
+// walks the whole K: up to kFewMaxSplit ranges of at least kFewMinKTiles 64-deep slices, while the weight's tiles
+// times its ranges stay below kFewMinWgs (measured at the QKV shape, K = 2048, 3072 output rows: 17-64 rows,
+// 27-29 -> 15-19 us per call).
+constexpr int kFewMaxRows = 64, kFewMaxSplit = 8, kFewMinKTiles = 4;
+constexpr int64_t kFewMinWgs = 256;
 constexpr int64_t kSplitPartFloats = int64_t(1) << 24;
 
 template <int BM, int BN, int BK, int STAGES>
@@ -398,20 +404,32 @@ int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const i
   // fetches half the operand bytes per product of a 64 x 64 tile's, and the ranges restore the workgroup count;
   // the partials are summed in range order); otherwise 64 x 64 tiles. The weights of each configuration share a
   // launch; split weights share one while their partials fit the area, then the next group starts.
-  GemmBatch wide{}, small{}, split{};
-  int64_t wide_tiles = 0, small_tiles = 0, split_wgs = 0, split_out = 0, part_used = 0;
+  GemmBatch wide{}, small{}, split{}, fsplit{};
+  int64_t wide_tiles = 0, small_tiles = 0, split_wgs = 0, split_out = 0, fsplit_wgs = 0, fsplit_out = 0,
+          part_used = 0;
   hipError_t e = nbhs_timing::launch(NBHS_K_SPLIT_ACTS, split_acts_kernel, dim3(unsigned(n)), dim3(64), s, x, in,
                                      in_pad, xh, xl, inv, vec);
+  // the weights taking K ranges (128 x 128 tiles, or 64 x 64 ones in calls of few rows), whose partial sums share
+  // the partial-sum area: their launches and sums, then the area is free again
   auto flush_split = [&]() {
-    if (e != hipSuccess || split.n_w == 0) return;
-    e = nbhs_timing::launch(NBHS_K_GEMM, gemm_f16w_kernel<kWideBM, kWideBN, kWideBK, kWideStages>,
-                            dim3(unsigned(split_wgs), wide_rows), dim3(kThreads), s, split, xh, xl, inv, n, in,
-                            in_pad);
-    if (e == hipSuccess)
-      e = nbhs_timing::launch(NBHS_K_GEMM_REDUCE, gemm_split_reduce_kernel, dim3(unsigned((split_out + 255) / 256)),
-                              dim3(256), s, split, inv, n, split_out);
-    split = GemmBatch{};
-    split_wgs = split_out = part_used = 0;
+    if (e == hipSuccess && split.n_w > 0) {
+      e = nbhs_timing::launch(NBHS_K_GEMM, gemm_f16w_kernel<kWideBM, kWideBN, kWideBK, kWideStages>,
+                              dim3(unsigned(split_wgs), wide_rows), dim3(kThreads), s, split, xh, xl, inv, n, in,
+                              in_pad);
+      if (e == hipSuccess)
+        e = nbhs_timing::launch(NBHS_K_GEMM_REDUCE, gemm_split_reduce_kernel,
+                                dim3(unsigned((split_out + 255) / 256)), dim3(256), s, split, inv, n, split_out);
+    }
+    if (e == hipSuccess && fsplit.n_w > 0) {
+      e = nbhs_timing::launch(NBHS_K_GEMM, gemm_f16w_kernel<kSmallBM, kSmallBN, kSmallBK, kSmallStages>,
+                              dim3(unsigned(fsplit_wgs), small_rows), dim3(kThreads), s, fsplit, xh, xl, inv, n, in,
+                              in_pad);
+      if (e == hipSuccess)
+        e = nbhs_timing::launch(NBHS_K_GEMM_REDUCE, gemm_split_reduce_kernel,
+                                dim3(unsigned((fsplit_out + 255) / 256)), dim3(256), s, fsplit, inv, n, fsplit_out);
+    }
+    split = fsplit = GemmBatch{};
+    split_wgs = split_out = fsplit_wgs = fsplit_out = part_used = 0;
   };
   for (int i = 0; i < n_w && e == hipSuccess; ++i) {
     const int64_t wt = (rows[i] + kWideBN - 1) / kWideBN * wide_rows;
@@ -432,10 +450,26 @@ int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const i
       split_out += n * rows[i];
       part_used += cnt;
     } else {
-      small.w[small.n_w++] = GemmWeight{wd, y[i], rows[i], int(small_tiles), 1, nullptr};
-      small_tiles += (rows[i] + kSmallBN - 1) / kSmallBN;
+      const int64_t st = (rows[i] + kSmallBN - 1) / kSmallBN * small_rows;
+      int fsp = 1;
+      if (n <= kFewMaxRows && n * rows[i] * kFewMaxSplit <= kSplitPartFloats) {
+        const int64_t nkt = in_pad / kSmallBK;
+        while (fsp < kFewMaxSplit && st * fsp * 2 <= kFewMinWgs && nkt / (2 * fsp) >= kFewMinKTiles) fsp *= 2;
+      }
+      if (fsp > 1) {
+        const int64_t cnt = n * rows[i] * fsp;
+        if (part_used + cnt > kSplitPartFloats) flush_split();
+        fsplit.w[fsplit.n_w++] = GemmWeight{wd, y[i], rows[i], int(fsplit_wgs), fsp, part + part_used};
+        fsplit_wgs += (rows[i] + kSmallBN - 1) / kSmallBN * fsp;
+        fsplit_out += n * rows[i];
+        part_used += cnt;
+      } else {
+        small.w[small.n_w++] = GemmWeight{wd, y[i], rows[i], int(small_tiles), 1, nullptr};
+        small_tiles += (rows[i] + kSmallBN - 1) / kSmallBN;
+      }
     }
-    if (wide_tiles > INT32_MAX || small_tiles > INT32_MAX || split_wgs > INT32_MAX) return NBHS_EINVAL;
+    if (wide_tiles > INT32_MAX || small_tiles > INT32_MAX || split_wgs > INT32_MAX || fsplit_wgs > INT32_MAX)
+      return NBHS_EINVAL;
   }
   flush_split();
   if (e == hipSuccess && wide.n_w > 0)

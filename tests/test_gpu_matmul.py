@@ -333,3 +333,20 @@ def test_f16_gemm_split_k_groups(backend):
         assert_within_bound(g, w, x, f"weight {i}")
         assert np.array_equal(bits(g), bits(sep[i])), f"weight {i}: matmul_multi differs from a separate call"
     backend.release_weights()
+
+
+@pytest.mark.parametrize("n", [17, 40, 64])
+def test_f16_gemm_few_rows_k_ranges(backend, n):
+    """Calls of few activation rows (at most 64) give few 64 x 64 tiles, so each weight takes K ranges of 64 x 64
+    tiles (up to 8, partials summed in range order): 300 and 40 rows at in = 2048 (8 ranges of 4 slices), and a
+    100-row weight at in = 1000 (K padded to 1024: ranges of 4 slices, the last one partial), in one call. Within the
+    summation bound and against the restated reference, and matmul_multi equals separate calls bit for bit."""
+    rng = np.random.default_rng(37 + n)
+    for in_, rows in ((2048, (300, 40)), (1000, (100,))):
+        ws = [rand(rng, (r, in_), np.float16, 0.3) for r in rows]
+        x = rand(rng, (n, in_))
+        got, sep = multi_vs_separate(backend, ws, x, n)
+        for i, (g, w) in enumerate(zip(got, ws)):
+            assert_matmul_close(g, w, x, f"in {in_}, weight {i} ({w.shape[0]} rows), n {n}")
+            assert np.array_equal(bits(g), bits(sep[i])), f"weight {i}: matmul_multi differs from a separate call"
+    backend.release_weights()
