@@ -29,6 +29,8 @@ constexpr int64_t kFp32PrefixRows = 128;
 // matmul calls with at most this many rows take the weight-streaming gemv kernel; longer ones are GEMMs.
 constexpr int64_t kGemvMaxRows = NBHS_GEMV_MAX_ROWS;
 constexpr size_t kGemvMaxWeights = NBHS_GEMV_MAX_WEIGHTS;
+// F16-weight calls of more rows than this take the fp16 MFMA GEMM where it applies, the rest stay on the gemv.
+constexpr int64_t kF16GemmMinRows = 11;
 
 std::string str(int64_t v) { return std::to_string(v); }
 
@@ -545,9 +547,23 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
   dw.resize(nf);
   if (dw.empty()) return;
   const std::vector<float*>& yv = ys_float_;
+  // F16 weights the fp16 MFMA GEMM below can take (16-byte aligned rows of a multiple of 8 elements)
+  const bool gemm_ok = !batch_invariant_ && in % 8 == 0;
+  auto f16_gemm = [&](const DeviceWeight& w) {
+    return gemm_ok && w.type == DType::F16 && reinterpret_cast<uintptr_t>(w.dev) % 16 == 0;
+  };
   if (n <= kGemvMaxRows) {
+    // Above kF16GemmMinRows rows those F16 weights take the GEMM (its K ranges fill the CUs sooner than the
+    // gemv's per-row work grows); the others stay here.
+    size_t ng = 0;
+    if (n > kF16GemmMinRows)
+      for (size_t i = 0; i < dw.size(); ++i)
+        if (f16_gemm(dw[i])) {
+          std::swap(dw[ng], dw[i]);
+          std::swap(ys_float_[ng++], ys_float_[i]);
+        }
     // One launch per (up to) eight weights: every weight row is read once for all n rows.
-    for (size_t b = 0; b < dw.size(); b += kGemvMaxWeights) {
+    for (size_t b = ng; b < dw.size(); b += kGemvMaxWeights) {
       const size_t cnt = std::min(dw.size() - b, kGemvMaxWeights);
       int f16[kGemvMaxWeights];
       const void* wp[kGemvMaxWeights];
@@ -561,15 +577,17 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
       }
       check(nbhs_gemv_multi(int(cnt), f16, wp, yp, rows, in, x, n, stream_), "matmul (gemv)");
     }
-    return;
+    if (ng == 0) return;
+    dw.resize(ng);
+    ys_float_.resize(ng);
   }
   // F16 weights on the fp16 MFMA GEMM (split activations, fp32-grade results, no fp32 copy of the weight): up to
   // eight per launch, sharing one split of x. Its scratch is the activation buffer (stream order keeps the
   // quantized launches above, which read that buffer, ahead of the split that overwrites it).
-  if (!batch_invariant_ && in % 8 == 0) {
+  if (gemm_ok) {
     size_t ng = 0;
     for (size_t i = 0; i < dw.size(); ++i)
-      if (dw[i].type == DType::F16 && reinterpret_cast<uintptr_t>(dw[i].dev) % 16 == 0) ++ng;
+      if (f16_gemm(dw[i])) ++ng;
     if (ng > 0) {
       const int64_t ws = nbhs_gemm_f16w_workspace(n, in);
       if (ws < 0) throw Error("matmul: invalid GEMM shape n=" + str(n) + " in=" + str(in));
@@ -585,7 +603,7 @@ void HipBackend::matmul_multi(std::span<const Tensor* const> ws, const float* x,
         cnt = 0;
       };
       for (size_t i = 0; i < dw.size(); ++i) {
-        if (dw[i].type == DType::F16 && reinterpret_cast<uintptr_t>(dw[i].dev) % 16 == 0) {
+        if (f16_gemm(dw[i])) {
           wp[cnt] = dw[i].dev;
           yp[cnt] = yv[i];
           rows[cnt] = dw[i].rows;
