@@ -161,9 +161,10 @@ constexpr int64_t kWideMinTiles = 256;
 constexpr int kMaxSplit = 4, kSplitMinKTiles = 48;
 // K ranges of a weight's 64 x 64 tiles in calls of few rows, where the tiles are too few to fill the CUs and each
 // walks the whole K: up to kFewMaxSplit ranges of at least kFewMinKTiles 64-deep slices, while the weight's tiles
-// times its ranges stay below kFewMinWgs (measured at the QKV shape, K = 2048, 3072 output rows: 17-64 rows,
-// 27-29 -> 15-19 us per call).
-constexpr int kFewMaxRows = 64, kFewMaxSplit = 8, kFewMinKTiles = 4;
+// times its ranges stay within kFewMinWgs (measured at the QKV shape, K = 2048, 3072 output rows: 12-64 rows,
+// 27-29 -> 15-19 us per call; 65-128 rows, 29-30 -> 19-22 us; FFN gate + up and down shapes unchanged. A target of
+// 512 workgroups, up to 256 rows, gained 2-4 us at 192-256 QKV rows but cost gate + up 4-10 us at 32-128 rows).
+constexpr int kFewMaxRows = 128, kFewMaxSplit = 8, kFewMinKTiles = 4;
 constexpr int64_t kFewMinWgs = 256;
 constexpr int64_t kSplitPartFloats = int64_t(1) << 24;
 

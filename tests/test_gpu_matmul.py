@@ -335,7 +335,7 @@ def test_f16_gemm_split_k_groups(backend):
     backend.release_weights()
 
 
-@pytest.mark.parametrize("n", [9, 12, 16, 17, 40, 64])
+@pytest.mark.parametrize("n", [9, 12, 16, 17, 40, 64, 96, 128])
 def test_f16_gemm_few_rows_k_ranges(backend, n):
     """Calls of few activation rows (at most 64) give few 64 x 64 tiles, so each weight takes K ranges of 64 x 64
     tiles (up to 8, partials summed in range order): 300 and 40 rows at in = 2048 (8 ranges of 4 slices), and a
