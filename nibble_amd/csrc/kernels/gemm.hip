@@ -164,6 +164,8 @@ constexpr int kMaxSplit = 4, kSplitMinKTiles = 48;
 // times its ranges stay within kFewMinWgs (measured at the QKV shape, K = 2048, 3072 output rows: 12-64 rows,
 // 27-29 -> 15-19 us per call; 65-128 rows, 29-30 -> 19-22 us; FFN gate + up and down shapes unchanged. A target of
 // 512 workgroups, up to 256 rows, gained 2-4 us at 192-256 QKV rows but cost gate + up 4-10 us at 32-128 rows).
+// Such calls take these ranges rather than the wide tiles' ones above, whose few 128 x 128 tiles would leave most CUs
+// idle (FFN down, K = 8192, 2048 output rows: 17-64 rows 61-64 -> 28-30 us, 96-128 rows 64-65 -> 40-41 us).
 constexpr int kFewMaxRows = 128, kFewMaxSplit = 8, kFewMinKTiles = 4;
 constexpr int64_t kFewMinWgs = 256;
 constexpr int64_t kSplitPartFloats = int64_t(1) << 24;
@@ -435,7 +437,7 @@ int nbhs_gemm_f16w_multi(int n_w, const void* const* w, float* const* y, const i
   for (int i = 0; i < n_w && e == hipSuccess; ++i) {
     const int64_t wt = (rows[i] + kWideBN - 1) / kWideBN * wide_rows;
     int sp = 1;
-    if (wt < kWideMinTiles && n * rows[i] * kMaxSplit <= kSplitPartFloats) {
+    if (wt < kWideMinTiles && n > kFewMaxRows && n * rows[i] * kMaxSplit <= kSplitPartFloats) {
       const int64_t nkt = in_pad / kWideBK;
       while (sp < kMaxSplit && wt * sp < kWideMinTiles && nkt / (2 * sp) >= kSplitMinKTiles) sp *= 2;
     }

@@ -56,8 +56,8 @@ def gpu_matmul(be, w, x, n):
 @pytest.mark.parametrize("in_out", [(256, 96), (200, 40), (100, 33)], ids=["256x96", "200x40", "100x33-unaligned"])
 @pytest.mark.parametrize("n", [1, 2, 7, 16, 17, 64, 65, 200])
 def test_matmul_matches_reference(backend, dtype, in_out, n):
-    """Both routes (gemv for n <= 16, GEMM above) and both weight types, aligned (in % 8 == 0) and not; partial
-    row, output and K tiles of the F16 GEMM (64 x 64 tiles, 64-deep slices: in 200 ends mid-slice, in 100 is not a
+    """Both routes (gemv for n <= 16, n <= 11 for F16 weights; GEMM above) and both weight types, aligned
+    (in % 8 == 0) and not; partial row, output and K tiles of the F16 GEMM (64 x 64 tiles, 64-deep slices: in 200 ends mid-slice, in 100 is not a
     multiple of 8 and takes the fp32 route)."""
     in_, out_ = in_out
     rng = np.random.default_rng(1000 * n + in_ + out_)
@@ -118,7 +118,7 @@ def test_qkv_projection_into_cache_rows(backend, shape, n):
 @pytest.mark.parametrize("n", [3, 16, 40, 512])
 def test_device_resident_weights_match_host_weights(backend, n):
     """Weights inside a buffer from alloc() are used in place. F32 ones run the same kernels on the same bytes as
-    host weights, so the same bits; so do F16 ones, the gemv for n <= 16 and the F16 GEMM above (which reads the
+    host weights, so the same bits; so do F16 ones, the gemv for n <= 11 and the F16 GEMM above (which reads the
     weight as fp16, so an in-place weight needs no widened copy)."""
     rng = np.random.default_rng(77 + n)
     in_, out_ = 256, 72
@@ -342,7 +342,7 @@ def test_f16_gemm_few_rows_k_ranges(backend, n):
     100-row weight at in = 1000 (K padded to 1024: ranges of 4 slices, the last one partial), in one call. Within the
     summation bound and against the restated reference, and matmul_multi equals separate calls bit for bit."""
     rng = np.random.default_rng(37 + n)
-    for in_, rows in ((2048, (300, 40)), (1000, (100,))):
+    for in_, rows in ((2048, (300, 40)), (1000, (100,)), (8200, (130,))):
         ws = [rand(rng, (r, in_), np.float16, 0.3) for r in rows]
         x = rand(rng, (n, in_))
         got, sep = multi_vs_separate(backend, ws, x, n)
